@@ -1,0 +1,345 @@
+"""Benchmark of the dynamic block-sparse attention path on one MI355X.
+
+Default workload = BASELINE config 4 ("2K fwd+bwd, one GPU's head share"):
+B=1, H=5, D=128, bf16, latent grid 21x90x160 (302,400 video tokens, padded
+to 24x96x160) plus 2,000 audio tokens; hybrid top-48 + cumulative 0.9.
+A step = A2V token norms + SelfAttention._run_bsa_dynamic forward (pad,
+zone stats, shapes, gather + pooling, scores, selection, attention, scatter,
+unpad) + its backward, on synthetic inputs already resident in HBM.
+
+Prints ONE JSON line.  value = kept-block algorithmic FLOP/s of the step
+((4 + 10) * 64 * 64 * D * sum_lens per step, FA convention).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "sparse-attn fwd+bwd ms & effective TFLOP/s at 2K shape; MFMA util %"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (B, H, D, grid_real, audio_tokens, C, topk, cdf, sparsity_only, struct_scale)
+    "c4": (1, 5, 128, (21, 90, 160), 2000, 5120, 48, 0.9, None, 2.0),
+    "c3": (1, 24, 128, (21, 68, 120), 2000, 3072, 32, 0.9, None, 2.0),
+    "c2": (1, 24, 128, (21, 45, 80), 2000, 3072, None, None, 0.75, 2.0),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ synthetic inputs (GPU, seeded)
+def lowrank_zone_field(gen, H, grid_pad, D, rank, scale, device):
+    """[H, T, Hg, Wg, D] per-zone rank-`rank` structure with smooth t/h/w
+    modulation and Dirichlet axis weights (zone variances differ)."""
+    import torch
+    T, Hg, Wg = grid_pad
+    ZT, ZH, ZW = T // 8, Hg // 8, Wg // 8
+    Nz = ZT * ZH * ZW
+    w = -torch.log(torch.rand(Nz, 3, generator=gen, device=device).clamp_min(1e-12))
+    w = w / w.sum(1, keepdim=True)
+    f = 0.5 + 2.5 * torch.rand(Nz, rank, 3, generator=gen, device=device)
+    ph = 2 * math.pi * torch.rand(Nz, rank, 3, generator=gen, device=device)
+    x = torch.linspace(0, 1, 8, device=device)
+    ct = torch.sin(f[..., 0, None] * math.pi * x + ph[..., 0, None])  # [Nz, r, 8]
+    ch = torch.sin(f[..., 1, None] * math.pi * x + ph[..., 1, None])
+    cw = torch.sin(f[..., 2, None] * math.pi * x + ph[..., 2, None])
+    coef = (w[:, None, 0, None, None, None] * ct[..., :, None, None]
+            + w[:, None, 1, None, None, None] * ch[..., None, :, None]
+            + w[:, None, 2, None, None, None] * cw[..., None, None, :]).reshape(Nz, rank, 512)
+    amp = scale * torch.rand(Nz, 1, 1, generator=gen, device=device)
+    out = torch.empty((H, T, Hg, Wg, D), device=device, dtype=torch.float32)
+    for h in range(H):
+        basis = torch.randn(Nz, rank, D, generator=gen, device=device)
+        s = amp * torch.bmm(coef.transpose(1, 2).contiguous(), basis)  # [Nz, 512, D]
+        s = s.view(ZT, ZH, ZW, 8, 8, 8, D).permute(0, 3, 1, 4, 2, 5, 6).reshape(T, Hg, Wg, D)
+        out[h] = s
+    return out
+
+
+def make_inputs(cfg_name, seed=0, device="cuda"):
+    import torch
+    B, H, D, grid, audio, C, topk, cdf, sp_only, scale = CONFIGS[cfg_name]
+    T, Hg, Wg = grid
+    gp = tuple((x + 7) // 8 * 8 for x in grid)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    qkv = []
+    for _ in range(3):
+        field = lowrank_zone_field(gen, H, gp, D, 8, scale, device)[:, :T, :Hg, :Wg]
+        x = torch.randn((B, H, T, Hg, Wg, D), generator=gen, device=device) + field[None]
+        x = x / x.std()  # unit marginal variance; the structure keeps its scale relative to the noise
+        qkv.append(x.reshape(B, H, T * Hg * Wg, D).to(torch.bfloat16).contiguous())
+        del field, x
+    # A2V bridge residual [B, S, C]: audio coupling concentrated in ~10% of zones
+    S = T * Hg * Wg
+    zone_amp = torch.zeros(gp[0] // 8, gp[1] // 8, gp[2] // 8, device=device)
+    zone_amp.view(-1)[torch.randperm(zone_amp.numel(), generator=gen, device=device)[: max(1, zone_amp.numel() // 10)]] = 2.0
+    amp = zone_amp.repeat_interleave(8, 0).repeat_interleave(8, 1).repeat_interleave(8, 2)[:T, :Hg, :Wg].reshape(S, 1)
+    res = (torch.randn((B, S, C), generator=gen, device=device, dtype=torch.bfloat16) * (1.0 + amp).to(torch.bfloat16))
+    do = torch.randn((B, H, S, D), generator=gen, device=device).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    return dict(q=qkv[0], k=qkv[1], v=qkv[2], res=res, do=do, grid=grid, grid_pad=gp, topk=topk, cdf=cdf,
+                sp_only=sp_only, B=B, H=H, D=D, S=S)
+
+
+# ------------------------------------------------------------------ timing helpers
+def time_region(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    st = torch.cuda.Event(enable_timing=True)
+    en = torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(steps):
+        fn()
+    en.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return st.elapsed_time(en) / steps, wall / steps * 1e3
+
+
+def kernel_ms(fn, reps=5):
+    """Average duration of the kernels `fn` launches on the current stream,
+    bracketed by HIP events on that stream."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.Event(enable_timing=True)
+    en = torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(reps):
+        fn()
+    en.record()
+    torch.cuda.synchronize()
+    return st.elapsed_time(en) / reps
+
+
+# ------------------------------------------------------------------ CPU baseline (oracle)
+def cpu_baseline(plan, inp, budget_s=12.0):
+    """float64 numpy oracle attention fwd+bwd on a seeded sample of query
+    tiles of the same plan, reported as kept-block TFLOP/s."""
+    import numpy as np
+    from oracle import oracle as O
+    B, H, S, D = plan.B, plan.H, plan.S, plan.D
+    Nt = plan.lay.Nt
+    qlen = plan.qlen.cpu().numpy()
+    qstart = plan.qstart.cpu().numpy()
+    qcols = plan.qcols.cpu().numpy()
+    rng = np.random.default_rng(0)
+    rows = rng.permutation(np.nonzero(qlen > 0)[0])
+    tof = lambda t: t.float().cpu().numpy().reshape(B * H, S, D)
+    q, k, v = tof(plan.q_re), tof(plan.k_re), tof(plan.v_re)
+    sm = 1 / math.sqrt(D)
+    done_pairs, t_used, n_rows = 0, 0.0, 0
+    for r in rows:
+        bh, t = divmod(int(r), Nt)
+        n = int(qlen[r])
+        t0 = time.perf_counter()
+        # one query tile against its listed key tiles: tile 0 holds the
+        # queries, tiles 1..n the keys/values, and only tile 0 has a list
+        keys = O._row_keys(qcols, int(qstart[r]), n)
+        Sx = 64 * (n + 1)
+        qx = np.zeros((1, Sx, D), np.float32)
+        kx = np.zeros((1, Sx, D), np.float32)
+        vx = np.zeros((1, Sx, D), np.float32)
+        qx[0, :64] = q[bh, t * 64:(t + 1) * 64]
+        kx[0, 64:] = k[bh, keys]
+        vx[0, 64:] = v[bh, keys]
+        st = np.zeros(n + 1, np.int64)
+        ln = np.zeros(n + 1, np.int32)
+        ln[0] = n
+        cols = np.arange(1, n + 1, dtype=np.int32)
+        o, lse = O.attn_fwd(qx, kx, vx, st, ln, cols, None, sm)
+        O.attn_bwd(qx, kx, vx, o, np.ones_like(o), lse, st, ln, cols, None, sm)
+        t_used += time.perf_counter() - t0
+        done_pairs += n
+        n_rows += 1
+        if t_used > budget_s:
+            break
+    flops = 14 * 64 * 64 * D * done_pairs
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": flops / t_used / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"float64 numpy oracle attention fwd+bwd on {n_rows} random query tiles "
+                      f"({done_pairs} kept tile pairs) of the same plan, {t_used:.1f} s"}
+
+
+# ------------------------------------------------------------------ main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
+    ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path shards by "
+              "head across GPUs and is not run multi-GPU here", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from prism_amd import DynamicBlockSparseAttention, a2v_token_norms, plan_dynamic, valid_mask_for
+    from prism_amd import ops
+    from prism_amd.adapter import padded_grid
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    log(f"[bench] config {args.config}: generating inputs")
+    inp = make_inputs(args.config)
+    B, H, D, S = inp["B"], inp["H"], inp["D"], inp["S"]
+    grid = inp["grid"]
+    gp, _ = padded_grid(grid)
+
+    # N_b from the shape decision on these inputs -> sparsity giving top-k exactly
+    norms0 = a2v_token_norms(inp["res"])
+    dyn = DynamicBlockSparseAttention("ivpq", {"dynamic_block_tau_128": 0.15})
+    q0 = inp["q"]
+    with torch.no_grad():
+        vm = valid_mask_for(grid, q0.device)
+        pad = lambda t: torch.nn.functional.pad(t.view(B, H, *grid, D), (0, 0, 0, gp[2] - grid[2], 0, gp[1] - grid[1], 0, gp[0] - grid[0])).reshape(B, H, -1, D)
+        npad = torch.nn.functional.pad(norms0.view(*grid), (0, gp[2] - grid[2], 0, gp[1] - grid[1], 0, gp[0] - grid[0])).reshape(-1)
+        from prism_amd.dynamic_block_shape import select_zone_shapes
+        sid = select_zone_shapes(pad(inp["v"]), npad, gp, "ivpq", valid_mask_thw=vm)
+        N_b = ops.ZoneLayout(sid, gp).N_b
+    if inp["sp_only"] is not None:
+        sparsity, cdf = inp["sp_only"], None
+    else:
+        sparsity, cdf = 1.0 - (inp["topk"] + 0.5) / N_b, inp["cdf"]
+    dyn.bsa_params.update({"sparsity": sparsity, "cdf_threshold": cdf})
+    log(f"[bench] N_b={N_b} sparsity={sparsity:.6f} cdf={cdf}")
+
+    q = inp["q"].clone().requires_grad_(True)
+    k = inp["k"].clone().requires_grad_(True)
+    v = inp["v"].clone().requires_grad_(True)
+    do = inp["do"]
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        norms = a2v_token_norms(inp["res"])
+        out = dyn(q, k, v, grid, norms)
+        out.backward(do)
+
+    log("[bench] timing full step")
+    ms, wall_ms = time_region(step, args.steps, args.warmup)
+
+    # plan (selection) on the same inputs for density / per-kernel timing
+    with torch.no_grad():
+        plan = plan_dynamic(pad(q.detach()), pad(k.detach()), pad(v.detach()), gp, method="ivpq", sparsity=sparsity,
+                            cdf_threshold=cdf, audio_token_norms=npad, valid_mask=vm)
+    sum_lens = plan.sum_lens()
+    Nt = plan.lay.Nt
+    density = sum_lens / (B * H * Nt * Nt)
+    kept_flops = 14 * 64 * 64 * D * sum_lens
+    sm = 1 / math.sqrt(D)
+
+    # per-kernel durations (HIP events on the launch stream)
+    log("[bench] per-kernel timing")
+    with torch.no_grad():
+        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.kv_valid, plan.qstart, plan.qlen, plan.qcols, sm)
+        do_pad = pad(do)
+        gd = ops.gather_pool(do_pad, plan.lay, None, rows=True, dot_with=o_re)
+        do_re, delta = gd["rows"], gd["rowdot"]
+        dot, qt, kt = ops.transpose_tiles(do_re), ops.transpose_tiles(plan.q_re), ops.transpose_tiles(plan.k_re)
+        klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, Nt)
+        t_fwd = kernel_ms(lambda: ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.kv_valid, plan.qstart, plan.qlen,
+                                              plan.qcols, sm))
+        dq = torch.empty_like(plan.q_re); dk = torch.empty_like(plan.k_re); dv = torch.empty_like(plan.v_re)
+        s_ = ops._stream()
+        P = lambda t: None if t is None else t.data_ptr()
+        t_dkdv = kernel_ms(lambda: ops._lib.call(
+            "prism_bsa_bwd_dkdv", P(plan.q_re), P(qt), P(plan.k_re), P(plan.v_re), P(do_re), P(dot), P(lse), P(delta),
+            B * H, plan.S, D, P(plan.kv_valid), P(klists[0]), P(klists[1]), P(klists[2]), sm, P(dk), P(dv), s_))
+        t_dq = kernel_ms(lambda: ops._lib.call(
+            "prism_bsa_bwd_dq", P(plan.q_re), P(plan.k_re), P(kt), P(plan.v_re), P(do_re), P(lse), P(delta), B * H,
+            plan.S, D, P(plan.kv_valid), P(plan.qstart), P(plan.qlen), P(plan.qcols), sm, P(dq), s_))
+        # selection-side kernels
+        t_stats = kernel_ms(lambda: ops.zone_stats(pad(v.detach()), gp, vm))
+        t_norms = kernel_ms(lambda: a2v_token_norms(inp["res"]))
+        t_gather = kernel_ms(lambda: ops.gather_pool(pad(q.detach()), plan.lay, vm, rows=True, pool=True))
+        qm = ops.gather_pool(pad(q.detach()), plan.lay, vm, rows=False, pool=True)["block_mean"]
+        km = ops.gather_pool(pad(k.detach()), plan.lay, vm, rows=False, pool=True)["block_mean"]
+        Nb = plan.lay.N_b
+        t_scores = kernel_ms(lambda: ops.block_scores(qm.view(B * H, Nb, D), km.view(B * H, Nb, D), plan.block_count))
+        t_select = kernel_ms(lambda: ops.select_tiles(plan.scores, sparsity, cdf, sm, plan.lay.block_first_tile,
+                                                      plan.tile_count))
+    fl = 64 * 64 * D * sum_lens
+    kern = {"bsa_fwd": (t_fwd, 4 * fl), "bsa_bwd_dkdv": (t_dkdv, 8 * fl), "bsa_bwd_dq": (t_dq, 6 * fl)}
+    dom = max(kern, key=lambda n: kern[n][0])
+    dom_ms, dom_fl = kern[dom]
+    att_ms = t_fwd + t_dkdv + t_dq
+    roof = {"kernel": dom, "bound": "mfma", "achieved": dom_fl / (dom_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "traffic": None}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    hbm = {
+        "zone_stats": (t_stats, B * H * S * D * 2 + plan.lay.Nz * 25 * D * 4),
+        "a2v_norms": (t_norms, S * inp["res"].shape[-1] * 2 + S * 2),
+        "select": (t_select, B * H * plan.lay.N_b ** 2 * 4 + 4 * int(plan.sel["ntiles"].sum().item())),
+    }
+    breakdown = {n: {"ms": round(t, 4), "tflops": round(f / (t * 1e-3) / 1e12, 1),
+                     "mfma_util": round(f / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)} for n, (t, f) in kern.items()}
+    for n, (t, b) in hbm.items():
+        breakdown[n] = {"ms": round(t, 4), "GBps": round(b / (t * 1e-3) / 1e9, 1),
+                        "hbm_frac": round(b / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    breakdown["gather_pool_q"] = {"ms": round(t_gather, 4)}
+    breakdown["block_scores"] = {"ms": round(t_scores, 4), "tflops_fp32": round(
+        2 * B * H * plan.lay.N_b ** 2 * D / (t_scores * 1e-3) / 1e12, 2)}
+    breakdown["attention_total"] = {"ms": round(att_ms, 3), "mfma_util_kept_10x": round(
+        (14 * fl) / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+
+    dense = None
+    if not args.no_dense:
+        log("[bench] dense SDPA comparison")
+        qd = inp["q"].clone().requires_grad_(True)
+        kd = inp["k"].clone().requires_grad_(True)
+        vd = inp["v"].clone().requires_grad_(True)
+
+        def dstep():
+            qd.grad = kd.grad = vd.grad = None
+            o = torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)
+            o.backward(do)
+
+        try:
+            dms, _ = time_region(dstep, 2, 1)
+            dense = {"impl": "torch SDPA (ROCm) fwd+bwd, same shape, unpadded", "ms": round(dms, 2),
+                     "tflops": round(14 * S * S * D * B * H / (dms * 1e-3) / 1e12, 1),
+                     "speedup_sparse_vs_dense": round(dms / ms, 2)}
+        except Exception as e:  # report, do not fail the bench
+            dense = {"error": repr(e)[:200]}
+        del qd, kd, vd
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU oracle baseline")
+        cpu = cpu_baseline(plan, inp, args.cpu_budget)
+
+    value = kept_flops / (ms * 1e-3) / 1e12
+    rec = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{args.config}: BASELINE config {'4 (2K fwd+bwd)' if args.config == 'c4' else args.config}",
+                   "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(gp),
+                   "audio_tokens": CONFIGS[args.config][4], "topk": inp["topk"], "cdf_threshold": cdf,
+                   "sparsity": sparsity, "N_b": plan.lay.N_b, "sum_lens": sum_lens, "density": round(density, 4),
+                   "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3)},
+        "roofline": roof, "cpu_baseline": cpu, "dense": dense, "breakdown": breakdown,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

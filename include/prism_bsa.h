@@ -1,0 +1,188 @@
+/*
+ * prism_bsa.h -- C-ABI of libprism_bsa.so, the MI355X (gfx950) implementation
+ * of Prism's dynamic block-sparse attention path.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is a device pointer
+ * (HIP) unless stated otherwise; every call is asynchronous on `stream` and
+ * returns 0 on success, 1 for an invalid argument, 2 for a HIP launch error;
+ * prism_last_error() then holds the message (per host thread).
+ *
+ * Citations name the reference function (file:line under
+ * hymm/models/modules/block_sparse_attention/ unless another path is given)
+ * whose behaviour the entry point provides.  The reference is Python/Triton;
+ * its host layer's calls into these functions are shown in INTEGRATION.md.
+ *
+ * dtype codes: PRISM_F32 = 0, PRISM_BF16 = 1.
+ * Layouts: "THW order" = the reference's flattened (t, h, w) token order of a
+ * padded grid T x Hg x Wg (all multiples of 8); "tile order" = the per-zone
+ * anisotropic rearrangement of _build_rearrange_index
+ * (dynamic_block_attention.py:107-135): zone z owns positions
+ * [512 z, 512 z + 512), tile t = position / 64.
+ */
+#ifndef PRISM_BSA_H_
+#define PRISM_BSA_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PRISM_F32 0
+#define PRISM_BF16 1
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* prism_last_error(void);
+/* ABI version of this library. */
+int prism_abi_version(void);
+
+/* ------------------------------------------------------------------ zone statistics */
+
+/* compute_zone_aggregates (dynamic_block_shape.py:68-129) applied to the
+ * batch-0 head mean of V (dynamic_block_attention.py:236).
+ * v: [B,H,S,D] THW order (only batch 0 is read), valid: [S] uint8 or NULL.
+ * packed: [Nz, 25*D] fp32 = channel(D) | frame means(8D) | h means(8D) | w means(8D);
+ * axis_valid: [Nz, 24] uint8 (t, h, w "has a valid token" flags). */
+int prism_zone_stats(const void* v, int dtype, int H, int64_t S, int D, const uint8_t* valid,
+                     int T, int Hg, int Wg, float* packed, uint8_t* axis_valid, hipStream_t stream);
+
+/* compute_audio_directional (dynamic_block_shape.py:189-245) before the
+ * max-normalisation of a_bar.  norms: [S] THW order.  abar: [Nz]; vhat: [Nz,3]. */
+int prism_audio_zone_stats(const void* norms, int dtype, const uint8_t* valid, int T, int Hg, int Wg,
+                           float* abar, float* vhat, hipStream_t stream);
+
+/* Per-zone part of compute_effective_gradient (dynamic_block_shape.py:248-289):
+ * rho_raw = spatial + temporal variance, aniso = axis variances / their sum. */
+int prism_zone_gradient(const float* packed, const uint8_t* axis_valid, int Nz, int D,
+                        float* rho_raw, float* aniso, hipStream_t stream);
+
+/* Zone normalisation, g = aniso + lambda_a * a_bar * v_hat (clamped >= 1e-4)
+ * (dynamic_block_shape.py:280, :297-300) and the shape decision of
+ * select_shapes_ivpq (method 0, :303-327) or select_shapes_penalty (method 1,
+ * :330-355).  abar/vhat NULL = no audio.  Outputs g [Nz,3], rho [Nz],
+ * shape_ids [Nz] int64 (index into the 13-entry candidate table :6-27). */
+int prism_zone_shapes(const float* rho_raw, const float* aniso, const float* abar, const float* vhat,
+                      int Nz, int method, float lambda_a, float tau_128, float lambda_128,
+                      float* g, float* rho, int64_t* shape_ids, hipStream_t stream);
+
+/* select_shapes_ivpq (method 0, dynamic_block_shape.py:303-327) /
+ * select_shapes_penalty (method 1, :330-355) on given g [Nz,3] and rho [Nz]. */
+int prism_assign_shapes(const float* g, const float* rho, int Nz, int method, float tau_128, float lambda_128,
+                        int64_t* shape_ids, hipStream_t stream);
+
+/* Per-token L2 norm of the A->V bridge residual, batch 0
+ * (hymm/models/modules/wan_video_dit.py:742-752).  res: [S, C]; out: [S]. */
+int prism_a2v_norms(const void* res, int dtype, int64_t S, int C, void* out, int out_dtype,
+                    hipStream_t stream);
+
+/* ------------------------------------------------------------------ geometry */
+
+/* _build_block_tile_maps (dynamic_block_attention.py:138-170) in CSR form.
+ * block_offset: [Nz+1] (block_offset[Nz] = N_b), block_id_of_tile: [Nz*8],
+ * block_first_tile: [Nz*8+1] (block b owns tiles [first[b], first[b+1]);
+ * entry N_b is the sentinel N_tiles, as kblock_tiles row N_b). */
+int prism_zone_layout(const int64_t* shape_ids, int Nz, int32_t* block_offset, int32_t* block_id_of_tile,
+                      int32_t* block_first_tile, hipStream_t stream);
+
+/* _build_rearrange_index (dynamic_block_attention.py:107-135): src_idx[S]
+ * (tile position -> THW index) and inv_idx[S]. */
+int prism_rearrange_index(const int64_t* shape_ids, int T, int Hg, int Wg, int64_t* src_idx, int64_t* inv_idx,
+                          hipStream_t stream);
+
+/* x.index_select(2, src_idx) (dynamic_block_attention.py:250-253) fused with
+ * masked_mean_pooling_compression + _logical_block_means
+ * (bsa_interface.py:177-201, dynamic_block_attention.py:173-188).
+ * x: [B,H,S,D] THW order.  Optional outputs (NULL to skip):
+ *   out_rows [B,H,S,D] bf16 tile order; block_mean [B,H,N_b,D] fp32;
+ *   block_count [N_b], tile_count [S/64] int32; valid_re [S] uint8 tile order;
+ *   rowdot [B,H,S] fp32 = rowsum(x_re * dot_with) with dot_with [B,H,S,D] bf16
+ *   tile order (the delta of common.py:110-127 when x = dO, dot_with = O). */
+int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, const uint8_t* valid,
+                      const int64_t* shape_ids, const int32_t* block_offset, int T, int Hg, int Wg, int64_t N_b,
+                      void* out_rows, float* block_mean, int32_t* block_count, int32_t* tile_count,
+                      uint8_t* valid_re, const void* dot_with, float* rowdot, hipStream_t stream);
+
+/* Transposed 64-row tiles: in [BH,S,D] bf16 -> out [BH,S/64,D,64] bf16 (the
+ * operand layout of the MFMA kernels for V in the forward and Q, K, dO in the
+ * backward; no reference counterpart, the Triton kernels transpose in SRAM). */
+int prism_transpose_tiles(const void* in_rows, int BH, int64_t S, int D, void* out_t, hipStream_t stream);
+
+/* o_re.index_select(2, inv_idx) (dynamic_block_attention.py:329): tile-order
+ * bf16 rows -> THW order rows of out_dtype. */
+int prism_scatter_rows(const void* in_rows, int B, int H, int64_t S, int D, const int64_t* shape_ids, int T,
+                       int Hg, int Wg, void* out, int out_dtype, hipStream_t stream);
+
+/* ------------------------------------------------------------------ selection */
+
+/* cal_score (bsa_interface.py:203-207) in fp32 with the invalid-key fill of
+ * dynamic_block_attention.py:276-279 (block_count[j] == 0 -> -inf; NULL = none).
+ * qc, kc: [BH, N, D] fp32; scores: [BH, N, N] fp32. */
+int prism_block_scores(const float* qc, const float* kc, const int32_t* block_count, int BH, int64_t N, int D,
+                       float* scores, hipStream_t stream);
+
+/* Per-row block selection fused with the block -> tile expansion:
+ *   mode 0: get_select_indices_topk_from_score (bsa_interface.py:235-248), k = k_lo;
+ *   mode 1: get_select_indices_cdf_from_score (:257-275), k_lo = 1;
+ *   mode 2: get_select_indices_cdf_topk_from_score (:284-304), k_lo = k_t;
+ * ub as the reference derives it; thr = cumulative threshold in 2^-60 fixed
+ * point (smallest X with fl32(X) 2^-60 >= p).  Expansion and padded-tile
+ * filtering: dynamic_block_attention.py:297-319 (tile_count NULL = keep all).
+ * tiles: [rows, tcap] ascending tile ids, ntiles: [rows];
+ * sel_blocks: [rows, bcap] ascending block ids (NULL to skip), nsel: [rows]. */
+int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, int64_t k_lo, int64_t ub,
+                       float scale, uint64_t thr, const int32_t* block_first_tile, const int32_t* tile_count,
+                       int64_t tcap, int32_t* tiles, int32_t* ntiles, int32_t* sel_blocks, int64_t bcap,
+                       int32_t* nsel, hipStream_t stream);
+
+/* q tile rows share their q block's list (tile_sel.index_select(2,
+ * block_id_of_tile), dynamic_block_attention.py:315-318):
+ * qstart[bh*Nt + t] = (bh*N_b + block_id_of_tile[t]) * tcap, qlen likewise. */
+int prism_tile_rows(const int32_t* ntiles, const int32_t* block_id_of_tile, int BH, int64_t Nt, int64_t N_b,
+                    int64_t tcap, int64_t* qstart, int32_t* qlen, hipStream_t stream);
+
+/* create_indices_k_from_indices_q_varlen (bsa_interface.py:147-161) as a
+ * bitmap transpose.  bitmap: workspace of BH*Nt*ceil(Nt/32) uint32.
+ * Output per key tile (row bh*Nt + k): kstart = row*kcap, klen, kcols
+ * ascending query tiles. */
+int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH, int64_t Nt,
+                          uint32_t* bitmap, int64_t kcap, int64_t* kstart, int32_t* klen, int32_t* kcols,
+                          hipStream_t stream);
+
+/* ------------------------------------------------------------------ attention */
+
+/* attn_fwd_bsa_varlen_triton (bsa_interface.py:328-385) with
+ * _attn_fwd_bsa_varlen_align (flash_attn_bsa_varlen_mask.py:191-319), chunk 64.
+ * q, k: [BH,S,D] bf16 tile order; vt: [BH,S/64,D,64] bf16 transposed tiles;
+ * kv_valid: [S] uint8 or NULL; per query tile row bh*Nt + t the key tiles
+ * qcols[qstart[row] .. + qlen[row]).  o: [BH,S,D] bf16; lse: [BH,S] fp32
+ * natural log (-inf for rows without a valid key; their o is 0). */
+int prism_bsa_fwd(const void* q, const void* k, const void* vt, int BH, int64_t S, int D, const uint8_t* kv_valid,
+                  const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, float sm_scale, void* o,
+                  float* lse, hipStream_t stream);
+
+/* _attn_bwd_preprocess (common.py:110-127): delta[r] = sum_d o[r][d] * do[r][d]
+ * over rows of bf16 [rows, D] tensors; fp32 out. */
+int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, float* delta, hipStream_t stream);
+
+/* dK, dV of attn_bwd_bsa_varlen_triton (bsa_interface.py:387-487;
+ * _attn_bwd_dkdv_bsa_varlen_wrapper, flash_attn_bsa_varlen_mask.py:562-704).
+ * qt, dot: transposed tiles of q and dO; delta from prism_gather_pool;
+ * lists per key tile from prism_transpose_lists. */
+int prism_bsa_bwd_dkdv(const void* q, const void* qt, const void* k, const void* v, const void* do_, const void* dot,
+                       const float* lse, const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid,
+                       const int64_t* kstart, const int32_t* klen, const int32_t* kcols, float sm_scale, void* dk,
+                       void* dv, hipStream_t stream);
+
+/* dQ of attn_bwd_bsa_varlen_triton (bsa_interface.py:489-523;
+ * _attn_bwd_dq_bsa_varlen_align_wrapper, flash_attn_bsa_varlen_mask.py:879-1014).
+ * kt: transposed tiles of k; lists per query tile as for prism_bsa_fwd. */
+int prism_bsa_bwd_dq(const void* q, const void* k, const void* kt, const void* v, const void* do_, const float* lse,
+                     const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid, const int64_t* qstart,
+                     const int32_t* qlen, const int32_t* qcols, float sm_scale, void* dq, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRISM_BSA_H_ */

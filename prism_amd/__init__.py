@@ -1,0 +1,18 @@
+"""prism_amd: MI355X-native (gfx950) dynamic block-sparse attention path of
+Tencent-Hunyuan/Prism, behind the reference's module API.
+
+Public surface (reference names):
+  flash_attn_bsa_3d_dynamic   dynamic_block_attention.py:194
+  select_zone_shapes          dynamic_block_shape.py:358
+  DynamicBlockSparseAttention SelfAttention._run_bsa_dynamic contract
+All compute runs in libprism_bsa.so (build: python -m prism_amd.build).
+"""
+from .dynamic_block_shape import (  # noqa: F401
+    ALL_CANDIDATE_SHAPES, CANDIDATE_SHAPES_64, CANDIDATE_SHAPES_128, NUM_CANDIDATES, NUM_CANDIDATES_64, ZONE_SIZE,
+    compute_audio_directional, compute_effective_gradient, compute_zone_aggregates, select_shapes_ivpq,
+    select_shapes_penalty, select_zone_shapes,
+)
+from .dynamic_block_attention import _TILE, flash_attn_bsa_3d_dynamic, plan_dynamic  # noqa: F401
+from .adapter import DynamicBlockSparseAttention, a2v_token_norms, valid_mask_for  # noqa: F401
+
+__version__ = "0.1.0"

@@ -1,0 +1,114 @@
+"""Caller-side adapter: the contract of SelfAttention._run_bsa_dynamic
+(hymm/models/modules/wan_video_dit.py:342-432) and the A2V norm computation
+(wan_video_dit.py:739-752), on top of flash_attn_bsa_3d_dynamic.
+
+Pads T, H, W up to multiples of ZONE_SIZE, builds the valid mask of the
+padded grid, pads the audio norms with zeros, reuses cached shape ids within
+one training forward pass (activation-checkpoint recompute), and unpads.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import ops
+from .dynamic_block_attention import flash_attn_bsa_3d_dynamic
+from .dynamic_block_shape import ZONE_SIZE
+
+# default bsa_params keys and values read by the reference (wan_video_dit.py:415-421)
+DEFAULT_BSA_PARAMS = {
+    "sparsity": 0.9375,
+    "cdf_threshold": None,
+    "dynamic_block_lambda_a": 0.5,
+    "dynamic_block_tau_128": 0.15,
+    "dynamic_block_lambda_128": 1.0,
+}
+
+
+def a2v_token_norms(a2v_bridge_residual: torch.Tensor) -> torch.Tensor:
+    """||residual[0, m, :]||_2 per token, in the residual's dtype
+    (wan_video_dit.py:742-752, single GPU: no all-gather)."""
+    with torch.no_grad():
+        return ops.a2v_norms(a2v_bridge_residual)
+
+
+def padded_grid(grid_size):
+    T, H, W = grid_size
+    pt = (ZONE_SIZE - T % ZONE_SIZE) % ZONE_SIZE
+    ph = (ZONE_SIZE - H % ZONE_SIZE) % ZONE_SIZE
+    pw = (ZONE_SIZE - W % ZONE_SIZE) % ZONE_SIZE
+    return (T + pt, H + ph, W + pw), (pt, ph, pw)
+
+
+def valid_mask_for(grid_size, device) -> Optional[torch.Tensor]:
+    """Bool [S_p] mask of real tokens in the padded grid (None if no padding)."""
+    T, H, W = grid_size
+    (Tp, Hp, Wp), pads = padded_grid(grid_size)
+    if not any(pads):
+        return None
+    it = torch.arange(Tp, device=device)
+    ih = torch.arange(Hp, device=device)
+    iw = torch.arange(Wp, device=device)
+    return ((it[:, None, None] < T) & (ih[None, :, None] < H) & (iw[None, None, :] < W)).reshape(-1).contiguous()
+
+
+class DynamicBlockSparseAttention:
+    """State the reference keeps on SelfAttention for the dynamic path: the
+    bsa_params dict, the method switch and the per-pass shape cache
+    (wan_video_dit.py:22-33, :401-427)."""
+
+    def __init__(self, method: str = "ivpq", bsa_params: Optional[dict] = None):
+        if method not in ("ivpq", "penalty"):
+            raise ValueError(f"unknown dynamic-block method: {method!r}")
+        self.method = method
+        self.bsa_params = dict(DEFAULT_BSA_PARAMS)
+        if bsa_params:
+            self.bsa_params.update(bsa_params)
+        self.training = False
+        self.pass_id = 0
+        self._dyn_shape_cache = None
+
+    def advance_pass(self) -> int:
+        """Call once per real outer forward (advance_dynamic_block_pass_id)."""
+        self.pass_id += 1
+        return self.pass_id
+
+    def __call__(self, q_bhsd, k_bhsd, v_bhsd, grid_size, audio_token_norms=None):
+        return self.run_bsa_dynamic(q_bhsd, k_bhsd, v_bhsd, grid_size, audio_token_norms)
+
+    def run_bsa_dynamic(self, q_bhsd, k_bhsd, v_bhsd, grid_size, audio_token_norms=None):
+        T, H, W = grid_size
+        B, n_heads, S, D = q_bhsd.shape
+        (Tp, Hp, Wp), (pt, ph, pw) = padded_grid(grid_size)
+        need_pad = pt > 0 or ph > 0 or pw > 0
+        valid_mask = None
+        audio_p = audio_token_norms
+        if need_pad:
+            valid_mask = valid_mask_for(grid_size, q_bhsd.device)
+
+            def _pad(t):
+                return F.pad(t.view(B, n_heads, T, H, W, D), (0, 0, 0, pw, 0, ph, 0, pt)).reshape(B, n_heads, -1, D)
+
+            q_bhsd, k_bhsd, v_bhsd = _pad(q_bhsd), _pad(k_bhsd), _pad(v_bhsd)
+            if audio_token_norms is not None:
+                audio_p = F.pad(audio_token_norms.reshape(T, H, W), (0, pw, 0, ph, 0, pt)).reshape(-1)
+        grid_padded = (Tp, Hp, Wp)
+        cached = None
+        if self.training and self._dyn_shape_cache is not None:
+            pid, g, ids = self._dyn_shape_cache
+            if pid == self.pass_id and g == grid_padded:
+                cached = ids
+        p = self.bsa_params
+        out, used = flash_attn_bsa_3d_dynamic(
+            q_bhsd, k_bhsd, v_bhsd, grid_padded, method=self.method,
+            sparsity=p.get("sparsity", 0.9375), cdf_threshold=p.get("cdf_threshold", None),
+            audio_token_norms=audio_p, valid_mask=valid_mask,
+            lambda_a=p.get("dynamic_block_lambda_a", 0.5), tau_128=p.get("dynamic_block_tau_128", 0.15),
+            lambda_128=p.get("dynamic_block_lambda_128", 1.0), shape_ids=cached, return_shape_ids=True)
+        if self.training:
+            self._dyn_shape_cache = (self.pass_id, grid_padded, used)
+        if need_pad:
+            out = out.view(B, n_heads, Tp, Hp, Wp, D)[:, :, :T, :H, :W, :].contiguous().reshape(B, n_heads, T * H * W, D)
+        return out

@@ -1,0 +1,453 @@
+// Block scores, hybrid top-k / cumulative-threshold selection, tile lists and
+// their transpose (gfx950).
+//
+// Reference (hymm/models/modules/block_sparse_attention/):
+//   block_scores_kernel  cal_score (bsa_interface.py:203-207) + invalid-key fill
+//                        (dynamic_block_attention.py:276-279), fp32 out
+//   select_kernel        get_select_indices_topk_from_score (bsa_interface.py:235-248),
+//                        get_select_indices_cdf_from_score (:257-275),
+//                        get_select_indices_cdf_topk_from_score (:284-304),
+//                        fused with the block -> tile expansion
+//                        (dynamic_block_attention.py:297-319)
+//   tile_rows_kernel     q-tile rows share their q-block's list (:315-318)
+//   transpose kernels    create_indices_k_from_indices_q_varlen (bsa_interface.py:147-161)
+//                        as a bitmap transpose instead of a dense N_tiles^2 mask + sort
+//
+// Canonical arithmetic (compiled with -ffp-contract=off):
+//   score   = fmaf chain over d ascending, from +0;
+//   softmax = e_j = canon_exp(s_j*scale - max), sum = fl32(sum_j floor(e_j 2^40)) 2^-40,
+//             w_j = e_j / sum;
+//   cdf     = exact fixed-point prefix sums of floor(w 2^60) in (w desc, index asc)
+//             order; "cdf < p" <=> prefix < thr (thr from the host).
+// The selection never sorts: the crossing element is found by bisection on
+// the fp32 bit pattern of w (order-preserving for w >= 0) with exact integer
+// sums, so the result does not depend on thread order.
+#include "common.h"
+
+namespace {
+
+// ------------------------------------------------------------------ scores
+constexpr int kSTile = 128, kSChunk = 16;
+
+__global__ __launch_bounds__(256) void block_scores_kernel(const float* __restrict__ qc, const float* __restrict__ kc,
+                                                           const int32_t* __restrict__ block_count, int64_t N, int D,
+                                                           float* __restrict__ scores) {
+  __shared__ float sA[kSChunk][kSTile + 4];
+  __shared__ float sB[kSChunk][kSTile + 4];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int64_t i0 = (int64_t)blockIdx.y * kSTile, j0 = (int64_t)blockIdx.x * kSTile;
+  const int bh = blockIdx.z;
+  const float* A = qc + (int64_t)bh * N * D;
+  const float* Bm = kc + (int64_t)bh * N * D;
+  float acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+
+  for (int d0 = 0; d0 < D; d0 += kSChunk) {
+    // 128 rows x 16 cols = 512 float4 per operand; 2 per thread
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = tid + u * 256;
+      const int row = idx >> 2, c4 = (idx & 3) * 4;
+      float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
+      if (i0 + row < N) va = *reinterpret_cast<const float4*>(A + (i0 + row) * D + d0 + c4);
+      if (j0 + row < N) vb = *reinterpret_cast<const float4*>(Bm + (j0 + row) * D + d0 + c4);
+      sA[c4 + 0][row] = va.x; sA[c4 + 1][row] = va.y; sA[c4 + 2][row] = va.z; sA[c4 + 3][row] = va.w;
+      sB[c4 + 0][row] = vb.x; sB[c4 + 1][row] = vb.y; sB[c4 + 2][row] = vb.z; sB[c4 + 3][row] = vb.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kSChunk; ++kk) {
+      float a[8], b[8];
+      const float4 a0 = *reinterpret_cast<const float4*>(&sA[kk][ty * 8]);
+      const float4 a1 = *reinterpret_cast<const float4*>(&sA[kk][ty * 8 + 4]);
+      const float4 b0 = *reinterpret_cast<const float4*>(&sB[kk][tx * 8]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&sB[kk][tx * 8 + 4]);
+      a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w; a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
+      b[0] = b0.x; b[1] = b0.y; b[2] = b0.z; b[3] = b0.w; b[4] = b1.x; b[5] = b1.y; b[6] = b1.z; b[7] = b1.w;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  const float ninf = -__uint_as_float(0x7f800000u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t row = i0 + ty * 8 + i;
+    if (row >= N) continue;
+    float* out = scores + ((int64_t)bh * N + row) * N;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t col = j0 + tx * 8 + j;
+      if (col < N) out[col] = (block_count && block_count[col] == 0) ? ninf : acc[i][j];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ block-wide helpers (256 threads)
+constexpr int kSelThreads = 256;
+constexpr int kSelWaves = kSelThreads / 64;
+
+struct SelShared {
+  uint64_t u64[kSelWaves];
+  uint32_t u32[kSelWaves];
+  float f32[kSelWaves];
+};
+
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, SelShared& sh) {
+  v = wave_sum_u64(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) sh.u64[wid] = v;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) t += sh.u64[w];
+  __syncthreads();
+  return t;
+}
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, SelShared& sh) {
+  v = wave_sum_u32(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) sh.u32[wid] = v;
+  __syncthreads();
+  uint32_t t = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) t += sh.u32[w];
+  __syncthreads();
+  return t;
+}
+__device__ __forceinline__ float block_max_f32(float v, SelShared& sh) {
+  v = wave_max_xor(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) sh.f32[wid] = v;
+  __syncthreads();
+  float t = sh.f32[0];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) t = fmaxf(t, sh.f32[w]);
+  __syncthreads();
+  return t;
+}
+// exclusive scan in thread order; returns the block total in *total
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, SelShared& sh, uint32_t* total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const uint32_t incl = wave_incl_scan_u32(v, lane);
+  if (lane == 63) sh.u32[wid] = incl;
+  __syncthreads();
+  uint32_t before = 0, t = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const uint32_t x = sh.u32[w];
+    before += (w < wid) ? x : 0u;
+    t += x;
+  }
+  __syncthreads();
+  *total = t;
+  return before + incl - v;
+}
+
+struct SelArgs {
+  const float* scores;            // [rows, N]
+  int64_t rows, N;
+  int mode;                       // 0 top-k, 1 cdf, 2 cdf + top-k
+  int64_t k_lo, ub;
+  float scale;
+  uint64_t thr;
+  const int32_t* block_first_tile;  // [N+1]
+  const int32_t* tile_count;        // [Nt] or null (no padded-tile filtering)
+  int64_t tcap;
+  int32_t* tiles;                 // [rows, tcap]
+  int32_t* ntiles;                // [rows]
+  int32_t* sel_blocks;            // [rows, bcap] or null
+  int64_t bcap;
+  int32_t* nsel;                  // [rows] or null
+};
+
+// One workgroup per row; element j lives in thread j % 256, slot j / 256.
+template <int EPT>
+__global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
+  __shared__ SelShared sh;
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* s = a.scores + row * a.N;
+  const int64_t N = a.N;
+
+  uint32_t key[EPT];
+  uint64_t W[EPT];
+  uint64_t present = 0;  // bit e: slot e holds a real element
+  int64_t eff = 0;
+  uint32_t v_e = 0;
+  uint64_t need = 0;
+
+  if (a.mode == 0) {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int64_t j = (int64_t)e * kSelThreads + tid;
+      key[e] = 0;
+      W[e] = 0;
+      if (j < N) {
+        const uint32_t u = __float_as_uint(s[j]);
+        key[e] = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        present |= 1ull << e;
+      }
+    }
+    eff = a.k_lo < N ? a.k_lo : N;
+  } else {
+    float x[EPT];
+    float m = -__uint_as_float(0x7f800000u);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int64_t j = (int64_t)e * kSelThreads + tid;
+      x[e] = m;
+      if (j < N) {
+        x[e] = s[j] * a.scale;
+        m = fmaxf(m, x[e]);
+        present |= 1ull << e;
+      }
+    }
+    m = block_max_f32(m, sh);
+    if (m == -__uint_as_float(0x7f800000u)) {
+      eff = 0;
+    } else {
+      uint64_t E = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        x[e] = ((present >> e) & 1) ? canon_exp(x[e] - m) : 0.0f;
+        E += fixp(x[e], 40);
+      }
+      E = block_sum_u64(E, sh);
+      const float sum = (float)E * 9.094947017729282e-13f;  // 2^-40
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float w = ((present >> e) & 1) ? x[e] / sum : 0.0f;
+        key[e] = __float_as_uint(w);
+        W[e] = fixp(w, 60);
+      }
+      // G(v) = sum of W over present elements with key >= v
+      auto G = [&](uint32_t v) {
+        uint64_t t = 0;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) t += (((present >> e) & 1) && key[e] >= v) ? W[e] : 0ull;
+        return block_sum_u64(t, sh);
+      };
+      auto Nge = [&](uint32_t v) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) t += (((present >> e) & 1) && key[e] >= v) ? 1u : 0u;
+        return block_sum_u32(t, sh);
+      };
+      int64_t c = a.ub;
+      bool crossed = false;
+      uint32_t vc = 0;
+      uint64_t jt = 0;
+      if (G(0) >= a.thr) {
+        uint32_t lo = 0, hi = 0x3f800001u;  // G(lo) >= thr > G(hi)
+        while (hi - lo > 1) {
+          const uint32_t mid = lo + (hi - lo) / 2;
+          if (G(mid) >= a.thr) lo = mid; else hi = mid;
+        }
+        vc = lo;
+        const uint64_t A = G(vc + 1);
+        const uint32_t ngt = Nge(vc + 1);
+        const uint64_t Wv = fixp(__uint_as_float(vc), 60);
+        jt = (a.thr - A - 1) / Wv;  // smallest j with A + (j+1) Wv >= thr
+        const int64_t k = (int64_t)ngt + (int64_t)jt;
+        if (k < a.ub) { c = k; crossed = true; }
+      }
+      int64_t n = c + 1;
+      if (n < a.k_lo) n = a.k_lo;
+      if (n > N) n = N;
+      eff = n < a.ub ? n : a.ub;
+      if (crossed && eff == c + 1) {
+        v_e = vc;
+        need = jt + 1;
+        eff = -eff;  // marks "v_e already known"
+      }
+    }
+  }
+
+  if (eff > 0) {  // count search: largest v with #(key >= v) >= eff
+    auto Nge = [&](uint64_t v) {
+      uint32_t t = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) t += (((present >> e) & 1) && (uint64_t)key[e] >= v) ? 1u : 0u;
+      return block_sum_u32(t, sh);
+    };
+    uint64_t lo = 0, hi = 0x100000000ull;
+    while (hi - lo > 1) {
+      const uint64_t mid = lo + (hi - lo) / 2;
+      if ((int64_t)Nge(mid) >= eff) lo = mid; else hi = mid;
+    }
+    v_e = (uint32_t)lo;
+    need = (uint64_t)eff - Nge(lo + 1);
+  } else {
+    eff = -eff;
+  }
+
+  // emit selected blocks in ascending index order, expanded to tiles
+  uint32_t tie_carry = 0, out_carry = 0;
+  int32_t* trow = a.tiles + row * a.tcap;
+  int32_t* brow = a.sel_blocks ? a.sel_blocks + row * a.bcap : nullptr;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int64_t j = (int64_t)e * kSelThreads + tid;
+    const bool pres = (present >> e) & 1;
+    const bool tie = eff > 0 && pres && key[e] == v_e;
+    uint32_t tot;
+    const uint32_t rank = tie_carry + block_excl_scan_u32(tie ? 1u : 0u, sh, &tot);
+    tie_carry += tot;
+    const bool sel = eff > 0 && pres && (key[e] > v_e || (tie && rank < need));
+    uint32_t nt = 0;
+    int32_t t0 = 0, t1 = 0;
+    if (sel) {
+      t0 = a.block_first_tile[j];
+      t1 = a.block_first_tile[j + 1];
+      for (int32_t t = t0; t < t1; ++t) nt += (a.tile_count == nullptr || a.tile_count[t] > 0) ? 1u : 0u;
+    }
+    const uint32_t packed = nt | ((sel ? 1u : 0u) << 16);
+    const uint32_t pos = out_carry + block_excl_scan_u32(packed, sh, &tot);
+    out_carry += tot;
+    if (sel) {
+      uint32_t p = pos & 0xffffu;
+      for (int32_t t = t0; t < t1; ++t)
+        if (a.tile_count == nullptr || a.tile_count[t] > 0) trow[p++] = t;
+      if (brow) brow[pos >> 16] = (int32_t)j;
+    }
+  }
+  if (tid == 0) {
+    a.ntiles[row] = (int32_t)(out_carry & 0xffffu);
+    if (a.nsel) a.nsel[row] = (int32_t)(out_carry >> 16);
+  }
+}
+
+// q tile t of head bh uses the list of its block (shared by the block's tiles)
+__global__ void tile_rows_kernel(const int32_t* __restrict__ ntiles, const int32_t* __restrict__ block_id_of_tile,
+                                 int64_t BH, int64_t Nt, int64_t N_b, int64_t tcap, int64_t* __restrict__ qstart,
+                                 int32_t* __restrict__ qlen) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= BH * Nt) return;
+  const int64_t bh = i / Nt, t = i - bh * Nt;
+  const int64_t r = bh * N_b + block_id_of_tile[t];
+  qstart[i] = r * tcap;
+  qlen[i] = ntiles[r];
+}
+
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+// one 64-lane group per q row: set bit q in the bitmap row of every listed k tile
+__global__ __launch_bounds__(64) void set_bits_kernel(const int64_t* __restrict__ qstart, const int32_t* __restrict__ qlen,
+                                                      const int32_t* __restrict__ qcols, int64_t Nt, int64_t words,
+                                                      uint32_t* __restrict__ bm) {
+  const int64_t row = blockIdx.x;
+  const int64_t bh = row / Nt, t = row - bh * Nt;
+  const int n = qlen[row];
+  const int32_t* cols = qcols + qstart[row];
+  for (int i = threadIdx.x; i < n; i += 64) {
+    const int64_t k = cols[i];
+    atomicOr(&bm[(bh * Nt + k) * words + (t >> 5)], 1u << (t & 31));
+  }
+}
+
+// one wave per k row: emit the set bits (ascending q tiles)
+__global__ __launch_bounds__(256) void emit_bits_kernel(const uint32_t* __restrict__ bm, int64_t rows, int64_t Nt,
+                                                        int64_t words, int64_t kcap, int64_t* __restrict__ kstart,
+                                                        int32_t* __restrict__ klen, int32_t* __restrict__ kcols) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const uint32_t* w = bm + row * words;
+  int32_t* out = kcols + row * kcap;
+  uint32_t carry = 0;
+  for (int64_t base = 0; base < words; base += 64) {
+    const int64_t wi = base + lane;
+    uint32_t word = wi < words ? w[wi] : 0u;
+    const uint32_t c = __popc(word);
+    const uint32_t incl = wave_incl_scan_u32(c, lane);
+    uint32_t pos = carry + incl - c;
+    while (word) {
+      const int b = __ffs(word) - 1;
+      out[pos++] = (int32_t)(wi * 32 + b);
+      word &= word - 1;
+    }
+    carry += __shfl(incl, 63, 64);
+  }
+  if (lane == 0) {
+    kstart[row] = row * kcap;
+    klen[row] = (int32_t)carry;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int prism_block_scores(const float* qc, const float* kc, const int32_t* block_count, int BH, int64_t N, int D,
+                       float* scores, hipStream_t stream) {
+  PRISM_REQUIRE(qc && kc && scores, "prism_block_scores: null pointer");
+  PRISM_REQUIRE(D > 0 && D % kSChunk == 0, "prism_block_scores: D=%d must be a multiple of %d", D, kSChunk);
+  PRISM_REQUIRE(BH >= 1 && N >= 1, "prism_block_scores: empty problem");
+  dim3 grid((unsigned)((N + kSTile - 1) / kSTile), (unsigned)((N + kSTile - 1) / kSTile), BH);
+  block_scores_kernel<<<grid, 256, 0, stream>>>(qc, kc, block_count, N, D, scores);
+  PRISM_LAUNCH_CHECK("prism_block_scores");
+  return PRISM_OK;
+}
+
+int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, int64_t k_lo, int64_t ub, float scale,
+                       uint64_t thr, const int32_t* block_first_tile, const int32_t* tile_count, int64_t tcap,
+                       int32_t* tiles, int32_t* ntiles, int32_t* sel_blocks, int64_t bcap, int32_t* nsel,
+                       hipStream_t stream) {
+  PRISM_REQUIRE(scores && block_first_tile && tiles && ntiles, "prism_select_tiles: null pointer");
+  PRISM_REQUIRE(mode >= 0 && mode <= 2, "prism_select_tiles: mode %d unknown", mode);
+  PRISM_REQUIRE(N >= 1 && N <= 64 * kSelThreads, "prism_select_tiles: N=%lld out of range [1, %d]",
+                (long long)N, 64 * kSelThreads);
+  PRISM_REQUIRE(k_lo >= 0 && ub >= 0 && ub <= N, "prism_select_tiles: bad k/ub");
+  PRISM_REQUIRE(mode == 0 || thr > 0, "prism_select_tiles: threshold must be positive");
+  PRISM_REQUIRE(tcap >= 2 * (mode == 0 ? (k_lo < N ? k_lo : N) : ub), "prism_select_tiles: tcap too small");
+  PRISM_REQUIRE(sel_blocks == nullptr || bcap >= (mode == 0 ? (k_lo < N ? k_lo : N) : ub),
+                "prism_select_tiles: bcap too small");
+  PRISM_REQUIRE(2 * N < 65536, "prism_select_tiles: N too large for the packed scan");
+  if (rows == 0) return PRISM_OK;
+  SelArgs a;
+  a.scores = scores; a.rows = rows; a.N = N; a.mode = mode; a.k_lo = k_lo; a.ub = ub; a.scale = scale; a.thr = thr;
+  a.block_first_tile = block_first_tile; a.tile_count = tile_count; a.tcap = tcap; a.tiles = tiles;
+  a.ntiles = ntiles; a.sel_blocks = sel_blocks; a.bcap = bcap; a.nsel = nsel;
+  const int64_t need = (N + kSelThreads - 1) / kSelThreads;
+  if (need <= 8) select_kernel<8><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
+  else if (need <= 16) select_kernel<16><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
+  else if (need <= 32) select_kernel<32><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
+  else select_kernel<64><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
+  PRISM_LAUNCH_CHECK("prism_select_tiles");
+  return PRISM_OK;
+}
+
+int prism_tile_rows(const int32_t* ntiles, const int32_t* block_id_of_tile, int BH, int64_t Nt, int64_t N_b,
+                    int64_t tcap, int64_t* qstart, int32_t* qlen, hipStream_t stream) {
+  PRISM_REQUIRE(ntiles && block_id_of_tile && qstart && qlen, "prism_tile_rows: null pointer");
+  const int64_t n = (int64_t)BH * Nt;
+  if (n == 0) return PRISM_OK;
+  tile_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(ntiles, block_id_of_tile, BH, Nt, N_b, tcap,
+                                                                    qstart, qlen);
+  PRISM_LAUNCH_CHECK("prism_tile_rows");
+  return PRISM_OK;
+}
+
+int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH, int64_t Nt,
+                          uint32_t* bitmap, int64_t kcap, int64_t* kstart, int32_t* klen, int32_t* kcols,
+                          hipStream_t stream) {
+  PRISM_REQUIRE(qstart && qlen && qcols && bitmap && kstart && klen && kcols, "prism_transpose_lists: null pointer");
+  PRISM_REQUIRE(kcap >= Nt, "prism_transpose_lists: kcap must be >= N_tiles");
+  const int64_t rows = (int64_t)BH * Nt, words = (Nt + 31) / 32;
+  if (rows == 0) return PRISM_OK;
+  fill_u32_kernel<<<1024, 256, 0, stream>>>(bitmap, rows * words, 0u);
+  set_bits_kernel<<<(unsigned)rows, 64, 0, stream>>>(qstart, qlen, qcols, Nt, words, bitmap);
+  emit_bits_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, stream>>>(bitmap, rows, Nt, words, kcap, kstart, klen, kcols);
+  PRISM_LAUNCH_CHECK("prism_transpose_lists");
+  return PRISM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,174 @@
+"""Dynamic-block-shape block-sparse attention, MI355X implementation.
+
+Drop-in for hymm/models/modules/block_sparse_attention/dynamic_block_attention.py
+of the reference: ``flash_attn_bsa_3d_dynamic`` keeps its signature, return
+contract, errors and autograd behaviour (gradients flow to q, k, v only).
+
+Pipeline (all HIP kernels of libprism_bsa.so, one host sync for N_b):
+  (1) zone statistics + shape ids      prism_zone_stats / _gradient / _shapes
+  (2) zone layout (block/tile maps)    prism_zone_layout
+  (3) rearranged rows + block means    prism_gather_pool (q, k, v)
+  (4) fp32 block scores + selection    prism_block_scores, prism_select_tiles
+  (5) tile lists per query tile        prism_tile_rows
+  (6) block-sparse attention           prism_bsa_fwd / prism_bsa_bwd_*
+  (7) back to THW order                prism_scatter_rows
+Deliberate differences from the reference (documented in DESIGN.md): block
+means and scores are fp32 (the reference pools and scores in q's dtype) and
+every reduction uses one fixed order, so zone statistics, shape ids and
+selected sets are reproducible bit for bit.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import ops
+from .dynamic_block_shape import ALL_CANDIDATE_SHAPES, ZONE_SIZE, _gradient_and_shapes
+
+_TILE = 64  # kernel tile (dynamic_block_attention.py:15)
+
+
+# ------------------------------------------------------------------ geometry helpers (API parity)
+def _build_rearrange_index(shape_ids, ZT, ZH, ZW, H, W, device):
+    """src_idx[S], inv_idx[S] int64 (dynamic_block_attention.py:107-135)."""
+    return ops.rearrange_index(shape_ids.to(device), (ZT * ZONE_SIZE, H, W))
+
+
+def _build_block_tile_maps(shape_ids, ZT, ZH, ZW, device):
+    """(block_id_of_tile [N_tiles], kblock_tiles [N_b+1, 2], N_b, N_tiles)
+    (dynamic_block_attention.py:138-170)."""
+    lay = ops.ZoneLayout(shape_ids.to(device), (ZT * ZONE_SIZE, ZH * ZONE_SIZE, ZW * ZONE_SIZE))
+    first = lay.block_first_tile[: lay.N_b + 1].to(torch.int64)
+    two = (first[1:] - first[:-1]) == 2
+    kbt = torch.full((lay.N_b + 1, 2), lay.Nt, device=device, dtype=torch.int64)
+    kbt[: lay.N_b, 0] = first[:-1]
+    kbt[: lay.N_b, 1] = torch.where(two, first[:-1] + 1, torch.full_like(first[:-1], lay.Nt))
+    return lay.block_id_of_tile.to(torch.int64), kbt, lay.N_b, lay.Nt
+
+
+# ------------------------------------------------------------------ selection (steps 3-5)
+class _Plan:
+    """Everything the attention kernels need for one call, built under no_grad."""
+
+    def __init__(self, q, k, v, grid, shape_ids, valid_mask, sparsity, cdf_threshold, sm_scale):
+        B, H, S, D = q.shape
+        self.B, self.H, self.S, self.D = B, H, S, D
+        self.grid = grid
+        self.lay = ops.ZoneLayout(shape_ids, grid)
+        lay = self.lay
+        gq = ops.gather_pool(q, lay, valid_mask, rows=True, pool=True, counts=True)
+        gk = ops.gather_pool(k, lay, valid_mask, rows=True, pool=True)
+        gv = ops.gather_pool(v, lay, valid_mask, rows=True)
+        self.q_re, self.k_re, self.v_re = gq["rows"], gk["rows"], gv["rows"]
+        self.vt = ops.transpose_tiles(self.v_re)
+        masked = valid_mask is not None
+        self.kv_valid = gq["valid_re"] if masked else None
+        self.block_count = gq["block_count"]
+        self.tile_count = gq["tile_count"]
+        scores = ops.block_scores(gq["block_mean"].view(B * H, lay.N_b, D), gk["block_mean"].view(B * H, lay.N_b, D),
+                                  self.block_count if masked else None)
+        self.scores = scores
+        sel = ops.select_tiles(scores, sparsity, cdf_threshold, sm_scale, lay.block_first_tile,
+                               self.tile_count if masked else None)
+        self.sel = sel
+        self.qstart, self.qlen = ops.tile_rows(sel["ntiles"], lay.block_id_of_tile, B * H, lay.Nt, lay.N_b,
+                                               sel["tcap"])
+        self.qcols = sel["tiles"].view(-1)
+        self.klists = None
+
+    def sum_lens(self) -> int:
+        """Executed (query tile, key tile) pairs (host sync)."""
+        return int(self.qlen.sum().item())
+
+
+class _DynBSA(torch.autograd.Function):
+    """Attention over a _Plan with gradients to the THW q, k, v
+    (_dyn_bsa_kernel, dynamic_block_attention.py:71-101, plus the autograd of
+    the gathers :250-252 and the scatter :329)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, plan: _Plan, sm_scale: float):
+        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.kv_valid, plan.qstart, plan.qlen, plan.qcols,
+                                sm_scale)
+        ctx.plan = plan
+        ctx.sm_scale = sm_scale
+        ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
+        ctx.save_for_backward(o_re, lse)
+        return ops.scatter_rows(o_re, plan.lay, q.dtype)
+
+    @staticmethod
+    def backward(ctx, do):
+        plan: _Plan = ctx.plan
+        o_re, lse = ctx.saved_tensors
+        lay = plan.lay
+        gd = ops.gather_pool(do.contiguous(), lay, None, rows=True, dot_with=o_re)
+        do_re, delta = gd["rows"], gd["rowdot"]
+        dot = ops.transpose_tiles(do_re)
+        qt = ops.transpose_tiles(plan.q_re)
+        kt = ops.transpose_tiles(plan.k_re)
+        if plan.klists is None:
+            plan.klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, plan.B * plan.H, lay.Nt)
+        dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, qt, plan.k_re, kt, plan.v_re, do_re, dot, lse, delta,
+                                          plan.kv_valid, (plan.qstart, plan.qlen, plan.qcols), plan.klists,
+                                          ctx.sm_scale)
+        tq, tk, tv = ctx.in_dtypes
+        dq = ops.scatter_rows(dq_re, lay, tq)
+        dk = ops.scatter_rows(dk_re, lay, tk)
+        dv = ops.scatter_rows(dv_re, lay, tv)
+        return dq, dk, dv, None, None
+
+
+def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold=None, audio_token_norms=None,
+                 valid_mask=None, lambda_a=0.5, tau_128=0.15, lambda_128=1.0, shape_ids=None) -> _Plan:
+    """Steps (1)-(5) of flash_attn_bsa_3d_dynamic: shape ids, layout, pooled
+    scores, selection and tile lists (no attention)."""
+    B, Hn, S, D = q.shape
+    T, H, W = grid_padded
+    assert T * H * W == S
+    assert T % ZONE_SIZE == 0 and H % ZONE_SIZE == 0 and W % ZONE_SIZE == 0
+    if sparsity is None and cdf_threshold is None:
+        raise ValueError("Either sparsity or cdf_threshold must be provided")
+    if method not in ("ivpq", "penalty") and shape_ids is None:
+        raise ValueError(f"unknown dynamic-block method: {method!r}")
+    sm_scale = 1.0 / (D ** 0.5)
+    with torch.no_grad():
+        if shape_ids is None:
+            shape_ids = _gradient_and_shapes(v.detach(), audio_token_norms, (T, H, W), method, lambda_a, tau_128,
+                                             lambda_128, valid_mask)[2]
+        return _Plan(q.detach(), k.detach(), v.detach(), (T, H, W), shape_ids, valid_mask, sparsity, cdf_threshold,
+                     sm_scale)
+
+
+def flash_attn_bsa_3d_dynamic(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    grid_padded: Tuple[int, int, int],
+    *,
+    method: str,
+    sparsity: Optional[float] = 0.9375,
+    cdf_threshold: Optional[float] = None,
+    audio_token_norms: Optional[torch.Tensor] = None,
+    valid_mask: Optional[torch.Tensor] = None,
+    lambda_a: float = 0.5,
+    tau_128: float = 0.15,
+    lambda_128: float = 1.0,
+    shape_ids: Optional[torch.Tensor] = None,
+    return_shape_ids: bool = False,
+):
+    """Dynamic-block-shape BSA for video self-attention; returns [B,H,S,D] in
+    THW order (dynamic_block_attention.py:194-332).  q, k, v: [B,H,S,D] THW
+    order on the GPU, grid padded to multiples of 8; float32 or bfloat16
+    (attention itself runs in bf16 MFMA with fp32 accumulation)."""
+    plan = plan_dynamic(q, k, v, grid_padded, method=method, sparsity=sparsity, cdf_threshold=cdf_threshold,
+                        audio_token_norms=audio_token_norms, valid_mask=valid_mask, lambda_a=lambda_a,
+                        tau_128=tau_128, lambda_128=lambda_128, shape_ids=shape_ids)
+    sm_scale = 1.0 / (q.shape[-1] ** 0.5)
+    out = _DynBSA.apply(q, k, v, plan, sm_scale)
+    if return_shape_ids:
+        return out, plan.lay.shape_ids
+    return out
+
+
+__all__ = ["flash_attn_bsa_3d_dynamic", "plan_dynamic", "ALL_CANDIDATE_SHAPES"]

@@ -1,0 +1,320 @@
+"""Tensor-level wrappers over the prism_bsa C-ABI.
+
+PyTorch supplies device memory (the caching allocator) and the current HIP
+stream; every computation runs in libprism_bsa.so.  Inputs must be CUDA (HIP)
+tensors; they are made contiguous where the kernels need it.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+F32, BF16 = 0, 1
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise TypeError(f"prism_amd: unsupported dtype {t.dtype} (float32 or bfloat16)")
+
+
+def _cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("prism_amd: tensors must live on the GPU (no CPU path)")
+
+
+def _grid(grid) -> Tuple[int, int, int]:
+    T, H, W = (int(x) for x in grid)
+    return T, H, W
+
+
+def _u8(valid: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    if valid is None:
+        return None
+    return valid.contiguous().view(torch.uint8) if valid.dtype == torch.bool else valid.contiguous().to(torch.uint8)
+
+
+# ------------------------------------------------------------------ statistics
+def zone_stats(v: torch.Tensor, grid, valid: Optional[torch.Tensor] = None):
+    """[B,H,S,D] THW -> packed [Nz, 25D] fp32, axis_valid [Nz, 24] uint8."""
+    _cuda(v, valid)
+    v = v.contiguous()
+    B, H, S, D = v.shape
+    T, Hg, Wg = _grid(grid)
+    Nz = (T // 8) * (Hg // 8) * (Wg // 8)
+    packed = torch.empty((Nz, 25 * D), device=v.device, dtype=torch.float32)
+    av = torch.empty((Nz, 24), device=v.device, dtype=torch.uint8)
+    vm = _u8(valid)
+    _lib.call("prism_zone_stats", _p(v), _code(v), H, S, D, _p(vm), T, Hg, Wg, _p(packed), _p(av), _stream())
+    return packed, av
+
+
+def audio_zone_stats(norms: torch.Tensor, grid, valid: Optional[torch.Tensor] = None):
+    _cuda(norms, valid)
+    norms = norms.contiguous()
+    T, Hg, Wg = _grid(grid)
+    Nz = (T // 8) * (Hg // 8) * (Wg // 8)
+    abar = torch.empty(Nz, device=norms.device, dtype=torch.float32)
+    vhat = torch.empty((Nz, 3), device=norms.device, dtype=torch.float32)
+    vm = _u8(valid)
+    _lib.call("prism_audio_zone_stats", _p(norms), _code(norms), _p(vm), T, Hg, Wg, _p(abar), _p(vhat), _stream())
+    return abar, vhat
+
+
+def zone_gradient(packed: torch.Tensor, axis_valid: torch.Tensor, D: int):
+    _cuda(packed, axis_valid)
+    Nz = packed.shape[0]
+    rho_raw = torch.empty(Nz, device=packed.device, dtype=torch.float32)
+    aniso = torch.empty((Nz, 3), device=packed.device, dtype=torch.float32)
+    _lib.call("prism_zone_gradient", _p(packed.contiguous()), _p(axis_valid.contiguous()), Nz, D, _p(rho_raw),
+              _p(aniso), _stream())
+    return rho_raw, aniso
+
+
+def zone_shapes(rho_raw, aniso, abar, vhat, method: str, lambda_a: float, tau_128: float, lambda_128: float):
+    if method not in ("ivpq", "penalty"):
+        raise ValueError(f"unknown dynamic-block method: {method!r}")
+    _cuda(rho_raw, aniso, abar, vhat)
+    Nz = rho_raw.shape[0]
+    dev = rho_raw.device
+    g = torch.empty((Nz, 3), device=dev, dtype=torch.float32)
+    rho = torch.empty(Nz, device=dev, dtype=torch.float32)
+    sid = torch.empty(Nz, device=dev, dtype=torch.int64)
+    _lib.call("prism_zone_shapes", _p(rho_raw), _p(aniso), _p(abar), _p(vhat), Nz, 0 if method == "ivpq" else 1,
+              float(lambda_a), float(tau_128), float(lambda_128), _p(g), _p(rho), _p(sid), _stream())
+    return g, rho, sid
+
+
+def a2v_norms(residual: torch.Tensor) -> torch.Tensor:
+    """Per-token L2 norm of batch 0: [B,S,C] (or [S,C]) -> [S] in the input dtype."""
+    _cuda(residual)
+    r = residual[0] if residual.dim() == 3 else residual
+    r = r.contiguous()
+    S, C = r.shape
+    out = torch.empty(S, device=r.device, dtype=r.dtype)
+    _lib.call("prism_a2v_norms", _p(r), _code(r), S, C, _p(out), _code(out), _stream())
+    return out
+
+
+# ------------------------------------------------------------------ geometry
+class ZoneLayout:
+    """Per-call block/tile bookkeeping for one set of shape ids."""
+
+    def __init__(self, shape_ids: torch.Tensor, grid):
+        _cuda(shape_ids)
+        self.grid = _grid(grid)
+        T, Hg, Wg = self.grid
+        self.Nz = (T // 8) * (Hg // 8) * (Wg // 8)
+        self.Nt = self.Nz * 8
+        self.S = T * Hg * Wg
+        self.shape_ids = shape_ids.contiguous().to(torch.int64)
+        dev = shape_ids.device
+        self.block_offset = torch.empty(self.Nz + 1, device=dev, dtype=torch.int32)
+        self.block_id_of_tile = torch.empty(self.Nt, device=dev, dtype=torch.int32)
+        self.block_first_tile = torch.empty(self.Nt + 1, device=dev, dtype=torch.int32)
+        _lib.call("prism_zone_layout", _p(self.shape_ids), self.Nz, _p(self.block_offset), _p(self.block_id_of_tile),
+                  _p(self.block_first_tile), _stream())
+        # the one host synchronisation of the path (the reference syncs here too,
+        # dynamic_block_attention.py:153): N_b sizes the block tensors
+        self.N_b = int(self.block_offset[self.Nz].item())
+
+
+def rearrange_index(shape_ids: torch.Tensor, grid):
+    _cuda(shape_ids)
+    T, Hg, Wg = _grid(grid)
+    S = T * Hg * Wg
+    src = torch.empty(S, device=shape_ids.device, dtype=torch.int64)
+    inv = torch.empty(S, device=shape_ids.device, dtype=torch.int64)
+    _lib.call("prism_rearrange_index", _p(shape_ids.contiguous()), T, Hg, Wg, _p(src), _p(inv), _stream())
+    return src, inv
+
+
+def gather_pool(x: torch.Tensor, lay: ZoneLayout, valid: Optional[torch.Tensor] = None, *, rows: bool = True,
+                pool: bool = False, counts: bool = False, dot_with: Optional[torch.Tensor] = None):
+    """Rearrange x [B,H,S,D] (THW) into tile order (bf16 rows) and optionally
+    pool block means / counts / rowdot with dot_with.  Returns a dict."""
+    _cuda(x, valid, dot_with)
+    x = x.contiguous()
+    B, H, S, D = x.shape
+    T, Hg, Wg = lay.grid
+    dev = x.device
+    out = {}
+    out["rows"] = torch.empty((B, H, S, D), device=dev, dtype=torch.bfloat16) if rows else None
+    out["block_mean"] = torch.empty((B, H, lay.N_b, D), device=dev, dtype=torch.float32) if pool else None
+    if counts:
+        out["block_count"] = torch.empty(lay.N_b, device=dev, dtype=torch.int32)
+        out["tile_count"] = torch.empty(lay.Nt, device=dev, dtype=torch.int32)
+        out["valid_re"] = torch.empty(S, device=dev, dtype=torch.uint8)
+    else:
+        out["block_count"] = out["tile_count"] = out["valid_re"] = None
+    rowdot = None
+    if dot_with is not None:
+        dot_with = dot_with.contiguous()
+        if dot_with.dtype != torch.bfloat16 or dot_with.shape != x.shape:
+            raise ValueError("gather_pool: dot_with must be bf16 of x's shape (tile order)")
+        rowdot = torch.empty((B, H, S), device=dev, dtype=torch.float32)
+    out["rowdot"] = rowdot
+    vm = _u8(valid)
+    _lib.call("prism_gather_pool", _p(x), _code(x), B, H, S, D, _p(vm), _p(lay.shape_ids), _p(lay.block_offset),
+              T, Hg, Wg, lay.N_b, _p(out["rows"]), _p(out["block_mean"]), _p(out["block_count"]),
+              _p(out["tile_count"]), _p(out["valid_re"]), _p(dot_with), _p(rowdot), _stream())
+    return out
+
+
+def transpose_tiles(rows: torch.Tensor) -> torch.Tensor:
+    """[B,H,S,D] bf16 tile order -> [B,H,S/64,D,64] transposed tiles."""
+    _cuda(rows)
+    rows = rows.contiguous()
+    B, H, S, D = rows.shape
+    out = torch.empty((B, H, S // 64, D, 64), device=rows.device, dtype=torch.bfloat16)
+    _lib.call("prism_transpose_tiles", _p(rows), B * H, S, D, _p(out), _stream())
+    return out
+
+
+def scatter_rows(rows: torch.Tensor, lay: ZoneLayout, out_dtype: torch.dtype) -> torch.Tensor:
+    _cuda(rows)
+    rows = rows.contiguous()
+    B, H, S, D = rows.shape
+    T, Hg, Wg = lay.grid
+    out = torch.empty((B, H, S, D), device=rows.device, dtype=out_dtype)
+    _lib.call("prism_scatter_rows", _p(rows), B, H, S, D, _p(lay.shape_ids), T, Hg, Wg, _p(out), _code(out),
+              _stream())
+    return out
+
+
+# ------------------------------------------------------------------ selection
+def block_scores(qc: torch.Tensor, kc: torch.Tensor, block_count: Optional[torch.Tensor]) -> torch.Tensor:
+    """[..., N, D] fp32 block means -> [..., N, N] fp32 scores (invalid keys -inf)."""
+    _cuda(qc, kc, block_count)
+    N, D = qc.shape[-2], qc.shape[-1]
+    BH = qc.numel() // (N * D)
+    qc = qc.contiguous().float()
+    kc = kc.contiguous().float()
+    out = torch.empty((*qc.shape[:-1], N), device=qc.device, dtype=torch.float32)
+    _lib.call("prism_block_scores", _p(qc), _p(kc), _p(block_count), BH, N, D, _p(out), _stream())
+    return out
+
+
+def cdf_threshold_fixed(p: float) -> int:
+    """Smallest X with fl32(X) * 2^-60 >= fl32(p): the fixed-point form of the
+    test "cumsum < p" (exact integer bisection on the host)."""
+    import numpy as np
+    pf = np.float32(p)
+    if not pf > 0:
+        raise ValueError("cdf_threshold must be positive")
+    lo, hi = 0, 1 << 62
+    scale = np.float32(2.0 ** -60)
+    while lo < hi:
+        mid = (lo + hi) // 2
+        if np.float32(np.uint64(mid)) * scale >= pf:
+            hi = mid
+        else:
+            lo = mid + 1
+    return lo
+
+
+def selection_params(N: int, sparsity: Optional[float], cdf_threshold: Optional[float]):
+    """(mode, k_lo, ub) exactly as bsa_interface.py:235-304 derives them."""
+    if sparsity is not None and cdf_threshold is None:
+        k = int((1 - sparsity) * N)
+        return 0, k, k
+    if sparsity is None and cdf_threshold is not None:
+        return 1, 1, min(N, int(cdf_threshold * N) + 1)
+    if sparsity is not None and cdf_threshold is not None:
+        kt = max(1, int((1 - sparsity) * N))
+        return 2, kt, min(N, max(kt, int(cdf_threshold * N) + 1))
+    raise ValueError("Either sparsity or cdf_threshold must be provided")
+
+
+def select_tiles(scores: torch.Tensor, sparsity, cdf_threshold, sm_scale: float, block_first_tile: torch.Tensor,
+                 tile_count: Optional[torch.Tensor], want_blocks: bool = False):
+    """Per-row selection + tile expansion.  scores: [..., N, N] fp32.
+    Returns dict(tiles [rows, tcap] int32, ntiles [rows], sel_blocks, nsel, tcap)."""
+    _cuda(scores, block_first_tile, tile_count)
+    N = scores.shape[-1]
+    rows = scores.numel() // N
+    mode, k_lo, ub = selection_params(N, sparsity, cdf_threshold)
+    width = min(k_lo, N) if mode == 0 else ub
+    tcap = max(2 * width, 1)
+    dev = scores.device
+    tiles = torch.empty((rows, tcap), device=dev, dtype=torch.int32)
+    ntiles = torch.empty(rows, device=dev, dtype=torch.int32)
+    sel = torch.full((rows, max(width, 1)), N, device=dev, dtype=torch.int32) if want_blocks else None
+    nsel = torch.empty(rows, device=dev, dtype=torch.int32) if want_blocks else None
+    thr = cdf_threshold_fixed(cdf_threshold) if mode != 0 else 0
+    _lib.call("prism_select_tiles", _p(scores.contiguous()), rows, N, mode, k_lo, ub, float(sm_scale), thr,
+              _p(block_first_tile), _p(tile_count), tcap, _p(tiles), _p(ntiles), _p(sel), max(width, 1), _p(nsel),
+              _stream())
+    return dict(tiles=tiles, ntiles=ntiles, sel_blocks=sel, nsel=nsel, tcap=tcap, width=width)
+
+
+def tile_rows(ntiles: torch.Tensor, block_id_of_tile: torch.Tensor, BH: int, Nt: int, N_b: int, tcap: int):
+    _cuda(ntiles, block_id_of_tile)
+    qstart = torch.empty(BH * Nt, device=ntiles.device, dtype=torch.int64)
+    qlen = torch.empty(BH * Nt, device=ntiles.device, dtype=torch.int32)
+    _lib.call("prism_tile_rows", _p(ntiles), _p(block_id_of_tile), BH, Nt, N_b, tcap, _p(qstart), _p(qlen), _stream())
+    return qstart, qlen
+
+
+def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tensor, BH: int, Nt: int):
+    """Per-query-tile key lists -> per-key-tile ascending query lists."""
+    _cuda(qstart, qlen, qcols)
+    dev = qstart.device
+    words = (Nt + 31) // 32
+    bitmap = torch.empty(BH * Nt * words, device=dev, dtype=torch.int32)
+    kstart = torch.empty(BH * Nt, device=dev, dtype=torch.int64)
+    klen = torch.empty(BH * Nt, device=dev, dtype=torch.int32)
+    kcols = torch.empty(BH * Nt * Nt, device=dev, dtype=torch.int32)
+    _lib.call("prism_transpose_lists", _p(qstart), _p(qlen), _p(qcols), BH, Nt, _p(bitmap), Nt, _p(kstart), _p(klen),
+              _p(kcols), _stream())
+    return kstart, klen, kcols
+
+
+# ------------------------------------------------------------------ attention
+def _bf16(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16 (MFMA kernels)")
+    return t.contiguous()
+
+
+def bsa_fwd(q, k, vt, kv_valid, qstart, qlen, qcols, sm_scale: float):
+    """q, k [B,H,S,D] bf16 tile order, vt [B,H,S/64,D,64] -> (o bf16, lse fp32 natural)."""
+    _cuda(q, k, vt, kv_valid, qstart, qlen, qcols)
+    q, k, vt = _bf16(q, "q"), _bf16(k, "k"), _bf16(vt, "vt")
+    B, H, S, D = q.shape
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), device=q.device, dtype=torch.float32)
+    _lib.call("prism_bsa_fwd", _p(q), _p(k), _p(vt), B * H, S, D, _p(kv_valid), _p(qstart), _p(qlen), _p(qcols),
+              float(sm_scale), _p(o), _p(lse), _stream())
+    return o, lse
+
+
+def bsa_bwd(q, qt, k, kt, v, do, dot, lse, delta, kv_valid, qlists, klists, sm_scale: float):
+    """Backward over tile-order tensors; returns dq, dk, dv (bf16, tile order)."""
+    _cuda(q, qt, k, kt, v, do, dot, lse, delta, kv_valid)
+    B, H, S, D = q.shape
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    qstart, qlen, qcols = qlists
+    kstart, klen, kcols = klists
+    s = _stream()
+    _lib.call("prism_bsa_bwd_dkdv", _p(q), _p(qt), _p(k), _p(v), _p(do), _p(dot), _p(lse), _p(delta), B * H, S, D,
+              _p(kv_valid), _p(kstart), _p(klen), _p(kcols), float(sm_scale), _p(dk), _p(dv), s)
+    _lib.call("prism_bsa_bwd_dq", _p(q), _p(k), _p(kt), _p(v), _p(do), _p(lse), _p(delta), B * H, S, D,
+              _p(kv_valid), _p(qstart), _p(qlen), _p(qcols), float(sm_scale), _p(dq), s)
+    return dq, dk, dv

@@ -1,0 +1,360 @@
+"""GPU parity: every HIP stage against the CPU oracle on identical seeded inputs.
+
+Bit-exact: zone statistics, gradients, shape ids, audio statistics, A2V norms,
+geometry, pooled block means, fp32 scores, selected sets / tile lists, list
+transpose.  Tolerance (bf16 vs float64 oracle): attention O, dQ, dK, dV with
+max-abs 2e-2 and mean-abs 2e-3.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.cases import bf16, padded_case
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(x: np.ndarray) -> torch.Tensor:
+    if x.dtype == np.uint16:
+        return torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    t = t.detach()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    if a.dtype == np.float32:
+        return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.astype(np.float32).view(np.uint32))
+    return a.shape == b.shape and np.array_equal(a, b)
+
+
+CASES = [
+    # (name, seed, B, H, grid_real, D, dtype, lowrank, audio)
+    ("c1_fp32_d64", 0, 1, 4, (4, 16, 16), 64, "f32", False, 64),
+    ("bf16_d128_lowrank", 1, 1, 3, (13, 20, 24), 128, "bf16", True, 32),
+    ("bf16_d128_nopad", 2, 2, 2, (8, 16, 16), 128, "bf16", False, 0),
+]
+
+
+def make(case):
+    name, seed, B, H, gr, D, dt, lowrank, audio = case
+    c = padded_case(seed, B, H, gr, D, lowrank=lowrank, audio_tokens=audio)
+    conv = bf16 if dt == "bf16" else (lambda x: x)
+    c["qh"], c["kh"], c["vh"] = conv(c["q"]), conv(c["k"]), conv(c["v"])
+    c["nh"] = None if c["norms"] is None else conv(c["norms"])
+    c["pad"] = tuple(gr) != tuple(c["grid"])
+    c["lowrank"] = lowrank
+    return c
+
+
+@pytest.fixture(scope="module", params=CASES, ids=[c[0] for c in CASES])
+def case(request):
+    say(request.param)
+    return make(request.param)
+
+
+def test_zone_stats_bitexact(case):
+    from prism_amd import ops
+    valid = case["valid"] if case["pad"] else None
+    p_ref, av_ref = O.zone_stats(case["vh"], case["grid"], valid)
+    p, av = ops.zone_stats(dev(case["vh"]), case["grid"], None if valid is None else dev(valid))
+    assert bits_equal(host(p), p_ref)
+    assert np.array_equal(host(av), av_ref)
+
+
+def test_zone_gradient_shapes_bitexact(case):
+    from prism_amd import ops
+    valid = case["valid"] if case["pad"] else None
+    D = case["q"].shape[-1]
+    p_ref, av_ref = O.zone_stats(case["vh"], case["grid"], valid)
+    rho_ref, an_ref = O.zone_gradient(p_ref, av_ref, D)
+    rho, an = ops.zone_gradient(dev(p_ref), dev(av_ref), D)
+    assert bits_equal(host(rho), rho_ref)
+    assert bits_equal(host(an), an_ref)
+    ab = vh = ab_d = vh_d = None
+    if case["nh"] is not None:
+        ab, vh = O.audio_zone_stats(case["nh"], case["grid"], valid)
+        ab_d, vh_d = ops.audio_zone_stats(dev(case["nh"]), case["grid"], None if valid is None else dev(valid))
+        assert bits_equal(host(ab_d), ab)
+        assert bits_equal(host(vh_d), vh)
+    for method in ("ivpq", "penalty"):
+        for tau in (0.15, 0.6, 1.5):
+            g_ref, r_ref, s_ref = O.zone_shapes(rho_ref, an_ref, ab, vh, method, 0.5, tau, 1.0)
+            g, r, s = ops.zone_shapes(dev(rho_ref), dev(an_ref), None if ab is None else dev(ab),
+                                      None if vh is None else dev(vh), method, 0.5, tau, 1.0)
+            assert bits_equal(host(g), g_ref)
+            assert bits_equal(host(r), r_ref)
+            assert np.array_equal(host(s), s_ref), (method, tau)
+
+
+def test_a2v_norms_bitexact():
+    from prism_amd import ops
+    rng = np.random.default_rng(5)
+    for S, C, dt in ((300, 256, "f32"), (257, 5120, "bf16"), (64, 3072, "bf16"), (10, 8, "f32")):
+        say("a2v", S, C, dt)
+        x = rng.standard_normal((1, S, C)).astype(np.float32)
+        xh = bf16(x) if dt == "bf16" else x
+        ref = O.a2v_norms(xh[0], dt == "bf16")
+        got = host(ops.a2v_norms(dev(xh)))
+        vt = np.uint32 if dt == "f32" else np.uint16
+        assert np.array_equal(got.view(vt), ref.view(vt))
+
+
+def _shape_ids_for(case, method="ivpq"):
+    valid = case["valid"] if case["pad"] else None
+    return O.select_zone_shapes(case["vh"], case["nh"], case["grid"], method, 0.5, 0.15, 1.0, valid)
+
+
+def test_layout_and_rearrange(case):
+    from prism_amd import ops
+    sid = _shape_ids_for(case)
+    # exercise every candidate shape as well
+    sid_all = np.arange(len(sid)) % 13
+    for s in (sid, sid_all):
+        src_ref, inv_ref = O.rearrange_index(s, case["grid"])
+        src, inv = ops.rearrange_index(dev(s), case["grid"])
+        assert np.array_equal(host(src), src_ref) and np.array_equal(host(inv), inv_ref)
+        bot, kbt, nb, boff = O.tile_maps(s)
+        lay = ops.ZoneLayout(dev(s), case["grid"])
+        assert lay.N_b == nb
+        assert np.array_equal(host(lay.block_id_of_tile), bot)
+        assert np.array_equal(host(lay.block_offset)[:-1], boff)
+        first = host(lay.block_first_tile)[: nb + 1]
+        assert np.array_equal(first[:-1], kbt[:nb, 0]) and first[-1] == len(bot)
+
+
+def test_gather_pool_bitexact(case):
+    from prism_amd import ops
+    sid = np.arange(case["grid"][0] // 8 * case["grid"][1] // 8 * case["grid"][2] // 8) % 13
+    valid = case["valid"] if case["pad"] else None
+    lay = ops.ZoneLayout(dev(sid), case["grid"])
+    vd = None if valid is None else dev(valid)
+    for name in ("qh", "kh"):
+        x = case[name]
+        ref, bc, tc = O.block_pool(x, sid, case["grid"], valid)
+        g = ops.gather_pool(dev(x), lay, vd, rows=True, pool=True, counts=True)
+        assert bits_equal(host(g["block_mean"]), ref)
+        assert np.array_equal(host(g["block_count"]), bc)
+        assert np.array_equal(host(g["tile_count"]), tc)
+        src, _ = O.rearrange_index(sid, case["grid"])
+        xf = x if x.dtype == np.uint16 else bf16(x)
+        assert np.array_equal(host(g["rows"]), xf[:, :, src])
+        vre = np.ones(len(src), np.uint8) if valid is None else valid[src]
+        assert np.array_equal(host(g["valid_re"]), vre)
+        t = host(ops.transpose_tiles(g["rows"]))
+        B, H, S, D = x.shape
+        exp = xf[:, :, src].reshape(B, H, S // 64, 64, D).transpose(0, 1, 2, 4, 3)
+        assert np.array_equal(t, exp)
+
+
+def test_scores_bitexact():
+    from prism_amd import ops
+    rng = np.random.default_rng(7)
+    for BH, N, D in ((2, 200, 64), (1, 333, 128), (3, 128, 128)):
+        say("scores", BH, N, D)
+        qc = rng.standard_normal((BH, N, D)).astype(np.float32)
+        kc = rng.standard_normal((BH, N, D)).astype(np.float32)
+        bc = (rng.random(N) > 0.1).astype(np.int32)
+        ref = O.block_scores(qc, kc, bc)
+        got = host(ops.block_scores(dev(qc), dev(kc), dev(bc)))
+        assert bits_equal(got, ref)
+
+
+def _random_scores(rng, rows, N, kind):
+    s = rng.standard_normal((rows, N)).astype(np.float32) * 3
+    if kind == "ties":
+        s = np.round(s * 2) / 2
+    if kind == "neginf":
+        s[:, rng.random(N) < 0.2] = -np.inf
+    if kind == "peaked":
+        s[:, : N // 10] += 8
+    return s
+
+
+@pytest.mark.parametrize("kind", ["plain", "ties", "neginf", "peaked"])
+def test_select_bitexact(kind):
+    from prism_amd import ops
+    rng = np.random.default_rng(11)
+    for N in (37, 300, 1440, 2900):
+        rows = 24
+        s = _random_scores(rng, rows, N, kind)
+        first = np.arange(N + 1, dtype=np.int32)
+        for sp, p in ((0.9, None), (None, 0.9), (1 - 5.5 / N, 0.9), (0.5, 0.3), (None, 0.2)):
+            say("select", kind, N, sp, p)
+            ref_sel, ref_n = O.select(s, sp, p, 0.125)
+            res = ops.select_tiles(dev(s), sp, p, 0.125, dev(first), None, want_blocks=True)
+            n = host(res["nsel"])
+            assert np.array_equal(n, ref_n), (kind, N, sp, p)
+            got = host(res["sel_blocks"])
+            for r in range(rows):
+                assert np.array_equal(got[r, : n[r]], ref_sel[r, : n[r]]), (kind, N, sp, p, r)
+
+
+def test_select_tile_expansion_bitexact(case):
+    from prism_amd import ops
+    sid = _shape_ids_for(case)
+    valid = case["valid"] if case["pad"] else None
+    r = O.select_pipeline(case["qh"], case["kh"], case["vh"], case["grid"], sparsity=0.75, cdf_threshold_p=0.9,
+                          audio_norms=case["nh"], valid=valid, shape_ids=sid)
+    lay = ops.ZoneLayout(dev(sid), case["grid"])
+    res = ops.select_tiles(dev(r["scores"]), 0.75, 0.9, 1 / math.sqrt(case["q"].shape[-1]), lay.block_first_tile,
+                           None if valid is None else dev(r["tile_count"]))
+    nt = host(res["ntiles"])
+    assert np.array_equal(nt, r["ntiles"])
+    tiles = host(res["tiles"])
+    for i in range(len(nt)):
+        assert np.array_equal(tiles[i, : nt[i]], r["tiles"][i, : nt[i]])
+
+
+def test_full_selection_pipeline_bitexact(case):
+    """plan_dynamic (stats -> shapes -> pooling -> scores -> selection) vs the
+    oracle pipeline on the same inputs."""
+    from prism_amd import plan_dynamic
+    valid = case["valid"] if case["pad"] else None
+    D = case["q"].shape[-1]
+    for method, sp, p in (("ivpq", 0.75, 0.9), ("penalty", 0.5, None), ("ivpq", None, 0.5)):
+        say("pipeline", method, sp, p)
+        ref = O.select_pipeline(case["qh"], case["kh"], case["vh"], case["grid"], method=method, sparsity=sp,
+                                cdf_threshold_p=p, audio_norms=case["nh"], valid=valid)
+        plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method=method,
+                            sparsity=sp, cdf_threshold=p,
+                            audio_token_norms=None if case["nh"] is None else dev(case["nh"]),
+                            valid_mask=None if valid is None else dev(valid).bool())
+        assert np.array_equal(host(plan.lay.shape_ids), ref["shape_ids"])
+        assert bits_equal(host(plan.scores).reshape(ref["scores"].shape), ref["scores"])
+        qlen = host(plan.qlen)
+        assert np.array_equal(qlen, ref["qlen"])
+        qs, qc = host(plan.qstart), host(plan.qcols)
+        for i in range(len(qlen)):
+            assert np.array_equal(qc[qs[i]: qs[i] + qlen[i]], ref["qcols"][ref["qstart"][i]: ref["qstart"][i] + qlen[i]])
+        assert D in (64, 128)
+
+
+def test_transpose_lists_bitexact(case):
+    from prism_amd import ops, plan_dynamic
+    valid = case["valid"] if case["pad"] else None
+    plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
+                        sparsity=0.7, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
+    BH = plan.B * plan.H
+    Nt = plan.lay.Nt
+    ks, kl, kc = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, BH, Nt)
+    ref_c, ref_l = O.transpose_lists(host(plan.qstart), host(plan.qlen), host(plan.qcols), BH, Nt)
+    kl = host(kl)
+    assert np.array_equal(kl, ref_l)
+    kc = host(kc).reshape(BH * Nt, Nt)
+    for i in range(BH * Nt):
+        assert np.array_equal(kc[i, : kl[i]], ref_c[i, : kl[i]])
+
+
+def _tol(got, ref, what):
+    """max-abs 2e-2, mean-abs 2e-3 (bf16 vs float64)."""
+    err = np.abs(got.astype(np.float64) - ref)
+    mx, mean = float(err.max()), float(err.mean())
+    say(what, "max-abs", mx, "mean-abs", mean)
+    assert mx <= 2e-2 and mean <= 2e-3, (what, mx, mean)
+
+
+def test_attention_fwd_bwd_tolerance(case):
+    """O, LSE, dQ, dK, dV of the MFMA kernels vs the float64 oracle on the
+    same bf16 tile-order inputs and the same lists."""
+    from prism_amd import ops, plan_dynamic
+    valid = case["valid"] if case["pad"] else None
+    B, H, S, D = case["q"].shape
+    sm = 1 / math.sqrt(D)
+    plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
+                        sparsity=0.6, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
+    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.kv_valid, plan.qstart, plan.qlen, plan.qcols, sm)
+    qf = O.bf16_bits_to_f32(host(plan.q_re)).reshape(B * H, S, D)
+    kf = O.bf16_bits_to_f32(host(plan.k_re)).reshape(B * H, S, D)
+    vf = O.bf16_bits_to_f32(host(plan.v_re)).reshape(B * H, S, D)
+    kv = None if plan.kv_valid is None else host(plan.kv_valid)
+    lists = (host(plan.qstart), host(plan.qlen), host(plan.qcols))
+    o_ref, lse_ref = O.attn_fwd(qf, kf, vf, *lists, kv, sm)
+    og = O.bf16_bits_to_f32(host(o)).reshape(B * H, S, D)
+    _tol(og, o_ref, "O")
+    lg = host(lse).reshape(B * H, S)
+    fin = np.isfinite(lse_ref)
+    assert np.array_equal(np.isfinite(lg), fin)
+    assert np.abs(lg[fin] - lse_ref[fin]).max() < 1e-3
+    # backward with a seeded dO
+    rng = np.random.default_rng(99)
+    do = bf16(rng.standard_normal((B, H, S, D)).astype(np.float32))
+    do_t = dev(do)
+    delta = torch.empty((B, H, S), device=DEV, dtype=torch.float32)
+    ops._lib.call("prism_bwd_preprocess", o.data_ptr(), do_t.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
+    klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, plan.lay.Nt)
+    dq, dk, dv = ops.bsa_bwd(plan.q_re, ops.transpose_tiles(plan.q_re), plan.k_re, ops.transpose_tiles(plan.k_re),
+                             plan.v_re, do_t, ops.transpose_tiles(do_t), lse, delta, plan.kv_valid,
+                             (plan.qstart, plan.qlen, plan.qcols), klists, sm)
+    dof = O.bf16_bits_to_f32(do).reshape(B * H, S, D)
+    dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, og, dof, lse_ref, *lists, kv, sm)
+    for name, g, r in (("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+        _tol(O.bf16_bits_to_f32(host(g)).reshape(B * H, S, D), r, name)
+
+
+def test_end_to_end_autograd(case):
+    """flash_attn_bsa_3d_dynamic forward + backward through autograd in THW
+    order vs the oracle attention on the oracle's own selection."""
+    from prism_amd import flash_attn_bsa_3d_dynamic
+    valid = case["valid"] if case["pad"] else None
+    B, H, S, D = case["q"].shape
+    sm = 1 / math.sqrt(D)
+    ref = O.select_pipeline(case["qh"], case["kh"], case["vh"], case["grid"], method="ivpq", sparsity=0.7,
+                            cdf_threshold_p=0.9, audio_norms=case["nh"], valid=valid)
+    src, inv = O.rearrange_index(ref["shape_ids"], case["grid"])
+    tof = (lambda a: O.bf16_bits_to_f32(a)) if case["qh"].dtype == np.uint16 else (lambda a: O.bf16_bits_to_f32(bf16(a)))
+    qf, kf, vf = (tof(case[n])[:, :, src].reshape(B * H, S, D) for n in ("qh", "kh", "vh"))
+    kv = None if valid is None else valid[src]
+    o_ref, lse_ref = O.attn_fwd(qf, kf, vf, ref["qstart"], ref["qlen"], ref["qcols"], kv, sm)
+    tdt = torch.bfloat16 if case["qh"].dtype == np.uint16 else torch.float32
+    q, k, v = (dev(case[n]).requires_grad_(True) for n in ("qh", "kh", "vh"))
+    out, sid = flash_attn_bsa_3d_dynamic(q, k, v, case["grid"], method="ivpq", sparsity=0.7, cdf_threshold=0.9,
+                                         audio_token_norms=None if case["nh"] is None else dev(case["nh"]),
+                                         valid_mask=None if valid is None else dev(valid).bool(),
+                                         return_shape_ids=True)
+    assert out.dtype == tdt
+    assert np.array_equal(host(sid), ref["shape_ids"])
+    og = out.detach().float().cpu().numpy().reshape(B * H, S, D)
+    _tol(og, o_ref[:, inv], "O(THW)")
+    rng = np.random.default_rng(3)
+    do = rng.standard_normal((B, H, S, D)).astype(np.float32)
+    do_q = O.bf16_bits_to_f32(bf16(do))
+    out.backward(torch.from_numpy(do_q).to(DEV).to(tdt))
+    o_bf = O.bf16_bits_to_f32(bf16(o_ref.astype(np.float32)))
+    dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, o_bf, do_q.reshape(B * H, S, D)[:, src], lse_ref, ref["qstart"],
+                                  ref["qlen"], ref["qcols"], kv, sm)
+    for name, t, r in (("dQ", q, dq_r), ("dK", k, dk_r), ("dV", v, dv_r)):
+        _tol(t.grad.float().cpu().numpy().reshape(B * H, S, D), r[:, inv], name + "(THW)")
+
+
+def test_determinism(case):
+    """Two identical calls give bit-identical outputs and gradients."""
+    from prism_amd import flash_attn_bsa_3d_dynamic
+    valid = case["valid"] if case["pad"] else None
+    outs = []
+    for _ in range(2):
+        q, k, v = (dev(case[n]).requires_grad_(True) for n in ("qh", "kh", "vh"))
+        o = flash_attn_bsa_3d_dynamic(q, k, v, case["grid"], method="penalty", sparsity=0.5, cdf_threshold=0.9,
+                                      valid_mask=None if valid is None else dev(valid).bool())
+        o.backward(torch.ones_like(o))
+        outs.append([host(o), host(q.grad), host(k.grad), host(v.grad)])
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
