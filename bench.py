@@ -28,10 +28,10 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 
 CONFIGS = {
-    # name: (B, H, D, grid_real, audio_tokens, C, topk, cdf, sparsity_only, struct_scale)
-    "c4": (1, 5, 128, (21, 90, 160), 2000, 5120, 48, 0.9, None, 2.0),
-    "c3": (1, 24, 128, (21, 68, 120), 2000, 3072, 32, 0.9, None, 2.0),
-    "c2": (1, 24, 128, (21, 45, 80), 2000, 3072, None, None, 0.75, 2.0),
+    # name: (B, H, D, grid_real, audio_tokens, C, topk, cdf, sparsity_only, struct_scale, field_amp, field_ell)
+    "c4": (1, 5, 128, (21, 90, 160), 2000, 5120, 48, 0.9, None, 2.0, 2.65, 16.0),
+    "c3": (1, 24, 128, (21, 68, 120), 2000, 3072, 32, 0.9, None, 2.0, 2.65, 16.0),
+    "c2": (1, 24, 128, (21, 45, 80), 2000, 3072, None, None, 0.75, 2.0, 2.65, 16.0),
 }
 
 
@@ -68,27 +68,55 @@ def lowrank_zone_field(gen, H, grid_pad, D, rank, scale, device):
     return out
 
 
-def make_inputs(cfg_name, seed=0, device="cuda"):
+def shared_field(gen, grid_pad, D, ell, device):
+    """Random Fourier features F [T*Hg*Wg, D] of the token coordinates with a
+    Gaussian kernel of length scale `ell` tokens, F(x).F(x') ~ D exp(-|x-x'|^2 /
+    (2 ell^2)).  Added to both q and k of a head, it makes block scores decay
+    with distance, so the hybrid selection keeps a local neighbourhood (the
+    amplitude sets the realized density)."""
     import torch
-    B, H, D, grid, audio, C, topk, cdf, sp_only, scale = CONFIGS[cfg_name]
+    T, Hg, Wg = grid_pad
+    om = torch.randn(D, 3, generator=gen, device=device) / ell
+    ph = 2 * math.pi * torch.rand(D, generator=gen, device=device)
+    R = torch.linalg.qr(torch.randn(D, D, generator=gen, device=device))[0]
+    t = torch.arange(T, device=device, dtype=torch.float32)
+    h = torch.arange(Hg, device=device, dtype=torch.float32)
+    w = torch.arange(Wg, device=device, dtype=torch.float32)
+    arg = t[:, None, None, None] * om[:, 0] + h[None, :, None, None] * om[:, 1] + w[None, None, :, None] * om[:, 2] + ph
+    return (math.sqrt(2.0) * torch.cos(arg)).reshape(-1, D) @ R.T.contiguous()
+
+
+def make_inputs(cfg_name, seed=0, device="cuda"):
+    """Seeded synthetic inputs of a BASELINE config: q, k, v [B,H,S,D] bf16 THW
+    order (noise + per-zone rank-8 structure; q and k also share a per-head
+    smooth field), the A2V bridge residual [B,S,C] bf16 with audio coupling in
+    ~10% of the zones, and dO."""
+    import torch
+    B, H, D, grid, audio, C, topk, cdf, sp_only, scale, famp, fell = CONFIGS[cfg_name]
     T, Hg, Wg = grid
     gp = tuple((x + 7) // 8 * 8 for x in grid)
     gen = torch.Generator(device=device).manual_seed(seed)
-    qkv = []
-    for _ in range(3):
-        field = lowrank_zone_field(gen, H, gp, D, 8, scale, device)[:, :T, :Hg, :Wg]
-        x = torch.randn((B, H, T, Hg, Wg, D), generator=gen, device=device) + field[None]
-        x = x / x.std()  # unit marginal variance; the structure keeps its scale relative to the noise
-        qkv.append(x.reshape(B, H, T * Hg * Wg, D).to(torch.bfloat16).contiguous())
-        del field, x
-    # A2V bridge residual [B, S, C]: audio coupling concentrated in ~10% of zones
     S = T * Hg * Wg
+    fields = torch.stack([shared_field(gen, gp, D, fell, device).view(*gp, D)[:T, :Hg, :Wg].reshape(S, D)
+                          for _ in range(H)])
+    qkv = []
+    for i in range(3):
+        low = lowrank_zone_field(gen, H, gp, D, 8, scale, device)[:, :T, :Hg, :Wg].reshape(H, S, D)
+        x = torch.randn((B, H, S, D), generator=gen, device=device) + low[None]
+        if i < 2:
+            x += famp * fields[None]
+        x = x / x.std()  # unit marginal variance; the structure keeps its scale relative to the noise
+        qkv.append(x.to(torch.bfloat16).contiguous())
+        del low, x
+    del fields
+    # A2V bridge residual [B, S, C]: audio coupling concentrated in ~10% of zones
     zone_amp = torch.zeros(gp[0] // 8, gp[1] // 8, gp[2] // 8, device=device)
     zone_amp.view(-1)[torch.randperm(zone_amp.numel(), generator=gen, device=device)[: max(1, zone_amp.numel() // 10)]] = 2.0
     amp = zone_amp.repeat_interleave(8, 0).repeat_interleave(8, 1).repeat_interleave(8, 2)[:T, :Hg, :Wg].reshape(S, 1)
     res = (torch.randn((B, S, C), generator=gen, device=device, dtype=torch.bfloat16) * (1.0 + amp).to(torch.bfloat16))
     do = torch.randn((B, H, S, D), generator=gen, device=device).to(torch.bfloat16)
-    torch.cuda.synchronize()
+    if str(device).startswith("cuda"):
+        torch.cuda.synchronize()
     return dict(q=qkv[0], k=qkv[1], v=qkv[2], res=res, do=do, grid=grid, grid_pad=gp, topk=topk, cdf=cdf,
                 sp_only=sp_only, B=B, H=H, D=D, S=S)
 
