@@ -139,22 +139,6 @@ def time_region(fn, steps, warmup):
     return st.elapsed_time(en) / steps, wall / steps * 1e3
 
 
-def kernel_ms(fn, reps=5):
-    """Average duration of the kernels `fn` launches on the current stream,
-    bracketed by HIP events on that stream."""
-    import torch
-    fn()
-    torch.cuda.synchronize()
-    st = torch.cuda.Event(enable_timing=True)
-    en = torch.cuda.Event(enable_timing=True)
-    st.record()
-    for _ in range(reps):
-        fn()
-    en.record()
-    torch.cuda.synchronize()
-    return st.elapsed_time(en) / reps
-
-
 # ------------------------------------------------------------------ CPU baseline (oracle)
 def cpu_baseline(plan, inp, budget_s=12.0):
     """float64 numpy oracle attention fwd+bwd on a seeded sample of query
@@ -261,72 +245,66 @@ def main():
         out = dyn(q, k, v, grid, norms)
         out.backward(do)
 
-    log("[bench] timing full step")
-    ms, wall_ms = time_region(step, args.steps, args.warmup)
+    log("[bench] warmup")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log("[bench] timed steps")
+    # timed region: every C-ABI launch is bracketed by HIP events on its stream
+    with ops.kernel_timing() as tm:
+        st = torch.cuda.Event(enable_timing=True)
+        en = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        st.record()
+        for _ in range(args.steps):
+            step()
+        en.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    ms = st.elapsed_time(en) / args.steps
+    kt = ops.summarize(tm)  # name -> (launches, average ms per launch)
 
-    # plan (selection) on the same inputs for density / per-kernel timing
+    # the plan of these inputs (deterministic: identical to the one inside each step)
     with torch.no_grad():
         plan = plan_dynamic(pad(q.detach()), pad(k.detach()), pad(v.detach()), gp, method="ivpq", sparsity=sparsity,
                             cdf_threshold=cdf, audio_token_norms=npad, valid_mask=vm)
     sum_lens = plan.sum_lens()
-    Nt = plan.lay.Nt
+    Nt, Nb, Sp = plan.lay.Nt, plan.lay.N_b, plan.S
     density = sum_lens / (B * H * Nt * Nt)
-    kept_flops = 14 * 64 * 64 * D * sum_lens
-    sm = 1 / math.sqrt(D)
+    fl = 64 * 64 * D * sum_lens  # one 64x64xD product over all kept tile pairs
+    kept_flops = 14 * fl          # FA convention: fwd 4, bwd 10
 
-    # per-kernel durations (HIP events on the launch stream)
-    log("[bench] per-kernel timing")
-    with torch.no_grad():
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.kv_valid, plan.qstart, plan.qlen, plan.qcols, sm)
-        do_pad = pad(do)
-        gd = ops.gather_pool(do_pad, plan.lay, None, rows=True, dot_with=o_re)
-        do_re, delta = gd["rows"], gd["rowdot"]
-        dot, qt, kt = ops.transpose_tiles(do_re), ops.transpose_tiles(plan.q_re), ops.transpose_tiles(plan.k_re)
-        klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, Nt)
-        t_fwd = kernel_ms(lambda: ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.kv_valid, plan.qstart, plan.qlen,
-                                              plan.qcols, sm))
-        dq = torch.empty_like(plan.q_re); dk = torch.empty_like(plan.k_re); dv = torch.empty_like(plan.v_re)
-        s_ = ops._stream()
-        P = lambda t: None if t is None else t.data_ptr()
-        t_dkdv = kernel_ms(lambda: ops._lib.call(
-            "prism_bsa_bwd_dkdv", P(plan.q_re), P(qt), P(plan.k_re), P(plan.v_re), P(do_re), P(dot), P(lse), P(delta),
-            B * H, plan.S, D, P(plan.kv_valid), P(klists[0]), P(klists[1]), P(klists[2]), sm, P(dk), P(dv), s_))
-        t_dq = kernel_ms(lambda: ops._lib.call(
-            "prism_bsa_bwd_dq", P(plan.q_re), P(plan.k_re), P(kt), P(plan.v_re), P(do_re), P(lse), P(delta), B * H,
-            plan.S, D, P(plan.kv_valid), P(plan.qstart), P(plan.qlen), P(plan.qcols), sm, P(dq), s_))
-        # selection-side kernels
-        t_stats = kernel_ms(lambda: ops.zone_stats(pad(v.detach()), gp, vm))
-        t_norms = kernel_ms(lambda: a2v_token_norms(inp["res"]))
-        t_gather = kernel_ms(lambda: ops.gather_pool(pad(q.detach()), plan.lay, vm, rows=True, pool=True))
-        qm = ops.gather_pool(pad(q.detach()), plan.lay, vm, rows=False, pool=True)["block_mean"]
-        km = ops.gather_pool(pad(k.detach()), plan.lay, vm, rows=False, pool=True)["block_mean"]
-        Nb = plan.lay.N_b
-        t_scores = kernel_ms(lambda: ops.block_scores(qm.view(B * H, Nb, D), km.view(B * H, Nb, D), plan.block_count))
-        t_select = kernel_ms(lambda: ops.select_tiles(plan.scores, sparsity, cdf, sm, plan.lay.block_first_tile,
-                                                      plan.tile_count))
-    fl = 64 * 64 * D * sum_lens
-    kern = {"bsa_fwd": (t_fwd, 4 * fl), "bsa_bwd_dkdv": (t_dkdv, 8 * fl), "bsa_bwd_dq": (t_dq, 6 * fl)}
-    dom = max(kern, key=lambda n: kern[n][0])
-    dom_ms, dom_fl = kern[dom]
-    att_ms = t_fwd + t_dkdv + t_dq
-    roof = {"kernel": dom, "bound": "mfma", "achieved": dom_fl / (dom_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "traffic": None}
-    roof["frac"] = roof["achieved"] / roof["peak"]
-    hbm = {
-        "zone_stats": (t_stats, B * H * S * D * 2 + plan.lay.Nz * 25 * D * 4),
-        "a2v_norms": (t_norms, S * inp["res"].shape[-1] * 2 + S * 2),
-        "select": (t_select, B * H * plan.lay.N_b ** 2 * 4 + 4 * int(plan.sel["ntiles"].sum().item())),
+    # attention kernels: algorithmic FLOPs per launch (executed in parentheses)
+    attn = {"prism_bsa_fwd": (4 * fl, 4 * fl), "prism_bsa_bwd_dkdv": (8 * fl, 8 * fl),
+            "prism_bsa_bwd_dq": (2 * fl, 6 * fl)}
+    X = B * H * Sp * D * 2  # one bf16 [B,H,S_p,D] tensor
+    nnz_tiles = int(plan.sel["ntiles"].sum().item())
+    hbm = {  # algorithmic bytes per launch (average over the step's launches of that entry point)
+        "prism_zone_stats": H * Sp * D * 2 + plan.lay.Nz * 25 * D * 4,
+        "prism_a2v_norms": S * inp["res"].shape[-1] * 2 + S * 2,
+        "prism_gather_pool": (4 * 2 * X + X) / 4,  # q, k, v, dO: read + write rows; dO also reads O
+        "prism_transpose_tiles": 2 * X,
+        "prism_scatter_rows": 2 * X,
+        "prism_block_scores": 2 * B * H * Nb * D * 4 + B * H * Nb * Nb * 4,
+        "prism_select_tiles": B * H * Nb * Nb * 4 + 4 * nnz_tiles + 4 * B * H * Nb,
     }
-    breakdown = {n: {"ms": round(t, 4), "tflops": round(f / (t * 1e-3) / 1e12, 1),
-                     "mfma_util": round(f / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)} for n, (t, f) in kern.items()}
-    for n, (t, b) in hbm.items():
-        breakdown[n] = {"ms": round(t, 4), "GBps": round(b / (t * 1e-3) / 1e9, 1),
-                        "hbm_frac": round(b / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-    breakdown["gather_pool_q"] = {"ms": round(t_gather, 4)}
-    breakdown["block_scores"] = {"ms": round(t_scores, 4), "tflops_fp32": round(
-        2 * B * H * plan.lay.N_b ** 2 * D / (t_scores * 1e-3) / 1e12, 2)}
-    breakdown["attention_total"] = {"ms": round(att_ms, 3), "mfma_util_kept_10x": round(
-        (14 * fl) / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    breakdown = {}
+    for name, (n, t) in sorted(kt.items(), key=lambda x: -x[1][0] * x[1][1]):
+        e = {"launches_per_step": n // args.steps, "ms": round(t, 4)}
+        if name in attn:
+            alg, exe = attn[name]
+            e.update(tflops=round(alg / (t * 1e-3) / 1e12, 1), executed_tflops=round(exe / (t * 1e-3) / 1e12, 1),
+                     mfma_frac=round(alg / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+        elif name in hbm:
+            e.update(GBps=round(hbm[name] / (t * 1e-3) / 1e9, 1),
+                     hbm_frac=round(hbm[name] / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
+        breakdown[name] = e
+    dom = max((n for n in kt if n in attn), key=lambda n: kt[n][1])
+    dom_ms = kt[dom][1]
+    roof = {"kernel": dom, "bound": "mfma", "achieved": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12, 2),
+            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "traffic": None}
+    att_ms = sum(kt[n][1] for n in attn if n in kt)
 
     dense = None
     if not args.no_dense:
@@ -362,8 +340,10 @@ def main():
         "config": {"workload": f"{args.config}: BASELINE config {'4 (2K fwd+bwd)' if args.config == 'c4' else args.config}",
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(gp),
                    "audio_tokens": CONFIGS[args.config][4], "topk": inp["topk"], "cdf_threshold": cdf,
-                   "sparsity": sparsity, "N_b": plan.lay.N_b, "sum_lens": sum_lens, "density": round(density, 4),
-                   "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3)},
+                   "sparsity": sparsity, "N_b": Nb, "sum_lens": sum_lens, "density": round(density, 4),
+                   "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3),
+                   "attention_ms": round(att_ms, 3),
+                   "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "dense": dense, "breakdown": breakdown,
     }
     print(json.dumps(rec), flush=True)

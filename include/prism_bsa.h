@@ -105,7 +105,10 @@ int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, 
 
 /* Transposed 64-row tiles: in [BH,S,D] bf16 -> out [BH,S/64,D,64] bf16 (the
  * operand layout of the MFMA kernels for V in the forward and Q, K, dO in the
- * backward; no reference counterpart, the Triton kernels transpose in SRAM). */
+ * backward; no reference counterpart, the Triton kernels transpose in SRAM).
+ * Inside each group of 16 positions of an output row, position j holds key
+ * 4*(j/8) + j%4 + 8*((j/4)%2) of the group (the k-slot order of
+ * v_mfma_f32_32x32x16_bf16 operands built from a 32x32 accumulator). */
 int prism_transpose_tiles(const void* in_rows, int BH, int64_t S, int D, void* out_t, hipStream_t stream);
 
 /* o_re.index_select(2, inv_idx) (dynamic_block_attention.py:329): tile-order
@@ -153,7 +156,9 @@ int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int3
 
 /* attn_fwd_bsa_varlen_triton (bsa_interface.py:328-385) with
  * _attn_fwd_bsa_varlen_align (flash_attn_bsa_varlen_mask.py:191-319), chunk 64.
- * q, k: [BH,S,D] bf16 tile order; vt: [BH,S/64,D,64] bf16 transposed tiles;
+ * S must be a multiple of 128 (query tiles are processed in pairs).
+ * q, k: [BH,S,D] bf16 tile order; vt: [BH,S/64,D,64] bf16 transposed tiles
+ * (prism_transpose_tiles); key tile lists ascending;
  * kv_valid: [S] uint8 or NULL; per query tile row bh*Nt + t the key tiles
  * qcols[qstart[row] .. + qlen[row]).  o: [BH,S,D] bf16; lse: [BH,S] fp32
  * natural log (-inf for rows without a valid key; their o is 0). */

@@ -108,7 +108,7 @@ def attn_bwd_bsa_varlen(do, q, k, v, o, dq, dk, dv, sm_scale, lse, block_indices
     do = do.to(torch.bfloat16).contiguous()
     o = o.to(torch.bfloat16).contiguous()
     delta = torch.empty((B, H, S), device=q.device, dtype=torch.float32)
-    ops._lib.call("prism_bwd_preprocess", o.data_ptr(), do.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
+    ops._call("prism_bwd_preprocess", o.data_ptr(), do.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
     klists = ops.transpose_lists(qstart, qlen, qcols, B * H, Nt)
     kv = ops._u8(kv_valid_mask)
     g_q, g_k, g_v = ops.bsa_bwd(q, ops.transpose_tiles(q), k, ops.transpose_tiles(k), v, do, ops.transpose_tiles(do),

@@ -17,6 +17,7 @@
 // tile t = position / 64.  Block means are fp32 sums over the block's valid
 // tokens in rearranged order (sequential per channel), divided by max(count, 1).
 #include "common.h"
+#include "mfma.h"
 
 namespace {
 
@@ -183,7 +184,9 @@ __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs 
   }
 }
 
-// grid (Nt, B*H): tile-order rows [64][D] -> transposed tile [D][64] (bf16).
+// grid (Nt, B*H): tile-order rows [64][D] -> transposed tile [D][64] (bf16)
+// whose 64 positions per row hold the keys in MFMA k-slot order: position j of
+// each 16-key group holds key tslot_key(j) of that group.
 template <int D>
 __global__ __launch_bounds__(256) void transpose_tiles_kernel(const uint16_t* __restrict__ in,
                                                               uint16_t* __restrict__ out, int64_t S) {
@@ -200,7 +203,8 @@ __global__ __launch_bounds__(256) void transpose_tiles_kernel(const uint16_t* __
   // output row d holds keys 0..63: 64 bf16 = 32 uint32
   uint32_t* dst = reinterpret_cast<uint32_t*>(out + base);
   for (int i = tid; i < D * 32; i += 256) {
-    const int d = i >> 5, kp = (i & 31) * 2;
+    const int d = i >> 5, p = (i & 31) * 2;
+    const int kp = (p & ~15) + tslot_key(p & 15);  // keys kp, kp + 1 at positions p, p + 1
     const uint32_t a0 = sP[kp][d >> 1], a1 = sP[kp + 1][d >> 1];
     const uint32_t lo = (d & 1) ? (a0 >> 16) : (a0 & 0xffffu);
     const uint32_t hi = (d & 1) ? (a1 >> 16) : (a1 & 0xffffu);

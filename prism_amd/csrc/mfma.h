@@ -1,0 +1,67 @@
+// MFMA operand helpers shared by the attention kernels (gfx950).
+//
+// v_mfma_f32_32x32x16_bf16 operand layout (64 lanes, g = lane / 32, l32 = lane % 32):
+//   A (32 x 16): lane holds A[l32][8g .. 8g+7]
+//   B (16 x 32): lane holds B[8g .. 8g+7][l32]
+//   C (32 x 32): lane holds C[8(r/4) + 4g + r%4][l32] in register r (16 registers)
+// A C block of 64 rows (two 32-row accumulators acc[0], acc[1]) becomes the B
+// operand of a following MFMA over k = those 64 rows in four 16-row steps
+// tt: step tt uses rows 16tt + {4g..4g+3, 8+4g..8+4g+3} as k-slots 8g..8g+7
+// (a permutation of k inside each 16-row group, applied identically to A).
+// "Transposed tiles" ([D][64] bf16, written by prism_transpose_tiles) store the
+// 64 keys of each row in that k-slot order, so the matching A operand is one
+// contiguous 16-byte load.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+__device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t* p) {
+  return as_bf16x8(*reinterpret_cast<const uint4*>(p));
+}
+__device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
+  return as_bf16x8(*reinterpret_cast<const uint4*>(p));
+}
+__device__ __forceinline__ f32x16 f32x16_zero() {
+  f32x16 z;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) z[r] = 0.0f;
+  return z;
+}
+// round-to-nearest-even bf16 pair
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  const __bf16 x = (__bf16)a, y = (__bf16)b;
+  return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+}
+// B operand of k-step tt from a 64-row accumulator pair (see the header comment)
+__device__ __forceinline__ bf16x8 b_from_acc(const f32x16* acc, int tt) {
+  const int h = tt >> 1, j0 = 2 * (tt & 1);
+  uint4 pb;
+  pb.x = pack_bf16(acc[h][4 * j0 + 0], acc[h][4 * j0 + 1]);
+  pb.y = pack_bf16(acc[h][4 * j0 + 2], acc[h][4 * j0 + 3]);
+  pb.z = pack_bf16(acc[h][4 * j0 + 4], acc[h][4 * j0 + 5]);
+  pb.w = pack_bf16(acc[h][4 * j0 + 6], acc[h][4 * j0 + 7]);
+  return as_bf16x8(pb);
+}
+// A operand (32 rows x 16 k) of k-step tt from a transposed tile in LDS
+// ([rows][pitch], keys in k-slot order)
+__device__ __forceinline__ bf16x8 a_from_t(const uint16_t* sT, int pitch, int dt, int tt, int l32, int g) {
+  return lds_bf16x8(sT + (32 * dt + l32) * pitch + 16 * tt + 8 * g);
+}
+// key stored at position j (0..15) of a 16-key group of a transposed tile
+__host__ __device__ __forceinline__ int tslot_key(int j) { return 4 * (j >> 3) + (j & 3) + 8 * ((j >> 2) & 1); }
+
+// 2^x on the transcendental unit (v_exp_f32); exp2(-inf) = 0
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+// L2).  Map the hardware id so that XCD x processes the contiguous logical
+// range [x*n/8, (x+1)*n/8) (a bijection on [0, n)).
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  const int xcd = bid & 7, slot = bid >> 3;
+  const int q = n >> 3, r = n & 7;
+  return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+}

@@ -122,7 +122,7 @@ def _assign(g: torch.Tensor, rho: torch.Tensor, method: int, tau_128: float, lam
     rho = rho.contiguous().float()
     Nz = rho.shape[0]
     sid = torch.empty(Nz, device=g.device, dtype=torch.int64)
-    ops._lib.call("prism_assign_shapes", g.data_ptr(), rho.data_ptr(), Nz, method, float(tau_128),
+    ops._call("prism_assign_shapes", g.data_ptr(), rho.data_ptr(), Nz, method, float(tau_128),
                   float(lambda_128), sid.data_ptr(), ops._stream())
     return sid
 

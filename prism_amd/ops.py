@@ -6,7 +6,8 @@ tensors; they are made contiguous where the kernels need it.
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple
+import contextlib
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
@@ -17,6 +18,40 @@ F32, BF16 = 0, 1
 
 def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
+
+
+# Optional per-entry-point timing: when enabled, every C-ABI call is bracketed
+# by a pair of HIP events on the stream it is launched on (the current stream).
+_timings: Optional[Dict[str, List[Tuple[torch.cuda.Event, torch.cuda.Event]]]] = None
+
+
+@contextlib.contextmanager
+def kernel_timing():
+    """Record HIP events around every C-ABI launch made inside the block.
+    Yields a dict name -> list of (start, end) events; after a synchronize,
+    ``summarize(d)`` gives per-entry-point call counts and average ms."""
+    global _timings
+    prev, _timings = _timings, {}
+    try:
+        yield _timings
+    finally:
+        _timings = prev
+
+
+def summarize(timings) -> Dict[str, Tuple[int, float]]:
+    return {name: (len(ev), sum(a.elapsed_time(b) for a, b in ev) / len(ev)) for name, ev in timings.items() if ev}
+
+
+def _call(name: str, *args) -> None:
+    if _timings is None:
+        _lib.call(name, *args)
+        return
+    st = torch.cuda.Event(enable_timing=True)
+    en = torch.cuda.Event(enable_timing=True)
+    st.record()
+    _lib.call(name, *args)
+    en.record()
+    _timings.setdefault(name, []).append((st, en))
 
 
 def _p(t: Optional[torch.Tensor]):
@@ -59,7 +94,7 @@ def zone_stats(v: torch.Tensor, grid, valid: Optional[torch.Tensor] = None):
     packed = torch.empty((Nz, 25 * D), device=v.device, dtype=torch.float32)
     av = torch.empty((Nz, 24), device=v.device, dtype=torch.uint8)
     vm = _u8(valid)
-    _lib.call("prism_zone_stats", _p(v), _code(v), H, S, D, _p(vm), T, Hg, Wg, _p(packed), _p(av), _stream())
+    _call("prism_zone_stats", _p(v), _code(v), H, S, D, _p(vm), T, Hg, Wg, _p(packed), _p(av), _stream())
     return packed, av
 
 
@@ -71,7 +106,7 @@ def audio_zone_stats(norms: torch.Tensor, grid, valid: Optional[torch.Tensor] = 
     abar = torch.empty(Nz, device=norms.device, dtype=torch.float32)
     vhat = torch.empty((Nz, 3), device=norms.device, dtype=torch.float32)
     vm = _u8(valid)
-    _lib.call("prism_audio_zone_stats", _p(norms), _code(norms), _p(vm), T, Hg, Wg, _p(abar), _p(vhat), _stream())
+    _call("prism_audio_zone_stats", _p(norms), _code(norms), _p(vm), T, Hg, Wg, _p(abar), _p(vhat), _stream())
     return abar, vhat
 
 
@@ -80,7 +115,7 @@ def zone_gradient(packed: torch.Tensor, axis_valid: torch.Tensor, D: int):
     Nz = packed.shape[0]
     rho_raw = torch.empty(Nz, device=packed.device, dtype=torch.float32)
     aniso = torch.empty((Nz, 3), device=packed.device, dtype=torch.float32)
-    _lib.call("prism_zone_gradient", _p(packed.contiguous()), _p(axis_valid.contiguous()), Nz, D, _p(rho_raw),
+    _call("prism_zone_gradient", _p(packed.contiguous()), _p(axis_valid.contiguous()), Nz, D, _p(rho_raw),
               _p(aniso), _stream())
     return rho_raw, aniso
 
@@ -94,7 +129,7 @@ def zone_shapes(rho_raw, aniso, abar, vhat, method: str, lambda_a: float, tau_12
     g = torch.empty((Nz, 3), device=dev, dtype=torch.float32)
     rho = torch.empty(Nz, device=dev, dtype=torch.float32)
     sid = torch.empty(Nz, device=dev, dtype=torch.int64)
-    _lib.call("prism_zone_shapes", _p(rho_raw), _p(aniso), _p(abar), _p(vhat), Nz, 0 if method == "ivpq" else 1,
+    _call("prism_zone_shapes", _p(rho_raw), _p(aniso), _p(abar), _p(vhat), Nz, 0 if method == "ivpq" else 1,
               float(lambda_a), float(tau_128), float(lambda_128), _p(g), _p(rho), _p(sid), _stream())
     return g, rho, sid
 
@@ -106,7 +141,7 @@ def a2v_norms(residual: torch.Tensor) -> torch.Tensor:
     r = r.contiguous()
     S, C = r.shape
     out = torch.empty(S, device=r.device, dtype=r.dtype)
-    _lib.call("prism_a2v_norms", _p(r), _code(r), S, C, _p(out), _code(out), _stream())
+    _call("prism_a2v_norms", _p(r), _code(r), S, C, _p(out), _code(out), _stream())
     return out
 
 
@@ -126,7 +161,7 @@ class ZoneLayout:
         self.block_offset = torch.empty(self.Nz + 1, device=dev, dtype=torch.int32)
         self.block_id_of_tile = torch.empty(self.Nt, device=dev, dtype=torch.int32)
         self.block_first_tile = torch.empty(self.Nt + 1, device=dev, dtype=torch.int32)
-        _lib.call("prism_zone_layout", _p(self.shape_ids), self.Nz, _p(self.block_offset), _p(self.block_id_of_tile),
+        _call("prism_zone_layout", _p(self.shape_ids), self.Nz, _p(self.block_offset), _p(self.block_id_of_tile),
                   _p(self.block_first_tile), _stream())
         # the one host synchronisation of the path (the reference syncs here too,
         # dynamic_block_attention.py:153): N_b sizes the block tensors
@@ -139,7 +174,7 @@ def rearrange_index(shape_ids: torch.Tensor, grid):
     S = T * Hg * Wg
     src = torch.empty(S, device=shape_ids.device, dtype=torch.int64)
     inv = torch.empty(S, device=shape_ids.device, dtype=torch.int64)
-    _lib.call("prism_rearrange_index", _p(shape_ids.contiguous()), T, Hg, Wg, _p(src), _p(inv), _stream())
+    _call("prism_rearrange_index", _p(shape_ids.contiguous()), T, Hg, Wg, _p(src), _p(inv), _stream())
     return src, inv
 
 
@@ -169,7 +204,7 @@ def gather_pool(x: torch.Tensor, lay: ZoneLayout, valid: Optional[torch.Tensor] 
         rowdot = torch.empty((B, H, S), device=dev, dtype=torch.float32)
     out["rowdot"] = rowdot
     vm = _u8(valid)
-    _lib.call("prism_gather_pool", _p(x), _code(x), B, H, S, D, _p(vm), _p(lay.shape_ids), _p(lay.block_offset),
+    _call("prism_gather_pool", _p(x), _code(x), B, H, S, D, _p(vm), _p(lay.shape_ids), _p(lay.block_offset),
               T, Hg, Wg, lay.N_b, _p(out["rows"]), _p(out["block_mean"]), _p(out["block_count"]),
               _p(out["tile_count"]), _p(out["valid_re"]), _p(dot_with), _p(rowdot), _stream())
     return out
@@ -181,7 +216,7 @@ def transpose_tiles(rows: torch.Tensor) -> torch.Tensor:
     rows = rows.contiguous()
     B, H, S, D = rows.shape
     out = torch.empty((B, H, S // 64, D, 64), device=rows.device, dtype=torch.bfloat16)
-    _lib.call("prism_transpose_tiles", _p(rows), B * H, S, D, _p(out), _stream())
+    _call("prism_transpose_tiles", _p(rows), B * H, S, D, _p(out), _stream())
     return out
 
 
@@ -191,7 +226,7 @@ def scatter_rows(rows: torch.Tensor, lay: ZoneLayout, out_dtype: torch.dtype) ->
     B, H, S, D = rows.shape
     T, Hg, Wg = lay.grid
     out = torch.empty((B, H, S, D), device=rows.device, dtype=out_dtype)
-    _lib.call("prism_scatter_rows", _p(rows), B, H, S, D, _p(lay.shape_ids), T, Hg, Wg, _p(out), _code(out),
+    _call("prism_scatter_rows", _p(rows), B, H, S, D, _p(lay.shape_ids), T, Hg, Wg, _p(out), _code(out),
               _stream())
     return out
 
@@ -205,7 +240,7 @@ def block_scores(qc: torch.Tensor, kc: torch.Tensor, block_count: Optional[torch
     qc = qc.contiguous().float()
     kc = kc.contiguous().float()
     out = torch.empty((*qc.shape[:-1], N), device=qc.device, dtype=torch.float32)
-    _lib.call("prism_block_scores", _p(qc), _p(kc), _p(block_count), BH, N, D, _p(out), _stream())
+    _call("prism_block_scores", _p(qc), _p(kc), _p(block_count), BH, N, D, _p(out), _stream())
     return out
 
 
@@ -256,7 +291,7 @@ def select_tiles(scores: torch.Tensor, sparsity, cdf_threshold, sm_scale: float,
     sel = torch.full((rows, max(width, 1)), N, device=dev, dtype=torch.int32) if want_blocks else None
     nsel = torch.empty(rows, device=dev, dtype=torch.int32) if want_blocks else None
     thr = cdf_threshold_fixed(cdf_threshold) if mode != 0 else 0
-    _lib.call("prism_select_tiles", _p(scores.contiguous()), rows, N, mode, k_lo, ub, float(sm_scale), thr,
+    _call("prism_select_tiles", _p(scores.contiguous()), rows, N, mode, k_lo, ub, float(sm_scale), thr,
               _p(block_first_tile), _p(tile_count), tcap, _p(tiles), _p(ntiles), _p(sel), max(width, 1), _p(nsel),
               _stream())
     return dict(tiles=tiles, ntiles=ntiles, sel_blocks=sel, nsel=nsel, tcap=tcap, width=width)
@@ -266,7 +301,7 @@ def tile_rows(ntiles: torch.Tensor, block_id_of_tile: torch.Tensor, BH: int, Nt:
     _cuda(ntiles, block_id_of_tile)
     qstart = torch.empty(BH * Nt, device=ntiles.device, dtype=torch.int64)
     qlen = torch.empty(BH * Nt, device=ntiles.device, dtype=torch.int32)
-    _lib.call("prism_tile_rows", _p(ntiles), _p(block_id_of_tile), BH, Nt, N_b, tcap, _p(qstart), _p(qlen), _stream())
+    _call("prism_tile_rows", _p(ntiles), _p(block_id_of_tile), BH, Nt, N_b, tcap, _p(qstart), _p(qlen), _stream())
     return qstart, qlen
 
 
@@ -279,7 +314,7 @@ def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tenso
     kstart = torch.empty(BH * Nt, device=dev, dtype=torch.int64)
     klen = torch.empty(BH * Nt, device=dev, dtype=torch.int32)
     kcols = torch.empty(BH * Nt * Nt, device=dev, dtype=torch.int32)
-    _lib.call("prism_transpose_lists", _p(qstart), _p(qlen), _p(qcols), BH, Nt, _p(bitmap), Nt, _p(kstart), _p(klen),
+    _call("prism_transpose_lists", _p(qstart), _p(qlen), _p(qcols), BH, Nt, _p(bitmap), Nt, _p(kstart), _p(klen),
               _p(kcols), _stream())
     return kstart, klen, kcols
 
@@ -298,7 +333,7 @@ def bsa_fwd(q, k, vt, kv_valid, qstart, qlen, qcols, sm_scale: float):
     B, H, S, D = q.shape
     o = torch.empty_like(q)
     lse = torch.empty((B, H, S), device=q.device, dtype=torch.float32)
-    _lib.call("prism_bsa_fwd", _p(q), _p(k), _p(vt), B * H, S, D, _p(kv_valid), _p(qstart), _p(qlen), _p(qcols),
+    _call("prism_bsa_fwd", _p(q), _p(k), _p(vt), B * H, S, D, _p(kv_valid), _p(qstart), _p(qlen), _p(qcols),
               float(sm_scale), _p(o), _p(lse), _stream())
     return o, lse
 
@@ -313,8 +348,8 @@ def bsa_bwd(q, qt, k, kt, v, do, dot, lse, delta, kv_valid, qlists, klists, sm_s
     qstart, qlen, qcols = qlists
     kstart, klen, kcols = klists
     s = _stream()
-    _lib.call("prism_bsa_bwd_dkdv", _p(q), _p(qt), _p(k), _p(v), _p(do), _p(dot), _p(lse), _p(delta), B * H, S, D,
+    _call("prism_bsa_bwd_dkdv", _p(q), _p(qt), _p(k), _p(v), _p(do), _p(dot), _p(lse), _p(delta), B * H, S, D,
               _p(kv_valid), _p(kstart), _p(klen), _p(kcols), float(sm_scale), _p(dk), _p(dv), s)
-    _lib.call("prism_bsa_bwd_dq", _p(q), _p(k), _p(kt), _p(v), _p(do), _p(lse), _p(delta), B * H, S, D,
+    _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(kt), _p(v), _p(do), _p(lse), _p(delta), B * H, S, D,
               _p(kv_valid), _p(qstart), _p(qlen), _p(qcols), float(sm_scale), _p(dq), s)
     return dq, dk, dv

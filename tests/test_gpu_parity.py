@@ -38,6 +38,12 @@ def host(t: torch.Tensor) -> np.ndarray:
     return t.cpu().numpy()
 
 
+# key held by each of the 64 positions of a transposed-tile row: inside a
+# 16-key group, positions 4-7 and 8-11 swap (MFMA k-slot order)
+TSLOT_PERM = np.array([16 * (p // 16) + [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15][p % 16]
+                       for p in range(64)])
+
+
 def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
     a = np.ascontiguousarray(a)
     b = np.ascontiguousarray(b)
@@ -162,7 +168,7 @@ def test_gather_pool_bitexact(case):
         t = host(ops.transpose_tiles(g["rows"]))
         B, H, S, D = x.shape
         exp = xf[:, :, src].reshape(B, H, S // 64, 64, D).transpose(0, 1, 2, 4, 3)
-        assert np.array_equal(t, exp)
+        assert np.array_equal(t, exp[..., TSLOT_PERM])
 
 
 def test_scores_bitexact():
