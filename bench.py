@@ -29,9 +29,9 @@ PEAK_HBM_GBS = 8000.0
 
 CONFIGS = {
     # name: (B, H, D, grid_real, audio_tokens, C, topk, cdf, sparsity_only, struct_scale, field_amp, field_ell)
-    "c4": (1, 5, 128, (21, 90, 160), 2000, 5120, 48, 0.9, None, 2.0, 2.65, 16.0),
-    "c3": (1, 24, 128, (21, 68, 120), 2000, 3072, 32, 0.9, None, 2.0, 2.65, 16.0),
-    "c2": (1, 24, 128, (21, 45, 80), 2000, 3072, None, None, 0.75, 2.0, 2.65, 16.0),
+    "c4": (1, 5, 128, (21, 90, 160), 2000, 5120, 48, 0.9, None, 2.0, 2.45, 16.0),
+    "c3": (1, 24, 128, (21, 68, 120), 2000, 3072, 32, 0.9, None, 2.0, 2.45, 16.0),
+    "c2": (1, 24, 128, (21, 45, 80), 2000, 3072, None, None, 0.75, 2.0, 2.45, 16.0),
 }
 
 
@@ -271,6 +271,8 @@ def main():
     sum_lens = plan.sum_lens()
     Nt, Nb, Sp = plan.lay.Nt, plan.lay.N_b, plan.S
     density = sum_lens / (B * H * Nt * Nt)
+    n_qvalid = int((plan.tile_count > 0).sum().item()) if plan.tile_count is not None else Nt
+    density_valid = sum_lens / (B * H * n_qvalid * Nt)  # over query tiles holding a valid token
     fl = 64 * 64 * D * sum_lens  # one 64x64xD product over all kept tile pairs
     kept_flops = 14 * fl          # FA convention: fwd 4, bwd 10
 
@@ -341,6 +343,7 @@ def main():
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(gp),
                    "audio_tokens": CONFIGS[args.config][4], "topk": inp["topk"], "cdf_threshold": cdf,
                    "sparsity": sparsity, "N_b": Nb, "sum_lens": sum_lens, "density": round(density, 4),
+                   "density_valid_q": round(density_valid, 4),
                    "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3),
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},

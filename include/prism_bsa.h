@@ -140,9 +140,12 @@ int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, i
 
 /* q tile rows share their q block's list (tile_sel.index_select(2,
  * block_id_of_tile), dynamic_block_attention.py:315-318):
- * qstart[bh*Nt + t] = (bh*N_b + block_id_of_tile[t]) * tcap, qlen likewise. */
-int prism_tile_rows(const int32_t* ntiles, const int32_t* block_id_of_tile, int BH, int64_t Nt, int64_t N_b,
-                    int64_t tcap, int64_t* qstart, int32_t* qlen, hipStream_t stream);
+ * qstart[bh*Nt + t] = (bh*N_b + block_id_of_tile[t]) * tcap, qlen likewise.
+ * q_tile_count [Nt] (or NULL): tiles with no valid query token get qlen 0
+ * (their rows are padding that the caller slices away, wan_video_dit.py:429-431;
+ * the reference still computes them). */
+int prism_tile_rows(const int32_t* ntiles, const int32_t* block_id_of_tile, const int32_t* q_tile_count, int BH,
+                    int64_t Nt, int64_t N_b, int64_t tcap, int64_t* qstart, int32_t* qlen, hipStream_t stream);
 
 /* create_indices_k_from_indices_q_varlen (bsa_interface.py:147-161) as a
  * bitmap transpose.  bitmap: workspace of BH*Nt*ceil(Nt/32) uint32.

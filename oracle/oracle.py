@@ -290,7 +290,7 @@ def transpose_lists(qstart, qlen, qcols, BH, Nt):
 # ---------------------------------------------------------------- full selection pipeline
 def select_pipeline(q, k, v, grid, *, method="ivpq", sparsity=0.9375, cdf_threshold_p=None,
                     audio_norms=None, valid=None, lambda_a=0.5, tau_128=0.15, lambda_128=1.0,
-                    shape_ids=None):
+                    shape_ids=None, skip_padded_queries=False):
     """Steps (1)-(5) of flash_attn_bsa_3d_dynamic
     (dynamic_block_attention.py:233-319): shape ids, geometry, pooled block
     means, scores, selection, per-q-tile key-tile lists.  Inputs are THW
@@ -312,6 +312,9 @@ def select_pipeline(q, k, v, grid, *, method="ivpq", sparsity=0.9375, cdf_thresh
     rows = (np.arange(B * H)[:, None] * nb + bot[None, :]).reshape(-1)
     qstart = rows * tcap
     qlen = ntiles[rows]
+    if skip_padded_queries and valid is not None:
+        # query tiles without a valid token attend to nothing
+        qlen = np.where(np.tile(tc == 0, B * H), 0, qlen).astype(np.int32)
     return dict(shape_ids=shape_ids, block_id_of_tile=bot, kblock_tiles=kbt, N_b=nb, block_offset=boff,
                 q_cmp=qc, k_cmp=kc, block_count=bc, tile_count=tc, scores=scores, sel=sel, nsel=nsel,
                 tiles=tiles, ntiles=ntiles, qstart=qstart, qlen=qlen, qcols=tiles.reshape(-1))

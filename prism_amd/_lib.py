@@ -33,7 +33,7 @@ SIGNATURES = {
     "prism_scatter_rows": [P, I32, I32, I64, I32, P, I32, I32, I32, P, I32, P],
     "prism_block_scores": [P, P, P, I32, I64, I32, P, P],
     "prism_select_tiles": [P, I64, I64, I32, I64, I64, F32, U64, P, P, I64, P, P, P, I64, P, P],
-    "prism_tile_rows": [P, P, I32, I64, I64, I64, P, P, P],
+    "prism_tile_rows": [P, P, P, I32, I64, I64, I64, P, P, P],
     "prism_transpose_lists": [P, P, P, I32, I64, P, I64, P, P, P, P],
     "prism_bsa_fwd": [P, P, P, I32, I64, I32, P, P, P, P, F32, P, P, P],
     "prism_bwd_preprocess": [P, P, I64, I32, P, P],

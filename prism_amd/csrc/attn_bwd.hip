@@ -99,7 +99,8 @@ __global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   __shared__ __align__(16) uint16_t sDO[2][64 * RP];
   __shared__ __align__(16) uint16_t sQT[2][D * TP];
   __shared__ __align__(16) uint16_t sDOT[2][D * TP];
-  __shared__ float sM[2][64], sDl[2][64];
+  __shared__ __align__(16) float sM[2][64];
+  __shared__ __align__(16) float sDl[2][64];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -170,14 +171,19 @@ __global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
           pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_bf16x8(&sDO[buf][(32 * qh + l32) * RP + 16 * s + 8 * g]),
                                                          vf[s], pacc, 0, 0, 0);
         }
-        // P and dS for rows q = 32qh + 8(r/4) + 4g + r%4, column = this lane's key
+        // P and dS for rows q = 32qh + 8j + 4g + i (register r = 4j + i), column = this lane's key
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int q = 32 * qh + 8 * (r >> 2) + 4 * g + (r & 3);
-          const float mq = sM[buf][q];
-          const float p = (kvalid && mq != NINF) ? fast_exp2(__builtin_fmaf(sacc[r], a.scale_log2, -mq)) : 0.0f;
-          sacc[r] = p;
-          pacc[r] = p * (pacc[r] - sDl[buf][q]);
+        for (int j = 0; j < 4; ++j) {
+          const float4 m4 = *reinterpret_cast<const float4*>(&sM[buf][32 * qh + 8 * j + 4 * g]);
+          const float4 d4 = *reinterpret_cast<const float4*>(&sDl[buf][32 * qh + 8 * j + 4 * g]);
+          const float mv[4] = {m4.x, m4.y, m4.z, m4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * j + i;
+            const float p = (kvalid && mv[i] != NINF) ? fast_exp2(__builtin_fmaf(sacc[r], a.scale_log2, -mv[i])) : 0.0f;
+            sacc[r] = p;
+            pacc[r] = p * (pacc[r] - dv4[i]);
+          }
         }
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2) {

@@ -135,36 +135,38 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     PRISM_FWD_ISSUE(more_nxt ? kt_nxt : kt_cur);
 
     if (act) {
-      // S^T[key][q] = K Q^T, two 32-key halves
-      f32x16 sacc[2];
+      // S^T[key][q] = K Q^T, two 32-key halves as interleaved MFMA chains
+      f32x16 sacc[2] = {f32x16_zero(), f32x16_zero()};
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        sacc[kh] = f32x16_zero();
+      for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
+        for (int kh = 0; kh < 2; ++kh) {
           const bf16x8 ka = lds_bf16x8(&sK[buf][(32 * kh + l32) * KP + 16 * s + 8 * g]);
           sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], sacc[kh], 0, 0, 0);
         }
-      }
       if (vmask != ~0ull) {
+        // this lane's keys are 32kh + 8j + 4g + i: bit (32kh + 8j + i) of vmask >> 4g
+        const uint64_t mm = vmask >> (4 * g);
+        const uint32_t lo = (uint32_t)mm, hi = (uint32_t)(mm >> 32);
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = 32 * kh + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (!((vmask >> key) & 1ull)) sacc[kh][r] = NINF;
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int b = 8 * (r >> 2) + (r & 3);
+          sacc[0][r] = ((lo >> b) & 1u) ? sacc[0][r] : NINF;
+          sacc[1][r] = ((hi >> b) & 1u) ? sacc[1][r] : NINF;
+        }
       }
-      float mx = NINF;
+      float mx = fmax_nn(sacc[0][0], sacc[1][0]);
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kh][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m, mx * a.scale_log2);
-      const bool dead = m_new == NINF;
-      const float alpha = dead ? 1.0f : fast_exp2(m - m_new);
-      const float mb = dead ? 0.0f : m_new;
+      for (int r = 1; r < 16; ++r) mx = fmax_nn(fmax_nn(mx, sacc[0][r]), sacc[1][r]);
+      mx = xor32_max(mx) * a.scale_log2;
+      // Lazy rescale: the running reference m only moves when the tile max
+      // exceeds it by more than 8 (log2 units), so p <= 2^8 and the O / l
+      // rescale is skipped unless some lane of the wave moved.  The final
+      // o = acc / l and lse = m + log2 l are unchanged by the choice of m.
+      const bool move = mx > m + 8.0f || (m == NINF && mx != NINF);
+      const float m_new = move ? mx : m;
+      const float alpha = move ? fast_exp2(m - m_new) : 1.0f;
+      const float mb = m_new == NINF ? 0.0f : m_new;
       float ls = 0.0f;
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
@@ -174,13 +176,15 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
           sacc[kh][r] = p;
           ls += p;
         }
-      ls += __shfl_xor(ls, 32, 64);
+      ls = xor32_add(ls);
       l = __builtin_fmaf(l, alpha, ls);
       m = m_new;
+      if (__builtin_amdgcn_ballot_w64(move)) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
+          for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
+      }
 
       // O^T[d][q] += V^T P^T over four 16-key steps
 #pragma unroll

@@ -31,10 +31,12 @@ __device__ __forceinline__ f32x16 f32x16_zero() {
   for (int r = 0; r < 16; ++r) z[r] = 0.0f;
   return z;
 }
-// round-to-nearest-even bf16 pair
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// round-to-nearest-even bf16 pair (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  const __bf16 x = (__bf16)a, y = (__bf16)b;
-  return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 // B operand of k-step tt from a 64-row accumulator pair (see the header comment)
 __device__ __forceinline__ bf16x8 b_from_acc(const f32x16* acc, int tt) {
@@ -53,6 +55,21 @@ __device__ __forceinline__ bf16x8 a_from_t(const uint16_t* sT, int pitch, int dt
 }
 // key stored at position j (0..15) of a 16-key group of a transposed tile
 __host__ __device__ __forceinline__ int tslot_key(int j) { return 4 * (j >> 3) + (j & 3) + 8 * ((j >> 2) & 1); }
+
+// max(a, b) for non-NaN inputs without NaN canonicalisation (v_med3 with
+// +inf folds into v_max3_f32 chains)
+__device__ __forceinline__ float fmax_nn(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, __builtin_inff()); }
+
+// x combined with the value of lane (l xor 32) by a symmetric op: one
+// v_permlane32_swap puts both halves' values in every lane
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmax_nn(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_add(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // 2^x on the transcendental unit (v_exp_f32); exp2(-inf) = 0
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -323,16 +323,17 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   }
 }
 
-// q tile t of head bh uses the list of its block (shared by the block's tiles)
+// q tile t of head bh uses the list of its block (shared by the block's tiles);
+// with q_tile_count, tiles without a valid query token get an empty list
 __global__ void tile_rows_kernel(const int32_t* __restrict__ ntiles, const int32_t* __restrict__ block_id_of_tile,
-                                 int64_t BH, int64_t Nt, int64_t N_b, int64_t tcap, int64_t* __restrict__ qstart,
-                                 int32_t* __restrict__ qlen) {
+                                 const int32_t* __restrict__ q_tile_count, int64_t BH, int64_t Nt, int64_t N_b,
+                                 int64_t tcap, int64_t* __restrict__ qstart, int32_t* __restrict__ qlen) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= BH * Nt) return;
   const int64_t bh = i / Nt, t = i - bh * Nt;
   const int64_t r = bh * N_b + block_id_of_tile[t];
   qstart[i] = r * tcap;
-  qlen[i] = ntiles[r];
+  qlen[i] = (q_tile_count && q_tile_count[t] == 0) ? 0 : ntiles[r];
 }
 
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
@@ -425,12 +426,12 @@ int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, i
   return PRISM_OK;
 }
 
-int prism_tile_rows(const int32_t* ntiles, const int32_t* block_id_of_tile, int BH, int64_t Nt, int64_t N_b,
-                    int64_t tcap, int64_t* qstart, int32_t* qlen, hipStream_t stream) {
+int prism_tile_rows(const int32_t* ntiles, const int32_t* block_id_of_tile, const int32_t* q_tile_count, int BH,
+                    int64_t Nt, int64_t N_b, int64_t tcap, int64_t* qstart, int32_t* qlen, hipStream_t stream) {
   PRISM_REQUIRE(ntiles && block_id_of_tile && qstart && qlen, "prism_tile_rows: null pointer");
   const int64_t n = (int64_t)BH * Nt;
   if (n == 0) return PRISM_OK;
-  tile_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(ntiles, block_id_of_tile, BH, Nt, N_b, tcap,
+  tile_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(ntiles, block_id_of_tile, q_tile_count, BH, Nt, N_b, tcap,
                                                                     qstart, qlen);
   PRISM_LAUNCH_CHECK("prism_tile_rows");
   return PRISM_OK;

@@ -51,7 +51,8 @@ def _build_block_tile_maps(shape_ids, ZT, ZH, ZW, device):
 class _Plan:
     """Everything the attention kernels need for one call, built under no_grad."""
 
-    def __init__(self, q, k, v, grid, shape_ids, valid_mask, sparsity, cdf_threshold, sm_scale):
+    def __init__(self, q, k, v, grid, shape_ids, valid_mask, sparsity, cdf_threshold, sm_scale,
+                 compute_padded_queries=False):
         B, H, S, D = q.shape
         self.B, self.H, self.S, self.D = B, H, S, D
         self.grid = grid
@@ -72,8 +73,9 @@ class _Plan:
         sel = ops.select_tiles(scores, sparsity, cdf_threshold, sm_scale, lay.block_first_tile,
                                self.tile_count if masked else None)
         self.sel = sel
+        skip = masked and not compute_padded_queries
         self.qstart, self.qlen = ops.tile_rows(sel["ntiles"], lay.block_id_of_tile, B * H, lay.Nt, lay.N_b,
-                                               sel["tcap"])
+                                               sel["tcap"], self.tile_count if skip else None)
         self.qcols = sel["tiles"].view(-1)
         self.klists = None
 
@@ -120,7 +122,8 @@ class _DynBSA(torch.autograd.Function):
 
 
 def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold=None, audio_token_norms=None,
-                 valid_mask=None, lambda_a=0.5, tau_128=0.15, lambda_128=1.0, shape_ids=None) -> _Plan:
+                 valid_mask=None, lambda_a=0.5, tau_128=0.15, lambda_128=1.0, shape_ids=None,
+                 compute_padded_queries=False) -> _Plan:
     """Steps (1)-(5) of flash_attn_bsa_3d_dynamic: shape ids, layout, pooled
     scores, selection and tile lists (no attention)."""
     B, Hn, S, D = q.shape
@@ -137,7 +140,7 @@ def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold
             shape_ids = _gradient_and_shapes(v.detach(), audio_token_norms, (T, H, W), method, lambda_a, tau_128,
                                              lambda_128, valid_mask)[2]
         return _Plan(q.detach(), k.detach(), v.detach(), (T, H, W), shape_ids, valid_mask, sparsity, cdf_threshold,
-                     sm_scale)
+                     sm_scale, compute_padded_queries)
 
 
 def flash_attn_bsa_3d_dynamic(
@@ -156,14 +159,24 @@ def flash_attn_bsa_3d_dynamic(
     lambda_128: float = 1.0,
     shape_ids: Optional[torch.Tensor] = None,
     return_shape_ids: bool = False,
+    compute_padded_queries: bool = False,
 ):
     """Dynamic-block-shape BSA for video self-attention; returns [B,H,S,D] in
     THW order (dynamic_block_attention.py:194-332).  q, k, v: [B,H,S,D] THW
     order on the GPU, grid padded to multiples of 8; float32 or bfloat16
-    (attention itself runs in bf16 MFMA with fp32 accumulation)."""
+    (attention itself runs in bf16 MFMA with fp32 accumulation).
+
+    With a valid_mask, query tiles that hold no valid token are padding the
+    caller slices away (wan_video_dit.py:429-431).  The reference still
+    attends for them (their pooled query is 0, so the threshold keeps ~p of
+    all blocks); here their output is 0 unless compute_padded_queries=True.
+    Outputs at valid positions and all gradients of valid tokens are the same
+    either way when the incoming gradient is 0 at padded positions (as the
+    caller's unpadding makes it)."""
     plan = plan_dynamic(q, k, v, grid_padded, method=method, sparsity=sparsity, cdf_threshold=cdf_threshold,
                         audio_token_norms=audio_token_norms, valid_mask=valid_mask, lambda_a=lambda_a,
-                        tau_128=tau_128, lambda_128=lambda_128, shape_ids=shape_ids)
+                        tau_128=tau_128, lambda_128=lambda_128, shape_ids=shape_ids,
+                        compute_padded_queries=compute_padded_queries)
     sm_scale = 1.0 / (q.shape[-1] ** 0.5)
     out = _DynBSA.apply(q, k, v, plan, sm_scale)
     if return_shape_ids:

@@ -297,11 +297,15 @@ def select_tiles(scores: torch.Tensor, sparsity, cdf_threshold, sm_scale: float,
     return dict(tiles=tiles, ntiles=ntiles, sel_blocks=sel, nsel=nsel, tcap=tcap, width=width)
 
 
-def tile_rows(ntiles: torch.Tensor, block_id_of_tile: torch.Tensor, BH: int, Nt: int, N_b: int, tcap: int):
-    _cuda(ntiles, block_id_of_tile)
+def tile_rows(ntiles: torch.Tensor, block_id_of_tile: torch.Tensor, BH: int, Nt: int, N_b: int, tcap: int,
+              q_tile_count: Optional[torch.Tensor] = None):
+    """Per-query-tile list starts and lengths; tiles whose q_tile_count is 0
+    (no valid query token) get empty lists."""
+    _cuda(ntiles, block_id_of_tile, q_tile_count)
     qstart = torch.empty(BH * Nt, device=ntiles.device, dtype=torch.int64)
     qlen = torch.empty(BH * Nt, device=ntiles.device, dtype=torch.int32)
-    _call("prism_tile_rows", _p(ntiles), _p(block_id_of_tile), BH, Nt, N_b, tcap, _p(qstart), _p(qlen), _stream())
+    _call("prism_tile_rows", _p(ntiles), _p(block_id_of_tile), _p(q_tile_count), BH, Nt, N_b, tcap, _p(qstart), _p(qlen),
+          _stream())
     return qstart, qlen
 
 

@@ -239,7 +239,7 @@ def test_full_selection_pipeline_bitexact(case):
     for method, sp, p in (("ivpq", 0.75, 0.9), ("penalty", 0.5, None), ("ivpq", None, 0.5)):
         say("pipeline", method, sp, p)
         ref = O.select_pipeline(case["qh"], case["kh"], case["vh"], case["grid"], method=method, sparsity=sp,
-                                cdf_threshold_p=p, audio_norms=case["nh"], valid=valid)
+                                cdf_threshold_p=p, audio_norms=case["nh"], valid=valid, skip_padded_queries=True)
         plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method=method,
                             sparsity=sp, cdf_threshold=p,
                             audio_token_norms=None if case["nh"] is None else dev(case["nh"]),
@@ -316,15 +316,18 @@ def test_attention_fwd_bwd_tolerance(case):
         _tol(O.bf16_bits_to_f32(host(g)).reshape(B * H, S, D), r, name)
 
 
-def test_end_to_end_autograd(case):
+@pytest.mark.parametrize("compute_padded", [False, True])
+def test_end_to_end_autograd(case, compute_padded):
     """flash_attn_bsa_3d_dynamic forward + backward through autograd in THW
-    order vs the oracle attention on the oracle's own selection."""
+    order vs the oracle attention on the oracle's own selection (with and
+    without attention for fully padded query tiles)."""
     from prism_amd import flash_attn_bsa_3d_dynamic
     valid = case["valid"] if case["pad"] else None
     B, H, S, D = case["q"].shape
     sm = 1 / math.sqrt(D)
     ref = O.select_pipeline(case["qh"], case["kh"], case["vh"], case["grid"], method="ivpq", sparsity=0.7,
-                            cdf_threshold_p=0.9, audio_norms=case["nh"], valid=valid)
+                            cdf_threshold_p=0.9, audio_norms=case["nh"], valid=valid,
+                            skip_padded_queries=not compute_padded)
     src, inv = O.rearrange_index(ref["shape_ids"], case["grid"])
     tof = (lambda a: O.bf16_bits_to_f32(a)) if case["qh"].dtype == np.uint16 else (lambda a: O.bf16_bits_to_f32(bf16(a)))
     qf, kf, vf = (tof(case[n])[:, :, src].reshape(B * H, S, D) for n in ("qh", "kh", "vh"))
@@ -335,7 +338,7 @@ def test_end_to_end_autograd(case):
     out, sid = flash_attn_bsa_3d_dynamic(q, k, v, case["grid"], method="ivpq", sparsity=0.7, cdf_threshold=0.9,
                                          audio_token_norms=None if case["nh"] is None else dev(case["nh"]),
                                          valid_mask=None if valid is None else dev(valid).bool(),
-                                         return_shape_ids=True)
+                                         return_shape_ids=True, compute_padded_queries=compute_padded)
     assert out.dtype == tdt
     assert np.array_equal(host(sid), ref["shape_ids"])
     og = out.detach().float().cpu().numpy().reshape(B * H, S, D)

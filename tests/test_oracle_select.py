@@ -355,3 +355,15 @@ def test_select_pipeline_vs_reference_torch_steps():
         assert ref["tiles"][r, : ref["ntiles"][r]].tolist() == exp, r
         checked += 1
     assert checked >= (B * H * nb) * 3 // 4
+
+
+def test_skip_padded_queries_only_empties_fully_padded_tiles():
+    from tests.cases import padded_case
+    c = padded_case(1, 1, 1, (5, 12, 16), 64)
+    full = O.select_pipeline(c["q"], c["k"], c["v"], c["grid"], sparsity=0.8, cdf_threshold_p=0.9, valid=c["valid"])
+    skip = O.select_pipeline(c["q"], c["k"], c["v"], c["grid"], sparsity=0.8, cdf_threshold_p=0.9, valid=c["valid"],
+                             skip_padded_queries=True)
+    empty = full["tile_count"] == 0
+    assert empty.any() and (~empty).any()
+    assert np.all(skip["qlen"][empty] == 0)
+    assert np.array_equal(skip["qlen"][~empty], full["qlen"][~empty])
