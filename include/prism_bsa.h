@@ -157,16 +157,41 @@ int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int3
 
 /* ------------------------------------------------------------------ attention */
 
+/* Work lists of the paired-tile attention kernels.  Every attention kernel runs
+ * one workgroup per pair of tiles (2p, 2p+1) and walks the sorted union of the
+ * two tiles' lists.  For pair p (rows 2p, 2p+1 of a per-row list; rows =
+ * BH*Nt, Nt even): ucols[ustart[p] .. + ulen[p]) ascending entries
+ * tile << 3 | partial << 2 | in_row_2p+1 << 1 | in_row_2p, where partial =
+ * (tile_masks != NULL && tile_masks[tile] != all ones), tile_masks from
+ * prism_tile_masks.  ustart[p] = p * ucap,
+ * ucap >= Nt.  Used on the per-query-tile key lists (forward, dQ; the
+ * reference's block_indices, bsa_interface.py:328-385) and on the per-key-tile
+ * query lists of prism_transpose_lists (dK/dV; bsa_interface.py:437-447).
+ * No counterpart routine in the reference: its kernels take one list per tile. */
+int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t Nt,
+                     const uint64_t* tile_masks, int64_t ucap, int64_t* ustart, int32_t* ulen, int32_t* ucols,
+                     hipStream_t stream);
+
+/* Key validity per 64-token tile (the reference's kv_valid_mask,
+ * bsa_interface.py:328-385, flash_attn_bsa_varlen_mask.py:263-295) packed as
+ * masks[t] bit j = valid[64 t + j] != 0.  valid: [Nt*64] uint8 tile order. */
+int prism_tile_masks(const uint8_t* valid, int64_t Nt, uint64_t* masks, hipStream_t stream);
+
+/* Base-2 row maximum of the backward (bsa_interface.py:405-416: M = lse / ln 2):
+ * m2[i] = lse[i] * log2(e), with lse = -inf (a row that saw no valid key)
+ * mapped to +inf so that its probabilities are exactly 0. */
+int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
+
 /* attn_fwd_bsa_varlen_triton (bsa_interface.py:328-385) with
  * _attn_fwd_bsa_varlen_align (flash_attn_bsa_varlen_mask.py:191-319), chunk 64.
  * S must be a multiple of 128 (query tiles are processed in pairs).
  * q, k: [BH,S,D] bf16 tile order; vt: [BH,S/64,D,64] bf16 transposed tiles
- * (prism_transpose_tiles); key tile lists ascending;
- * kv_valid: [S] uint8 or NULL; per query tile row bh*Nt + t the key tiles
- * qcols[qstart[row] .. + qlen[row]).  o: [BH,S,D] bf16; lse: [BH,S] fp32
- * natural log (-inf for rows without a valid key; their o is 0). */
-int prism_bsa_fwd(const void* q, const void* k, const void* vt, int BH, int64_t S, int D, const uint8_t* kv_valid,
-                  const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, float sm_scale, void* o,
+ * (prism_transpose_tiles); ustart/ulen/ucols: prism_pair_union of the
+ * per-query-tile key lists with the same tile_masks (prism_tile_masks of the
+ * key validity, or NULL when no key is padded).  o: [BH,S,D] bf16; lse: [BH,S] fp32 natural log (-inf for rows
+ * without a valid key; their o is 0). */
+int prism_bsa_fwd(const void* q, const void* k, const void* vt, int BH, int64_t S, int D, const uint64_t* tile_masks,
+                  const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* o,
                   float* lse, hipStream_t stream);
 
 /* _attn_bwd_preprocess (common.py:110-127): delta[r] = sum_d o[r][d] * do[r][d]
@@ -175,19 +200,21 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 
 /* dK, dV of attn_bwd_bsa_varlen_triton (bsa_interface.py:387-487;
  * _attn_bwd_dkdv_bsa_varlen_wrapper, flash_attn_bsa_varlen_mask.py:562-704).
- * qt, dot: transposed tiles of q and dO; delta from prism_gather_pool;
- * lists per key tile from prism_transpose_lists. */
+ * qt, dot: transposed tiles of q and dO; m2 from prism_lse_to_m2; delta from
+ * prism_gather_pool or prism_bwd_preprocess; kv_valid: [S] uint8 tile order
+ * or NULL; ustart/ulen/ucols: prism_pair_union of the per-key-tile query
+ * lists of prism_transpose_lists (tile_masks NULL). */
 int prism_bsa_bwd_dkdv(const void* q, const void* qt, const void* k, const void* v, const void* do_, const void* dot,
-                       const float* lse, const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid,
-                       const int64_t* kstart, const int32_t* klen, const int32_t* kcols, float sm_scale, void* dk,
+                       const float* m2, const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid,
+                       const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk,
                        void* dv, hipStream_t stream);
 
 /* dQ of attn_bwd_bsa_varlen_triton (bsa_interface.py:489-523;
  * _attn_bwd_dq_bsa_varlen_align_wrapper, flash_attn_bsa_varlen_mask.py:879-1014).
- * kt: transposed tiles of k; lists per query tile as for prism_bsa_fwd. */
-int prism_bsa_bwd_dq(const void* q, const void* k, const void* kt, const void* v, const void* do_, const float* lse,
-                     const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid, const int64_t* qstart,
-                     const int32_t* qlen, const int32_t* qcols, float sm_scale, void* dq, hipStream_t stream);
+ * kt: transposed tiles of k; lists and tile_masks as for prism_bsa_fwd. */
+int prism_bsa_bwd_dq(const void* q, const void* k, const void* kt, const void* v, const void* do_, const float* m2,
+                     const float* delta, int BH, int64_t S, int D, const uint64_t* tile_masks, const int64_t* ustart,
+                     const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream);
 
 #ifdef __cplusplus
 }

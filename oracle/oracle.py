@@ -287,6 +287,34 @@ def transpose_lists(qstart, qlen, qcols, BH, Nt):
     return kcols.reshape(BH * Nt, Nt), klen
 
 
+def tile_masks(valid: np.ndarray) -> np.ndarray:
+    """Key validity per 64-token tile as a 64-bit word, bit j = token j valid
+    (the kv_valid_mask of bsa_interface.py:328-385 regrouped per tile)."""
+    v = (np.asarray(valid).reshape(-1, TILE) != 0).astype(np.uint64)
+    return (v << np.arange(TILE, dtype=np.uint64)[None, :]).sum(axis=1, dtype=np.uint64)
+
+
+def pair_union(start, length, cols, Nt, masks=None):
+    """For each row pair (2p, 2p+1): the ascending union of the two rows'
+    tile lists, entry = tile << 3 | partial << 2 | in_second << 1 | in_first,
+    partial = masks is given and masks[tile] is not all ones.  This is the
+    work list of the paired-tile attention kernels (no reference counterpart:
+    the reference walks one list per tile, bsa_interface.py:328-523)."""
+    start = np.asarray(start, np.int64)
+    length = np.asarray(length, np.int64)
+    cols = np.asarray(cols, np.int64)
+    out = []
+    for p in range(start.size // 2):
+        a = cols[start[2 * p]: start[2 * p] + length[2 * p]]
+        b = cols[start[2 * p + 1]: start[2 * p + 1] + length[2 * p + 1]]
+        u = np.union1d(a, b)
+        e = (u << 3) | np.isin(u, a).astype(np.int64) | (np.isin(u, b).astype(np.int64) << 1)
+        if masks is not None:
+            e |= (np.asarray(masks, np.uint64)[u] != np.uint64(0xFFFFFFFFFFFFFFFF)).astype(np.int64) << 2
+        out.append(e.astype(np.int32))
+    return out
+
+
 # ---------------------------------------------------------------- full selection pipeline
 def select_pipeline(q, k, v, grid, *, method="ivpq", sparsity=0.9375, cdf_threshold_p=None,
                     audio_norms=None, valid=None, lambda_a=0.5, tau_128=0.15, lambda_128=1.0,

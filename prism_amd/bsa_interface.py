@@ -76,9 +76,11 @@ def attn_fwd_bsa_varlen(q, k, v, sm_scale, block_indices, block_indices_lens, ch
     Returns (o [B,H,S,D], lse [B,H,S] natural log)."""
     _check_chunks(chunk_size_q, chunk_size_k)
     qstart, qlen, qcols = _lists_from_dense(block_indices, block_indices_lens)
+    Nt = q.shape[2] // 64
+    tm = ops.tile_masks(ops._u8(kv_valid_mask))
+    qunion = ops.pair_union(qstart, qlen, qcols, Nt, tm)
     vt = ops.transpose_tiles(v)
-    kv = ops._u8(kv_valid_mask)
-    return ops.bsa_fwd(q, k, vt, kv, qstart, qlen, qcols, sm_scale)
+    return ops.bsa_fwd(q, k, vt, tm, qunion, sm_scale)
 
 
 def create_indices_k_from_indices_q_varlen(block_indices: torch.Tensor, N_cols_mask: int):
@@ -111,8 +113,12 @@ def attn_bwd_bsa_varlen(do, q, k, v, o, dq, dk, dv, sm_scale, lse, block_indices
     ops._call("prism_bwd_preprocess", o.data_ptr(), do.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
     klists = ops.transpose_lists(qstart, qlen, qcols, B * H, Nt)
     kv = ops._u8(kv_valid_mask)
+    tm = ops.tile_masks(kv)
+    qunion = ops.pair_union(qstart, qlen, qcols, Nt, tm)
+    kunion = ops.pair_union(*klists, Nt)
+    m2 = ops.lse_to_m2(lse)
     g_q, g_k, g_v = ops.bsa_bwd(q, ops.transpose_tiles(q), k, ops.transpose_tiles(k), v, do, ops.transpose_tiles(do),
-                                lse.float().contiguous(), delta, kv, (qstart, qlen, qcols), klists, sm_scale)
+                                m2, delta, kv, tm, qunion, kunion, sm_scale)
     dq.copy_(g_q)
     dk.copy_(g_k)
     dv.copy_(g_v)

@@ -21,7 +21,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libprism_bsa.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-SOURCES = ["errors.hip", "stats.hip", "layout.hip", "select.hip", "attn_fwd.hip", "attn_bwd.hip"]
+SOURCES = ["errors.hip", "stats.hip", "layout.hip", "select.hip", "lists.hip", "attn_fwd.hip", "attn_bwd.hip"]
 CANONICAL = {"stats.hip", "layout.hip", "select.hip"}
 
 COMMON_FLAGS = [

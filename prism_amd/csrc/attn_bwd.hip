@@ -11,36 +11,45 @@
 //
 // Layouts (per head, tile order): Q, K, V, dO row-major [S][D]; Q^T, K^T, dO^T
 // as transposed 64-row tiles [Nt][D][64] with keys in MFMA k-slot order
-// (prism_transpose_tiles).
+// (prism_transpose_tiles).  m2 = lse * log2(e) with rows that saw no valid key
+// at +inf (prism_lse_to_m2).
 //
 // MI355X design, shared by both kernels:
-//  * one workgroup (4 waves) per PAIR of tiles (2p, 2p+1) walking the sorted
-//    union of their two lists; waves 0-1 own tile 2p, waves 2-3 tile 2p+1 and
-//    skip the math for list entries that are not theirs;
-//  * operand tiles are staged HBM -> registers -> LDS with the next tile's
-//    loads in flight during the current tile's math (double-buffered LDS,
-//    one wave per SIMD); LDS
-//    rows are padded so MFMA operand reads are conflict-free 16-byte loads;
+//  * one workgroup of 8 waves per PAIR of tiles (2p, 2p+1), one workgroup per
+//    CU (two waves per SIMD), walking the sorted union of the two tiles' lists
+//    (prism_pair_union);
+//  * the operand tiles of the next list entry are copied HBM -> LDS by
+//    global_load_lds_dwordx4 while the current entry is multiplied
+//    (double-buffered stages, one barrier per entry, no VGPR staging);
+//  * the eight waves split the work of each (tile, tile) product in two
+//    halves of the contracted dimension, so every wave holds half-size
+//    partial accumulators; the two partials are added in a fixed order
+//    through LDS at the end (deterministic);
 //  * workgroup ids are remapped per XCD (contiguous zones per L2).
-// dK/dV: wave w owns keys [32w', 32w'+32) of its tile.  S = Q K^T and
-// dP = dO V^T keep one key per lane column, so P and dS feed the B operand of
-// dV^T = dO^T P and dK^T = Q^T dS straight from the accumulators; the 64 query
-// rows are processed in two 32-row halves to bound register pressure.
-// dQ: wave w owns 32 queries.  S^T = K Q^T and dP^T = V dO^T keep one query per
-// lane column; dQ^T = K^T dS^T.
+// dK/dV: wave w owns keys [32 kh, 32 kh + 32) of tile 2p + tk and query rows
+// [32 qh, 32 qh + 32) of every listed query tile (kh = w & 1, tk = (w >> 1) & 1,
+// qh = w >> 2).  S = Q K^T and dP = dO V^T keep one key per lane column, so P
+// and dS feed the B operand of dV^T = dO^T P and dK^T = Q^T dS straight from
+// the accumulators.
+// dQ: wave w owns query rows [32 qh, 32 qh + 32) of tile 2p + tq and keys
+// [32 kh, 32 kh + 32) of every listed key tile (qh = w & 1,
+// tq = (w >> 1) & 1, kh = w >> 2).  S^T = K Q^T and dP^T = V dO^T keep one
+// query per lane column; dQ^T = K^T dS^T.
 #include "common.h"
 #include "mfma.h"
+#include "tile_dma.h"
 
 namespace {
 
 struct BwdArgs {
   const uint16_t *q, *qt, *k, *kt, *v, *do_, *dot;
-  const float* lse;         // [BH, S] natural log
+  const float* m2;          // [BH, S] base-2 row max (lse * log2 e, +inf for empty rows)
   const float* delta;       // [BH, S]
-  const uint8_t* kv_valid;  // [S] tile order or null
-  const int64_t* start;     // list starts (per key tile for dK/dV, per query tile for dQ)
-  const int32_t* len;
-  const int32_t* cols;
+  const uint8_t* kv_valid;  // [S] tile order or null (dK/dV)
+  const uint64_t* tmask;    // [Nt] per-tile key validity or null (dQ)
+  const int64_t* ustart;    // pair-union lists
+  const int32_t* ulen;
+  const int32_t* ucols;
   int64_t S, Nt;
   int npairs;
   float sm_scale, scale_log2;
@@ -49,293 +58,316 @@ struct BwdArgs {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// merge cursor over two ascending lists (wave-uniform)
-struct Union2 {
-  const int32_t *A, *B;
-  int nA, nB, ia, ib;
-  __device__ __forceinline__ bool next(int& t, bool& inA, bool& inB) {
-    const int ca = ia < nA ? A[ia] : INT32_MAX;
-    const int cb = ib < nB ? B[ib] : INT32_MAX;
-    t = ca < cb ? ca : cb;
-    inA = ca == t;
-    inB = cb == t;
-    if (t == INT32_MAX) return false;
-    ia += inA;
-    ib += inB;
-    return true;
-  }
+template <int D>
+struct BwdTiles {
+  static constexpr int RW = 2 * D, RPB = RW + 16, R_KB = 64 * RPB / 1024;  // row-major [64][D]
+  static constexpr int TW = 128, TPB = TW + 16, T_KB = D * TPB / 1024;     // transposed [D][64]
+  static_assert(64 * RPB % 1024 == 0 && D * TPB % 1024 == 0, "tiles must fill whole KB");
+  // dQ stage: K, V (row-major), K^T
+  static constexpr int DQ_KB = 2 * R_KB + T_KB;
+  static constexpr int DQ_SLOTS = (DQ_KB + 7) / 8;
+  // dK/dV stage: Q, dO (row-major), Q^T, dO^T, then m2 and delta rows (256 B each)
+  static constexpr int DKDV_KB = 2 * R_KB + 2 * T_KB;
+  static constexpr int DKDV_BYTES = DKDV_KB * 1024 + 512;
+  static constexpr int DKDV_SLOTS = (DKDV_KB + 7) / 8;
 };
 
-// Global -> register staging of one bf16 tile of 64*D elements (contiguous in
-// HBM) by 256 threads: KCH 16-byte chunks per thread, chunk c = tid + 256 i.
-template <int KCH>
-__device__ __forceinline__ void stage_load(uint4* r, const uint16_t* __restrict__ g, int tid) {
-#pragma unroll
-  for (int i = 0; i < KCH; ++i) r[i] = *reinterpret_cast<const uint4*>(g + (tid + i * 256) * 8);
-}
-// register -> LDS: row-major [64][D] tile with pitch RP
-template <int D, int KCH, int RP>
-__device__ __forceinline__ void stage_rows(uint16_t* s, const uint4* r, int tid) {
-#pragma unroll
-  for (int i = 0; i < KCH; ++i) {
-    const int c = tid + i * 256;
-    *reinterpret_cast<uint4*>(&s[(c / (D / 8)) * RP + (c % (D / 8)) * 8]) = r[i];
-  }
-}
-// register -> LDS: transposed [D][64] tile with pitch TP
-template <int KCH, int TP>
-__device__ __forceinline__ void stage_trans(uint16_t* s, const uint4* r, int tid) {
-#pragma unroll
-  for (int i = 0; i < KCH; ++i) {
-    const int c = tid + i * 256;
-    *reinterpret_cast<uint4*>(&s[(c >> 3) * TP + (c & 7) * 8]) = r[i];
-  }
-}
-
 template <int D>
-__global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
-  constexpr int RP = D + 8, TP = 64 + 8, NS = D / 16, NDT = D / 32, KCH = 64 * D / 8 / 256;
-  __shared__ __align__(16) uint16_t sQ[2][64 * RP];
-  __shared__ __align__(16) uint16_t sDO[2][64 * RP];
-  __shared__ __align__(16) uint16_t sQT[2][D * TP];
-  __shared__ __align__(16) uint16_t sDOT[2][D * TP];
-  __shared__ __align__(16) float sM[2][64];
-  __shared__ __align__(16) float sDl[2][64];
+__global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
+  using T = BwdTiles<D>;
+  constexpr int NS = D / 16, NDT = D / 32;
+  constexpr int SB = T::DKDV_BYTES;
+  __shared__ __align__(16) uint8_t smem[2 * SB];
+  static_assert(4 * 64 * 2 * NDT * 16 * 4 <= 2 * SB, "reduction buffer must fit the stages");
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int w = (int)uniform_u32((uint32_t)tid >> 6);
+  const int kh = w & 1, tk = (w >> 1) & 1, qh = w >> 2;
   const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
-  const int64_t rowA = (int64_t)bh * a.Nt + 2 * pair;
-  Union2 u{a.cols + a.start[rowA], a.cols + a.start[rowA + 1], a.len[rowA], a.len[rowA + 1], 0, 0};
-  const bool mine_is_b = w >= 2;
+  const int32_t* U = a.ucols + a.ustart[logical];
+  const int n = a.ulen[logical];
+  const int mybit = 1 << tk;
   const int64_t hoff = (int64_t)bh * a.S * D;
-  const int64_t key = (int64_t)(2 * pair + (w >> 1)) * 64 + 32 * (w & 1) + l32;
-  const bool kvalid = a.kv_valid ? a.kv_valid[key] != 0 : true;
-  const float NINF = -__builtin_inff();
-  const float* lse_h = a.lse + (int64_t)bh * a.S;
-  const float* dl_h = a.delta + (int64_t)bh * a.S;
+  const float* m2h = a.m2 + (int64_t)bh * a.S;
+  const float* dlh = a.delta + (int64_t)bh * a.S;
 
+  // DMA plan: wave w issues KB-instructions w, w + 8, ... (Q, dO, Q^T, dO^T);
+  // wave 7 also copies the m2 row and wave 6 the delta row of the entry.
+  uint32_t soff[T::DKDV_SLOTS];
+#pragma unroll
+  for (int s = 0; s < T::DKDV_SLOTS; ++s) {
+    const int i = w + 8 * s;
+    soff[s] = i < 2 * T::R_KB ? padded_src_offset<T::RW>(i % T::R_KB, lane)
+                              : padded_src_offset<T::TW>((i - 2 * T::R_KB) % T::T_KB, lane);
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int qtile, int st) {
+    const int64_t toff = hoff + (int64_t)qtile * 64 * D;
+    const void* src4[4] = {uniform_ptr(a.q + toff), uniform_ptr(a.do_ + toff), uniform_ptr(a.qt + toff),
+                           uniform_ptr(a.dot + toff)};
+    const uint32_t base = lds0 + (uint32_t)(st * SB);
+#pragma unroll
+    for (int s = 0; s < T::DKDV_SLOTS; ++s) {
+      const int i = w + 8 * s;
+      const int which = i < T::R_KB ? 0 : i < 2 * T::R_KB ? 1 : i < 2 * T::R_KB + T::T_KB ? 2 : 3;
+      if (s + 1 < T::DKDV_SLOTS || i < T::DKDV_KB) dma_b128(soff[s], src4[which], base + (uint32_t)i * 1024u);
+    }
+    if (w >= 6) {
+      const float* rowsrc = (w == 7 ? m2h : dlh) + (int64_t)qtile * 64;
+      dma_b32((uint32_t)lane * 4u, uniform_ptr(rowsrc), base + T::DKDV_KB * 1024u + (w == 7 ? 0u : 256u));
+    }
+  };
+
+  int e_cur = n > 0 ? sload_i32(U) : 0;
+  int e_nxt = n > 1 ? sload_i32(U + 1) : 0;
+  if (n > 0) issue(e_cur >> 3, 0);
+
+  const int64_t key = (int64_t)(2 * pair + tk) * 64 + 32 * kh + l32;
   bf16x8 kf[NS], vf[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     kf[s] = ld_bf16x8(a.k + hoff + key * D + 16 * s + 8 * g);
     vf[s] = ld_bf16x8(a.v + hoff + key * D + 16 * s + 8 * g);
   }
+  const bool kvalid = a.kv_valid ? a.kv_valid[key] != 0 : true;
+  const float kbias = kvalid ? 0.0f : -__builtin_inff();
+  const bool all_valid = __builtin_amdgcn_ballot_w64(!kvalid) == 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    consume_regs(kf[s]);
+    consume_regs(vf[s]);
+  }
+  consume_regs(kbias);
   f32x16 dk[NDT], dv[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) { dk[dt] = f32x16_zero(); dv[dt] = f32x16_zero(); }
 
-  uint4 rq[KCH], rdo[KCH], rqt[KCH], rdot[KCH];
-  float rm = 0.0f;
-#define PRISM_DKDV_ISSUE(qt_)                                          \
-  do {                                                                 \
-    const int64_t toff = hoff + (int64_t)(qt_) * 64 * D;               \
-    stage_load<KCH>(rq, a.q + toff, tid);                              \
-    stage_load<KCH>(rdo, a.do_ + toff, tid);                           \
-    stage_load<KCH>(rqt, a.qt + toff, tid);                            \
-    stage_load<KCH>(rdot, a.dot + toff, tid);                          \
-    if (tid < 64) rm = lse_h[(int64_t)(qt_) * 64 + tid] * kLog2e;      \
-    else if (tid < 128) rm = dl_h[(int64_t)(qt_) * 64 + tid - 64];     \
-  } while (0)
-#define PRISM_DKDV_COMMIT(b)                                           \
-  do {                                                                 \
-    stage_rows<D, KCH, RP>(sQ[b], rq, tid);                            \
-    stage_rows<D, KCH, RP>(sDO[b], rdo, tid);                          \
-    stage_trans<KCH, TP>(sQT[b], rqt, tid);                            \
-    stage_trans<KCH, TP>(sDOT[b], rdot, tid);                          \
-    if (tid < 64) sM[b][tid] = rm;                                     \
-    else if (tid < 128) sDl[b][tid - 64] = rm;                         \
-  } while (0)
+  for (int j = 0; j < n; ++j) {
+    dma_wait_all();
+    __syncthreads();
+    const int e = e_cur;
+    if (j + 1 < n) issue(e_nxt >> 3, (j + 1) & 1);
+    e_cur = e_nxt;
+    e_nxt = j + 2 < n ? sload_i32(U + j + 2) : 0;
+    if (!(e & mybit)) continue;
 
-  int qt_cur = 0;
-  bool inA = false, inB = false;
-  bool more = u.next(qt_cur, inA, inB);
-  PRISM_DKDV_ISSUE(more ? qt_cur : 0);
-  PRISM_DKDV_COMMIT(0);
-  __syncthreads();
-  int buf = 0;
-  while (more) {
-    const bool act = mine_is_b ? inB : inA;
-    int qt_nxt = qt_cur;
-    bool nA = false, nB = false;
-    const bool more_nxt = u.next(qt_nxt, nA, nB);
-    PRISM_DKDV_ISSUE(more_nxt ? qt_nxt : qt_cur);
-    if (act) {
+    const uint8_t* sQ = smem + (j & 1) * SB;
+    const uint8_t* sDO = sQ + T::R_KB * 1024;
+    const uint8_t* sQT = sDO + T::R_KB * 1024;
+    const uint8_t* sDOT = sQT + T::T_KB * 1024;
+    const float* sM = reinterpret_cast<const float*>(sDOT + T::T_KB * 1024);
+    const float* sDl = sM + 64;
+    f32x16 sacc = f32x16_zero(), pacc = f32x16_zero();
 #pragma unroll
-      for (int qh = 0; qh < 2; ++qh) {
-        f32x16 sacc = f32x16_zero(), pacc = f32x16_zero();
+    for (int s = 0; s < NS; ++s) {
+      const int off = (32 * qh + l32) * T::RPB + 32 * s + 16 * g;
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sQ + off), kf[s], sacc, 0, 0, 0);
+      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sDO + off), vf[s], pacc, 0, 0, 0);
+    }
+    // P and dS for query rows 32qh + 8j + 4g + i (register r = 4j + i), column = this lane's key
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_bf16x8(&sQ[buf][(32 * qh + l32) * RP + 16 * s + 8 * g]),
-                                                         kf[s], sacc, 0, 0, 0);
-          pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_bf16x8(&sDO[buf][(32 * qh + l32) * RP + 16 * s + 8 * g]),
-                                                         vf[s], pacc, 0, 0, 0);
-        }
-        // P and dS for rows q = 32qh + 8j + 4g + i (register r = 4j + i), column = this lane's key
+    for (int jj = 0; jj < 4; ++jj) {
+      const float4 m4 = *reinterpret_cast<const float4*>(sM + 32 * qh + 8 * jj + 4 * g);
+      const float4 d4 = *reinterpret_cast<const float4*>(sDl + 32 * qh + 8 * jj + 4 * g);
+      const float mv[4] = {m4.x, m4.y, m4.z, m4.w}, dl4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float4 m4 = *reinterpret_cast<const float4*>(&sM[buf][32 * qh + 8 * j + 4 * g]);
-          const float4 d4 = *reinterpret_cast<const float4*>(&sDl[buf][32 * qh + 8 * j + 4 * g]);
-          const float mv[4] = {m4.x, m4.y, m4.z, m4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 4 * j + i;
-            const float p = (kvalid && mv[i] != NINF) ? fast_exp2(__builtin_fmaf(sacc[r], a.scale_log2, -mv[i])) : 0.0f;
-            sacc[r] = p;
-            pacc[r] = p * (pacc[r] - dv4[i]);
-          }
-        }
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          const int tt = 2 * qh + t2;
-          const bf16x8 pb = b_from_acc(&sacc, t2);
-          const bf16x8 sb = b_from_acc(&pacc, t2);
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_from_t(sDOT[buf], TP, dt, tt, l32, g), pb, dv[dt], 0, 0, 0);
-            dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_from_t(sQT[buf], TP, dt, tt, l32, g), sb, dk[dt], 0, 0, 0);
-          }
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * jj + i;
+        float x = __builtin_fmaf(sacc[r], a.scale_log2, -mv[i]);
+        if (!all_valid) x += kbias;
+        const float p = fast_exp2(x);
+        sacc[r] = p;
+        pacc[r] = p * (pacc[r] - dl4[i]);
       }
     }
-    PRISM_DKDV_COMMIT(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-    more = more_nxt;
-    qt_cur = qt_nxt;
-    inA = nA;
-    inB = nB;
-  }
-#undef PRISM_DKDV_ISSUE
-#undef PRISM_DKDV_COMMIT
-  uint16_t* dkr = a.dk + hoff + key * D;
-  uint16_t* dvr = a.dv + hoff + key * D;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+    for (int t2 = 0; t2 < 2; ++t2) {
+      const int tt = 2 * qh + t2;
+      const bf16x8 pb = b_from_acc(&sacc, t2);
+      const bf16x8 sb = b_from_acc(&pacc, t2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint2 o;
-      o.x = pack_bf16(dk[dt][4 * j + 0] * a.sm_scale, dk[dt][4 * j + 1] * a.sm_scale);
-      o.y = pack_bf16(dk[dt][4 * j + 2] * a.sm_scale, dk[dt][4 * j + 3] * a.sm_scale);
-      *reinterpret_cast<uint2*>(dkr + 32 * dt + 8 * j + 4 * g) = o;
-      o.x = pack_bf16(dv[dt][4 * j + 0], dv[dt][4 * j + 1]);
-      o.y = pack_bf16(dv[dt][4 * j + 2], dv[dt][4 * j + 3]);
-      *reinterpret_cast<uint2*>(dvr + 32 * dt + 8 * j + 4 * g) = o;
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int off = (32 * dt + l32) * T::TPB + 32 * tt + 16 * g;
+        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sDOT + off), pb, dv[dt], 0, 0, 0);
+        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sQT + off), sb, dk[dt], 0, 0, 0);
+      }
     }
+  }
+
+  // add the two query-half partials in a fixed order (qh = 0 + qh = 1)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+  const int slot = w & 3;
+  if (qh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        red[((slot * 2 * NDT + dt) * 16 + r) * 64 + lane] = dk[dt][r];
+        red[((slot * 2 * NDT + NDT + dt) * 16 + r) * 64 + lane] = dv[dt][r];
+      }
+  }
+  __syncthreads();
+  if (qh == 0) {
+    uint16_t* dkr = a.dk + hoff + key * D;
+    uint16_t* dvr = a.dv + hoff + key * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dk[dt][r] += red[((slot * 2 * NDT + dt) * 16 + r) * 64 + lane];
+        dv[dt][r] += red[((slot * 2 * NDT + NDT + dt) * 16 + r) * 64 + lane];
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        uint2 o;
+        o.x = pack_bf16(dk[dt][4 * jj + 0] * a.sm_scale, dk[dt][4 * jj + 1] * a.sm_scale);
+        o.y = pack_bf16(dk[dt][4 * jj + 2] * a.sm_scale, dk[dt][4 * jj + 3] * a.sm_scale);
+        *reinterpret_cast<uint2*>(dkr + 32 * dt + 8 * jj + 4 * g) = o;
+        o.x = pack_bf16(dv[dt][4 * jj + 0], dv[dt][4 * jj + 1]);
+        o.y = pack_bf16(dv[dt][4 * jj + 2], dv[dt][4 * jj + 3]);
+        *reinterpret_cast<uint2*>(dvr + 32 * dt + 8 * jj + 4 * g) = o;
+      }
+    }
+  }
 }
 
 template <int D>
-__global__ __launch_bounds__(256, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
-  constexpr int RP = D + 8, TP = 64 + 8, NS = D / 16, NDT = D / 32, KCH = 64 * D / 8 / 256;
-  __shared__ __align__(16) uint16_t sK[2][64 * RP];
-  __shared__ __align__(16) uint16_t sV[2][64 * RP];
-  __shared__ __align__(16) uint16_t sKT[2][D * TP];
+__global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
+  using T = BwdTiles<D>;
+  constexpr int NS = D / 16, NDT = D / 32;
+  constexpr int SB = T::DQ_KB * 1024;
+  __shared__ __align__(16) uint8_t smem[2 * SB];
+  static_assert(4 * 64 * NDT * 16 * 4 <= 2 * SB, "reduction buffer must fit the stages");
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int w = (int)uniform_u32((uint32_t)tid >> 6);
+  const int qh = w & 1, tq = (w >> 1) & 1, kh = w >> 2;
   const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
-  const int64_t rowA = (int64_t)bh * a.Nt + 2 * pair;
-  Union2 u{a.cols + a.start[rowA], a.cols + a.start[rowA + 1], a.len[rowA], a.len[rowA + 1], 0, 0};
-  const bool mine_is_b = w >= 2;
+  const int32_t* U = a.ucols + a.ustart[logical];
+  const int n = a.ulen[logical];
+  const int mybit = 1 << tq;
   const int64_t hoff = (int64_t)bh * a.S * D;
-  const int64_t qrow = (int64_t)(2 * pair + (w >> 1)) * 64 + 32 * (w & 1) + l32;
-  const bool has_mask = a.kv_valid != nullptr;
   const float NINF = -__builtin_inff();
 
+  // DMA plan: wave w issues KB-instructions w, w + 8, ... (K, V, K^T)
+  uint32_t soff[T::DQ_SLOTS];
+#pragma unroll
+  for (int s = 0; s < T::DQ_SLOTS; ++s) {
+    const int i = w + 8 * s;
+    soff[s] = i < 2 * T::R_KB ? padded_src_offset<T::RW>(i % T::R_KB, lane)
+                              : padded_src_offset<T::TW>(i - 2 * T::R_KB, lane);
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int ktile, int st) {
+    const int64_t toff = hoff + (int64_t)ktile * 64 * D;
+    const void* src3[3] = {uniform_ptr(a.k + toff), uniform_ptr(a.v + toff), uniform_ptr(a.kt + toff)};
+    const uint32_t base = lds0 + (uint32_t)(st * SB);
+#pragma unroll
+    for (int s = 0; s < T::DQ_SLOTS; ++s) {
+      const int i = w + 8 * s;
+      const int which = i < T::R_KB ? 0 : i < 2 * T::R_KB ? 1 : 2;
+      if (s + 1 < T::DQ_SLOTS || i < T::DQ_KB) dma_b128(soff[s], src3[which], base + (uint32_t)i * 1024u);
+    }
+  };
+
+  int e_cur = n > 0 ? sload_i32(U) : 0;
+  int e_nxt = n > 1 ? sload_i32(U + 1) : 0;
+  if (n > 0) issue(e_cur >> 3, 0);
+
+  const int64_t qrow = (int64_t)(2 * pair + tq) * 64 + 32 * qh + l32;
   bf16x8 qf[NS], df[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     qf[s] = ld_bf16x8(a.q + hoff + qrow * D + 16 * s + 8 * g);
     df[s] = ld_bf16x8(a.do_ + hoff + qrow * D + 16 * s + 8 * g);
   }
-  const float mq = a.lse[(int64_t)bh * a.S + qrow] * kLog2e;
+  const float mq = a.m2[(int64_t)bh * a.S + qrow];
   const float dlt = a.delta[(int64_t)bh * a.S + qrow];
-  const bool qlive = mq != NINF;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    consume_regs(qf[s]);
+    consume_regs(df[s]);
+  }
+  consume_regs(mq);
+  consume_regs(dlt);
   f32x16 dq[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) dq[dt] = f32x16_zero();
 
-  uint4 rk[KCH], rv[KCH], rkt[KCH];
-  uint8_t rvalid = 1;
-#define PRISM_DQ_ISSUE(kt_)                                                 \
-  do {                                                                      \
-    const int64_t toff = hoff + (int64_t)(kt_) * 64 * D;                    \
-    stage_load<KCH>(rk, a.k + toff, tid);                                   \
-    stage_load<KCH>(rv, a.v + toff, tid);                                   \
-    stage_load<KCH>(rkt, a.kt + toff, tid);                                 \
-    if (has_mask) rvalid = a.kv_valid[(int64_t)(kt_) * 64 + lane];          \
-  } while (0)
-#define PRISM_DQ_COMMIT(b)                                                  \
-  do {                                                                      \
-    stage_rows<D, KCH, RP>(sK[b], rk, tid);                                 \
-    stage_rows<D, KCH, RP>(sV[b], rv, tid);                                 \
-    stage_trans<KCH, TP>(sKT[b], rkt, tid);                                 \
-  } while (0)
+  for (int j = 0; j < n; ++j) {
+    dma_wait_all();
+    __syncthreads();
+    const int e = e_cur;
+    if (j + 1 < n) issue(e_nxt >> 3, (j + 1) & 1);
+    e_cur = e_nxt;
+    e_nxt = j + 2 < n ? sload_i32(U + j + 2) : 0;
+    if (!(e & mybit)) continue;
 
-  int kt_cur = 0;
-  bool inA = false, inB = false;
-  bool more = u.next(kt_cur, inA, inB);
-  PRISM_DQ_ISSUE(more ? kt_cur : 0);
-  uint64_t vmask_next = has_mask ? (uint64_t)__ballot(rvalid != 0) : ~0ull;
-  PRISM_DQ_COMMIT(0);
-  __syncthreads();
-  int buf = 0;
-  while (more) {
-    const bool act = mine_is_b ? inB : inA;
-    const uint64_t vmask = vmask_next;
-    int kt_nxt = kt_cur;
-    bool nA = false, nB = false;
-    const bool more_nxt = u.next(kt_nxt, nA, nB);
-    PRISM_DQ_ISSUE(more_nxt ? kt_nxt : kt_cur);
-    if (act) {
+    const uint8_t* sK = smem + (j & 1) * SB;
+    const uint8_t* sV = sK + T::R_KB * 1024;
+    const uint8_t* sKT = sV + T::R_KB * 1024;
+    f32x16 sacc = f32x16_zero(), pacc = f32x16_zero();
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        f32x16 sacc = f32x16_zero(), pacc = f32x16_zero();
+    for (int s = 0; s < NS; ++s) {
+      const int off = (32 * kh + l32) * T::RPB + 32 * s + 16 * g;
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sK + off), qf[s], sacc, 0, 0, 0);
+      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sV + off), df[s], pacc, 0, 0, 0);
+    }
+    // element r: key 32kh + 8(r >> 2) + 4g + (r & 3), query = this lane's column
+    if (e & 4) {
+      const uint32_t bits = (uint32_t)(sload_u64(a.tmask + (e >> 3)) >> (32 * kh + 4 * g));
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_bf16x8(&sK[buf][(32 * kh + l32) * RP + 16 * s + 8 * g]),
-                                                         qf[s], sacc, 0, 0, 0);
-          pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lds_bf16x8(&sV[buf][(32 * kh + l32) * RP + 16 * s + 8 * g]),
-                                                         df[s], pacc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = 32 * kh + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = qlive && ((vmask >> kk) & 1ull);
-          const float p = ok ? fast_exp2(__builtin_fmaf(sacc[r], a.scale_log2, -mq)) : 0.0f;
-          pacc[r] = p * (pacc[r] - dlt);
-        }
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          const int tt = 2 * kh + t2;
-          const bf16x8 sb = b_from_acc(&pacc, t2);
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt)
-            dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_from_t(sKT[buf], TP, dt, tt, l32, g), sb, dq[dt], 0, 0, 0);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int b = 8 * (r >> 2) + (r & 3);
+        sacc[r] = ((bits >> b) & 1u) ? sacc[r] : NINF;
       }
     }
-    vmask_next = has_mask ? (uint64_t)__ballot(rvalid != 0) : ~0ull;
-    PRISM_DQ_COMMIT(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-    more = more_nxt;
-    kt_cur = kt_nxt;
-    inA = nA;
-    inB = nB;
-  }
-#undef PRISM_DQ_ISSUE
-#undef PRISM_DQ_COMMIT
-  uint16_t* dqr = a.dq + hoff + qrow * D;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint2 o;
-      o.x = pack_bf16(dq[dt][4 * j + 0] * a.sm_scale, dq[dt][4 * j + 1] * a.sm_scale);
-      o.y = pack_bf16(dq[dt][4 * j + 2] * a.sm_scale, dq[dt][4 * j + 3] * a.sm_scale);
-      *reinterpret_cast<uint2*>(dqr + 32 * dt + 8 * j + 4 * g) = o;
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(__builtin_fmaf(sacc[r], a.scale_log2, -mq));
+      pacc[r] = p * (pacc[r] - dlt);
     }
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      const int tt = 2 * kh + t2;
+      const bf16x8 sb = b_from_acc(&pacc, t2);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int off = (32 * dt + l32) * T::TPB + 32 * tt + 16 * g;
+        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sKT + off), sb, dq[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  // add the two key-half partials in a fixed order (kh = 0 + kh = 1)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+  const int slot = w & 3;
+  if (kh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((slot * NDT + dt) * 16 + r) * 64 + lane] = dq[dt][r];
+  }
+  __syncthreads();
+  if (kh == 0) {
+    uint16_t* dqr = a.dq + hoff + qrow * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dq[dt][r] += red[((slot * NDT + dt) * 16 + r) * 64 + lane];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        uint2 o;
+        o.x = pack_bf16(dq[dt][4 * jj + 0] * a.sm_scale, dq[dt][4 * jj + 1] * a.sm_scale);
+        o.y = pack_bf16(dq[dt][4 * jj + 2] * a.sm_scale, dq[dt][4 * jj + 3] * a.sm_scale);
+        *reinterpret_cast<uint2*>(dqr + 32 * dt + 8 * jj + 4 * g) = o;
+      }
+    }
+  }
 }
 
 // delta[row] = sum_d o[row][d] * do[row][d]: one wave per row, 4 rows per block
@@ -375,39 +407,39 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 }
 
 int prism_bsa_bwd_dkdv(const void* q, const void* qt, const void* k, const void* v, const void* do_, const void* dot,
-                       const float* lse, const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid,
-                       const int64_t* kstart, const int32_t* klen, const int32_t* kcols, float sm_scale, void* dk,
+                       const float* m2, const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid,
+                       const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk,
                        void* dv, hipStream_t stream) {
   int rc = check_common(q, k, BH, S, D, "prism_bsa_bwd_dkdv");
   if (rc) return rc;
-  PRISM_REQUIRE(qt && v && do_ && dot && lse && delta && kstart && klen && kcols && dk && dv,
+  PRISM_REQUIRE(qt && v && do_ && dot && m2 && delta && ustart && ulen && ucols && dk && dv,
                 "prism_bsa_bwd_dkdv: null pointer");
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.qt = (const uint16_t*)qt; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
-  a.do_ = (const uint16_t*)do_; a.dot = (const uint16_t*)dot; a.lse = lse; a.delta = delta; a.kv_valid = kv_valid;
-  a.start = kstart; a.len = klen; a.cols = kcols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
+  a.do_ = (const uint16_t*)do_; a.dot = (const uint16_t*)dot; a.m2 = m2; a.delta = delta; a.kv_valid = kv_valid;
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
-  if (D == 128) bsa_bwd_dkdv_kernel<128><<<blocks, 256, 0, stream>>>(a);
-  else bsa_bwd_dkdv_kernel<64><<<blocks, 256, 0, stream>>>(a);
+  if (D == 128) bsa_bwd_dkdv_kernel<128><<<blocks, 512, 0, stream>>>(a);
+  else bsa_bwd_dkdv_kernel<64><<<blocks, 512, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_bsa_bwd_dkdv");
   return PRISM_OK;
 }
 
-int prism_bsa_bwd_dq(const void* q, const void* k, const void* kt, const void* v, const void* do_, const float* lse,
-                     const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid, const int64_t* qstart,
-                     const int32_t* qlen, const int32_t* qcols, float sm_scale, void* dq, hipStream_t stream) {
+int prism_bsa_bwd_dq(const void* q, const void* k, const void* kt, const void* v, const void* do_, const float* m2,
+                     const float* delta, int BH, int64_t S, int D, const uint64_t* tile_masks, const int64_t* ustart,
+                     const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream) {
   int rc = check_common(q, k, BH, S, D, "prism_bsa_bwd_dq");
   if (rc) return rc;
-  PRISM_REQUIRE(kt && v && do_ && lse && delta && qstart && qlen && qcols && dq, "prism_bsa_bwd_dq: null pointer");
+  PRISM_REQUIRE(kt && v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq: null pointer");
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.kt = (const uint16_t*)kt; a.v = (const uint16_t*)v;
-  a.do_ = (const uint16_t*)do_; a.lse = lse; a.delta = delta; a.kv_valid = kv_valid;
-  a.start = qstart; a.len = qlen; a.cols = qcols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
+  a.do_ = (const uint16_t*)do_; a.m2 = m2; a.delta = delta; a.tmask = tile_masks;
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
-  if (D == 128) bsa_bwd_dq_kernel<128><<<blocks, 256, 0, stream>>>(a);
-  else bsa_bwd_dq_kernel<64><<<blocks, 256, 0, stream>>>(a);
+  if (D == 128) bsa_bwd_dq_kernel<128><<<blocks, 512, 0, stream>>>(a);
+  else bsa_bwd_dq_kernel<64><<<blocks, 512, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_bsa_bwd_dq");
   return PRISM_OK;
 }

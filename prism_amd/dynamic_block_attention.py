@@ -77,7 +77,12 @@ class _Plan:
         self.qstart, self.qlen = ops.tile_rows(sel["ntiles"], lay.block_id_of_tile, B * H, lay.Nt, lay.N_b,
                                                sel["tcap"], self.tile_count if skip else None)
         self.qcols = sel["tiles"].view(-1)
+        # pair unions of the per-query-tile key lists (forward, dQ) and the key
+        # validity words of padded key tiles
+        self.tmasks = ops.tile_masks(self.kv_valid) if masked else None
+        self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks)
         self.klists = None
+        self.kunion = None
 
     def sum_lens(self) -> int:
         """Executed (query tile, key tile) pairs (host sync)."""
@@ -91,8 +96,7 @@ class _DynBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _Plan, sm_scale: float):
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.kv_valid, plan.qstart, plan.qlen, plan.qcols,
-                                sm_scale)
+        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.tmasks, plan.qunion, sm_scale)
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
@@ -109,11 +113,12 @@ class _DynBSA(torch.autograd.Function):
         dot = ops.transpose_tiles(do_re)
         qt = ops.transpose_tiles(plan.q_re)
         kt = ops.transpose_tiles(plan.k_re)
-        if plan.klists is None:
+        if plan.kunion is None:
             plan.klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, plan.B * plan.H, lay.Nt)
-        dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, qt, plan.k_re, kt, plan.v_re, do_re, dot, lse, delta,
-                                          plan.kv_valid, (plan.qstart, plan.qlen, plan.qcols), plan.klists,
-                                          ctx.sm_scale)
+            plan.kunion = ops.pair_union(*plan.klists, lay.Nt)
+        m2 = ops.lse_to_m2(lse)
+        dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, qt, plan.k_re, kt, plan.v_re, do_re, dot, m2, delta,
+                                          plan.kv_valid, plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale)
         tq, tk, tv = ctx.in_dtypes
         dq = ops.scatter_rows(dq_re, lay, tq)
         dk = ops.scatter_rows(dk_re, lay, tk)

@@ -324,36 +324,76 @@ def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tenso
 
 
 # ------------------------------------------------------------------ attention
+def pair_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt: int,
+               tmasks: Optional[torch.Tensor] = None):
+    """Sorted union of the lists of each row pair (2p, 2p+1) with membership
+    flags (entry = tile << 3 | partial << 2 | in_second << 1 | in_first).
+    Returns (ustart [rows/2] int64, ulen [rows/2] int32, ucols int32)."""
+    _cuda(start, length, cols, tmasks)
+    rows = start.numel()
+    pairs = rows // 2
+    dev = start.device
+    ucap = int(Nt)
+    ustart = torch.empty(pairs, device=dev, dtype=torch.int64)
+    ulen = torch.empty(pairs, device=dev, dtype=torch.int32)
+    ucols = torch.empty(max(pairs * ucap, 1), device=dev, dtype=torch.int32)
+    _call("prism_pair_union", _p(start), _p(length), _p(cols), rows, int(Nt), _p(tmasks), ucap, _p(ustart),
+          _p(ulen), _p(ucols), _stream())
+    return ustart, ulen, ucols
+
+
+def tile_masks(valid: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """[Nt*64] uint8/bool tile-order validity -> [Nt] 64-bit masks (int64 storage)."""
+    if valid is None:
+        return None
+    _cuda(valid)
+    v = _u8(valid)
+    Nt = v.numel() // 64
+    out = torch.empty(Nt, device=v.device, dtype=torch.int64)
+    _call("prism_tile_masks", _p(v), Nt, _p(out), _stream())
+    return out
+
+
+def lse_to_m2(lse: torch.Tensor) -> torch.Tensor:
+    _cuda(lse)
+    lse = lse.contiguous().float()
+    out = torch.empty_like(lse)
+    _call("prism_lse_to_m2", _p(lse), lse.numel(), _p(out), _stream())
+    return out
+
+
 def _bf16(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.dtype != torch.bfloat16:
         raise TypeError(f"{name} must be bfloat16 (MFMA kernels)")
     return t.contiguous()
 
 
-def bsa_fwd(q, k, vt, kv_valid, qstart, qlen, qcols, sm_scale: float):
-    """q, k [B,H,S,D] bf16 tile order, vt [B,H,S/64,D,64] -> (o bf16, lse fp32 natural)."""
-    _cuda(q, k, vt, kv_valid, qstart, qlen, qcols)
+def bsa_fwd(q, k, vt, tmasks, qunion, sm_scale: float):
+    """q, k [B,H,S,D] bf16 tile order, vt [B,H,S/64,D,64]; qunion = pair_union
+    of the per-query-tile key lists -> (o bf16, lse fp32 natural)."""
+    _cuda(q, k, vt, tmasks)
     q, k, vt = _bf16(q, "q"), _bf16(k, "k"), _bf16(vt, "vt")
     B, H, S, D = q.shape
+    ustart, ulen, ucols = qunion
     o = torch.empty_like(q)
     lse = torch.empty((B, H, S), device=q.device, dtype=torch.float32)
-    _call("prism_bsa_fwd", _p(q), _p(k), _p(vt), B * H, S, D, _p(kv_valid), _p(qstart), _p(qlen), _p(qcols),
-              float(sm_scale), _p(o), _p(lse), _stream())
+    _call("prism_bsa_fwd", _p(q), _p(k), _p(vt), B * H, S, D, _p(tmasks), _p(ustart), _p(ulen), _p(ucols),
+          float(sm_scale), _p(o), _p(lse), _stream())
     return o, lse
 
 
-def bsa_bwd(q, qt, k, kt, v, do, dot, lse, delta, kv_valid, qlists, klists, sm_scale: float):
-    """Backward over tile-order tensors; returns dq, dk, dv (bf16, tile order)."""
-    _cuda(q, qt, k, kt, v, do, dot, lse, delta, kv_valid)
+def bsa_bwd(q, qt, k, kt, v, do, dot, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float):
+    """Backward over tile-order tensors; qunion / kunion = pair unions of the
+    per-query-tile key lists and of the per-key-tile query lists.  Returns
+    dq, dk, dv (bf16, tile order)."""
+    _cuda(q, qt, k, kt, v, do, dot, m2, delta, kv_valid, tmasks)
     B, H, S, D = q.shape
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    qstart, qlen, qcols = qlists
-    kstart, klen, kcols = klists
     s = _stream()
-    _call("prism_bsa_bwd_dkdv", _p(q), _p(qt), _p(k), _p(v), _p(do), _p(dot), _p(lse), _p(delta), B * H, S, D,
-              _p(kv_valid), _p(kstart), _p(klen), _p(kcols), float(sm_scale), _p(dk), _p(dv), s)
-    _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(kt), _p(v), _p(do), _p(lse), _p(delta), B * H, S, D,
-              _p(kv_valid), _p(qstart), _p(qlen), _p(qcols), float(sm_scale), _p(dq), s)
+    _call("prism_bsa_bwd_dkdv", _p(q), _p(qt), _p(k), _p(v), _p(do), _p(dot), _p(m2), _p(delta), B * H, S, D,
+          _p(kv_valid), _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), float(sm_scale), _p(dk), _p(dv), s)
+    _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(kt), _p(v), _p(do), _p(m2), _p(delta), B * H, S, D,
+          _p(tmasks), _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), float(sm_scale), _p(dq), s)
     return dq, dk, dv

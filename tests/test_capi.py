@@ -75,4 +75,4 @@ def test_invalid_arguments_raise_without_gpu():
         _lib.call("prism_bsa_fwd", None, None, None, 1, 64, 64, None, None, None, None, 0.1, None, None, None)
     with pytest.raises(ValueError, match="head_dim"):
         _lib.call("prism_bsa_fwd", 1, 1, 1, 1, 64, 96, None, 1, 1, 1, 0.1, 1, 1, None)
-    assert _lib.load().prism_abi_version() == 1
+    assert _lib.load().prism_abi_version() == 2

@@ -270,6 +270,39 @@ def test_transpose_lists_bitexact(case):
         assert np.array_equal(kc[i, : kl[i]], ref_c[i, : kl[i]])
 
 
+def test_pair_union_bitexact(case):
+    """prism_pair_union on the plan's query-tile lists (with key-validity
+    words) and on the transposed key-tile lists vs the oracle's set union."""
+    from prism_amd import ops, plan_dynamic
+    valid = case["valid"] if case["pad"] else None
+    B, H, S, D = case["q"].shape
+    plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
+                        sparsity=0.6, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
+    Nt = plan.lay.Nt
+    tm = None if plan.tmasks is None else host(plan.tmasks).view(np.uint64)
+    if valid is not None:
+        assert np.array_equal(tm, O.tile_masks(host(plan.kv_valid)))
+    klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, Nt)
+    for lists, masks in (((plan.qstart, plan.qlen, plan.qcols), tm), (klists, None)):
+        st, ln, cl = (host(t) for t in lists)
+        ustart, ulen, ucols = ops.pair_union(*lists, Nt, None if masks is None else plan.tmasks)
+        ref = O.pair_union(st, ln, cl, Nt, masks)
+        ulen, ustart, ucols = host(ulen), host(ustart), host(ucols)
+        assert len(ref) == len(ulen)
+        for p, r in enumerate(ref):
+            assert ulen[p] == len(r)
+            assert np.array_equal(ucols[ustart[p]: ustart[p] + ulen[p]], r)
+
+
+def test_lse_to_m2():
+    from prism_amd import ops
+    x = torch.tensor([0.0, -1.5, 3.25, -float("inf"), 80.0], device=DEV)
+    m2 = host(ops.lse_to_m2(x))
+    ref = np.array([0.0, -1.5, 3.25, np.inf, 80.0], np.float32) * np.float32(1.4426950408889634)
+    ref[3] = np.inf
+    assert np.array_equal(m2, ref.astype(np.float32))
+
+
 def _tol(got, ref, what):
     """max-abs 2e-2, mean-abs 2e-3 (bf16 vs float64)."""
     err = np.abs(got.astype(np.float64) - ref)
@@ -287,7 +320,7 @@ def test_attention_fwd_bwd_tolerance(case):
     sm = 1 / math.sqrt(D)
     plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
                         sparsity=0.6, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
-    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.kv_valid, plan.qstart, plan.qlen, plan.qcols, sm)
+    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.tmasks, plan.qunion, sm)
     qf = O.bf16_bits_to_f32(host(plan.q_re)).reshape(B * H, S, D)
     kf = O.bf16_bits_to_f32(host(plan.k_re)).reshape(B * H, S, D)
     vf = O.bf16_bits_to_f32(host(plan.v_re)).reshape(B * H, S, D)
@@ -307,9 +340,10 @@ def test_attention_fwd_bwd_tolerance(case):
     delta = torch.empty((B, H, S), device=DEV, dtype=torch.float32)
     ops._lib.call("prism_bwd_preprocess", o.data_ptr(), do_t.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
     klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, plan.lay.Nt)
+    kunion = ops.pair_union(*klists, plan.lay.Nt)
     dq, dk, dv = ops.bsa_bwd(plan.q_re, ops.transpose_tiles(plan.q_re), plan.k_re, ops.transpose_tiles(plan.k_re),
-                             plan.v_re, do_t, ops.transpose_tiles(do_t), lse, delta, plan.kv_valid,
-                             (plan.qstart, plan.qlen, plan.qcols), klists, sm)
+                             plan.v_re, do_t, ops.transpose_tiles(do_t), ops.lse_to_m2(lse), delta, plan.kv_valid,
+                             plan.tmasks, plan.qunion, kunion, sm)
     dof = O.bf16_bits_to_f32(do).reshape(B * H, S, D)
     dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, og, dof, lse_ref, *lists, kv, sm)
     for name, g, r in (("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):

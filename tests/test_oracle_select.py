@@ -367,3 +367,40 @@ def test_skip_padded_queries_only_empties_fully_padded_tiles():
     assert empty.any() and (~empty).any()
     assert np.all(skip["qlen"][empty] == 0)
     assert np.array_equal(skip["qlen"][~empty], full["qlen"][~empty])
+
+
+def test_pair_union_brute_force():
+    """oracle.pair_union vs Python set arithmetic on random sorted lists
+    (empty rows, identical rows, disjoint rows) and tile masks."""
+    rng = np.random.default_rng(5)
+    Nt, rows = 40, 12
+    lists = []
+    for r in range(rows):
+        kind = r % 4
+        if kind == 0:
+            lists.append([])
+        elif kind == 1 and r > 0:
+            lists.append(list(lists[-1]))
+        else:
+            lists.append(sorted(rng.choice(Nt, size=int(rng.integers(1, Nt)), replace=False).tolist()))
+    cap = Nt
+    start = np.arange(rows, dtype=np.int64) * cap
+    length = np.array([len(x) for x in lists], np.int32)
+    cols = np.full(rows * cap, -7, np.int32)
+    for r, x in enumerate(lists):
+        cols[r * cap: r * cap + len(x)] = x
+    valid = (rng.random(Nt * O.TILE) > 0.02).astype(np.uint8)
+    valid[: 5 * O.TILE] = 1
+    masks = O.tile_masks(valid)
+    for t in range(Nt):
+        want = sum(1 << j for j in range(O.TILE) if valid[t * O.TILE + j])
+        assert int(masks[t]) == want
+    got = O.pair_union(start, length, cols, Nt, masks)
+    assert len(got) == rows // 2
+    for p in range(rows // 2):
+        a, b = set(lists[2 * p]), set(lists[2 * p + 1])
+        want = []
+        for t in sorted(a | b):
+            partial = int(masks[t]) != (1 << 64) - 1
+            want.append(t * 8 + (4 if partial else 0) + (2 if t in b else 0) + (1 if t in a else 0))
+        assert got[p].tolist() == want
