@@ -273,6 +273,8 @@ def main():
     density = sum_lens / (B * H * Nt * Nt)
     n_qvalid = int((plan.tile_count > 0).sum().item()) if plan.tile_count is not None else Nt
     density_valid = sum_lens / (B * H * n_qvalid * Nt)  # over query tiles holding a valid token
+    # fraction of (wave, key tile) slots of the paired-tile kernels that do math
+    union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
     fl = 64 * 64 * D * sum_lens  # one 64x64xD product over all kept tile pairs
     kept_flops = 14 * fl          # FA convention: fwd 4, bwd 10
 
@@ -343,7 +345,7 @@ def main():
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(gp),
                    "audio_tokens": CONFIGS[args.config][4], "topk": inp["topk"], "cdf_threshold": cdf,
                    "sparsity": sparsity, "N_b": Nb, "sum_lens": sum_lens, "density": round(density, 4),
-                   "density_valid_q": round(density_valid, 4),
+                   "density_valid_q": round(density_valid, 4), "pair_union_efficiency": round(union_eff, 4),
                    "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3),
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},

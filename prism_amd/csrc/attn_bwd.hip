@@ -25,7 +25,8 @@
 //    halves of the contracted dimension, so every wave holds half-size
 //    partial accumulators; the two partials are added in a fixed order
 //    through LDS at the end (deterministic);
-//  * workgroup ids are remapped per XCD (contiguous zones per L2).
+//  * workgroup ids are remapped per XCD (xcd_group_remap: runs of
+//    neighbouring pairs per L2, one head region at a time GPU-wide).
 // dK/dV: wave w owns keys [32 kh, 32 kh + 32) of tile 2p + tk and query rows
 // [32 qh, 32 qh + 32) of every listed query tile (kh = w & 1, tk = (w >> 1) & 1,
 // qh = w >> 2).  S = Q K^T and dP = dO V^T keep one key per lane column, so P
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
   const int kh = w & 1, tk = (w >> 1) & 1, qh = w >> 2;
-  const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int logical = xcd_group_remap<32>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
@@ -244,7 +245,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
   const int qh = w & 1, tq = (w >> 1) & 1, kh = w >> 2;
-  const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int logical = xcd_group_remap<32>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];

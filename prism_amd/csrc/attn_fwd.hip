@@ -27,9 +27,10 @@
 //    16-byte LDS load.
 //  * key validity: union entries flag tiles that contain padding; only those
 //    load their 64-bit validity word and mask.
-//  * workgroup ids are remapped so that each XCD (own L2) processes a
-//    contiguous range of zones: neighbouring query tiles select overlapping
-//    key tiles, which then hit in that XCD's L2.
+//  * workgroup ids are remapped (xcd_group_remap) so that each XCD (own L2)
+//    processes runs of neighbouring tile pairs, whose lists overlap, while the
+//    whole GPU sweeps one head region at a time (K/V stay in the Infinity
+//    Cache).
 #include "common.h"
 #include "mfma.h"
 #include "tile_dma.h"
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
-  const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int logical = xcd_group_remap<64>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];

@@ -75,10 +75,17 @@ __device__ __forceinline__ float xor32_add(float x) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
-// L2).  Map the hardware id so that XCD x processes the contiguous logical
-// range [x*n/8, (x+1)*n/8) (a bijection on [0, n)).
-__device__ __forceinline__ int xcd_remap(int bid, int n) {
-  const int xcd = bid & 7, slot = bid >> 3;
-  const int q = n >> 3, r = n & 7;
-  return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+// 4 MB L2) in increasing id order, so the resident workgroups at any moment
+// are a window of consecutive ids.  Map hardware ids in chunks of 8*G: inside
+// a chunk, XCD x takes the G consecutive logical ids [x*G, (x+1)*G) (tiles
+// that select overlapping lists share one L2), and the chunks advance through
+// the logical order together, so the whole GPU works on one neighbourhood of
+// one head at a time (its K/V stay resident in the 256 MB Infinity Cache).
+// Ids past the last full chunk map to themselves; a bijection on [0, n).
+template <int G>
+__device__ __forceinline__ int xcd_group_remap(int bid, int n) {
+  const int full = n / (8 * G) * (8 * G);
+  if (bid >= full) return bid;
+  const int chunk = bid / (8 * G), xcd = bid & 7, slot = (bid >> 3) % G;
+  return chunk * 8 * G + xcd * G + slot;
 }
