@@ -287,7 +287,6 @@ def main():
         "prism_zone_stats": H * Sp * D * 2 + plan.lay.Nz * 25 * D * 4,
         "prism_a2v_norms": S * inp["res"].shape[-1] * 2 + S * 2,
         "prism_gather_pool": (4 * 2 * X + X) / 4,  # q, k, v, dO: read + write rows; dO also reads O
-        "prism_transpose_tiles": 2 * X,
         "prism_scatter_rows": 2 * X,
         "prism_block_scores": 2 * B * H * Nb * D * 4 + B * H * Nb * Nb * 4,
         "prism_select_tiles": B * H * Nb * Nb * 4 + 4 * nnz_tiles + 4 * B * H * Nb,

@@ -103,14 +103,6 @@ int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, 
                       void* out_rows, float* block_mean, int32_t* block_count, int32_t* tile_count,
                       uint8_t* valid_re, const void* dot_with, float* rowdot, hipStream_t stream);
 
-/* Transposed 64-row tiles: in [BH,S,D] bf16 -> out [BH,S/64,D,64] bf16 (the
- * operand layout of the MFMA kernels for V in the forward and Q, K, dO in the
- * backward; no reference counterpart, the Triton kernels transpose in SRAM).
- * Inside each group of 16 positions of an output row, position j holds key
- * 4*(j/8) + j%4 + 8*((j/4)%2) of the group (the k-slot order of
- * v_mfma_f32_32x32x16_bf16 operands built from a 32x32 accumulator). */
-int prism_transpose_tiles(const void* in_rows, int BH, int64_t S, int D, void* out_t, hipStream_t stream);
-
 /* o_re.index_select(2, inv_idx) (dynamic_block_attention.py:329): tile-order
  * bf16 rows -> THW order rows of out_dtype. */
 int prism_scatter_rows(const void* in_rows, int B, int H, int64_t S, int D, const int64_t* shape_ids, int T,
@@ -185,12 +177,11 @@ int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
 /* attn_fwd_bsa_varlen_triton (bsa_interface.py:328-385) with
  * _attn_fwd_bsa_varlen_align (flash_attn_bsa_varlen_mask.py:191-319), chunk 64.
  * S must be a multiple of 128 (query tiles are processed in pairs).
- * q, k: [BH,S,D] bf16 tile order; vt: [BH,S/64,D,64] bf16 transposed tiles
- * (prism_transpose_tiles); ustart/ulen/ucols: prism_pair_union of the
+ * q, k, v: [BH,S,D] bf16 tile order; ustart/ulen/ucols: prism_pair_union of the
  * per-query-tile key lists with the same tile_masks (prism_tile_masks of the
  * key validity, or NULL when no key is padded).  o: [BH,S,D] bf16; lse: [BH,S] fp32 natural log (-inf for rows
  * without a valid key; their o is 0). */
-int prism_bsa_fwd(const void* q, const void* k, const void* vt, int BH, int64_t S, int D, const uint64_t* tile_masks,
+int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S, int D, const uint64_t* tile_masks,
                   const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* o,
                   float* lse, hipStream_t stream);
 
@@ -200,21 +191,21 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 
 /* dK, dV of attn_bwd_bsa_varlen_triton (bsa_interface.py:387-487;
  * _attn_bwd_dkdv_bsa_varlen_wrapper, flash_attn_bsa_varlen_mask.py:562-704).
- * qt, dot: transposed tiles of q and dO; m2 from prism_lse_to_m2; delta from
+ * q, k, v, do_: [BH,S,D] bf16 tile order; m2 from prism_lse_to_m2; delta from
  * prism_gather_pool or prism_bwd_preprocess; kv_valid: [S] uint8 tile order
  * or NULL; ustart/ulen/ucols: prism_pair_union of the per-key-tile query
- * lists of prism_transpose_lists (tile_masks NULL). */
-int prism_bsa_bwd_dkdv(const void* q, const void* qt, const void* k, const void* v, const void* do_, const void* dot,
-                       const float* m2, const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid,
-                       const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk,
-                       void* dv, hipStream_t stream);
+ * lists of prism_transpose_lists (tile_masks NULL).  dk, dv: [BH,S,D] bf16. */
+int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
+                       const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid, const int64_t* ustart,
+                       const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk, void* dv,
+                       hipStream_t stream);
 
 /* dQ of attn_bwd_bsa_varlen_triton (bsa_interface.py:489-523;
  * _attn_bwd_dq_bsa_varlen_align_wrapper, flash_attn_bsa_varlen_mask.py:879-1014).
- * kt: transposed tiles of k; lists and tile_masks as for prism_bsa_fwd. */
-int prism_bsa_bwd_dq(const void* q, const void* k, const void* kt, const void* v, const void* do_, const float* m2,
-                     const float* delta, int BH, int64_t S, int D, const uint64_t* tile_masks, const int64_t* ustart,
-                     const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream);
+ * Lists and tile_masks as for prism_bsa_fwd; dq: [BH,S,D] bf16. */
+int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
+                     int BH, int64_t S, int D, const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen,
+                     const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream);
 
 #ifdef __cplusplus
 }

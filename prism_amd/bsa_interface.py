@@ -79,8 +79,7 @@ def attn_fwd_bsa_varlen(q, k, v, sm_scale, block_indices, block_indices_lens, ch
     Nt = q.shape[2] // 64
     tm = ops.tile_masks(ops._u8(kv_valid_mask))
     qunion = ops.pair_union(qstart, qlen, qcols, Nt, tm)
-    vt = ops.transpose_tiles(v)
-    return ops.bsa_fwd(q, k, vt, tm, qunion, sm_scale)
+    return ops.bsa_fwd(q, k, v, tm, qunion, sm_scale)
 
 
 def create_indices_k_from_indices_q_varlen(block_indices: torch.Tensor, N_cols_mask: int):
@@ -117,8 +116,7 @@ def attn_bwd_bsa_varlen(do, q, k, v, o, dq, dk, dv, sm_scale, lse, block_indices
     qunion = ops.pair_union(qstart, qlen, qcols, Nt, tm)
     kunion = ops.pair_union(*klists, Nt)
     m2 = ops.lse_to_m2(lse)
-    g_q, g_k, g_v = ops.bsa_bwd(q, ops.transpose_tiles(q), k, ops.transpose_tiles(k), v, do, ops.transpose_tiles(do),
-                                m2, delta, kv, tm, qunion, kunion, sm_scale)
+    g_q, g_k, g_v = ops.bsa_bwd(q, k, v, do, m2, delta, kv, tm, qunion, kunion, sm_scale)
     dq.copy_(g_q)
     dk.copy_(g_k)
     dv.copy_(g_v)

@@ -9,18 +9,20 @@
 //   inner loop :479-541).  Both passes are deterministic (no atomics), as in the
 //   reference.
 //
-// Layouts (per head, tile order): Q, K, V, dO row-major [S][D]; Q^T, K^T, dO^T
-// as transposed 64-row tiles [Nt][D][64] with keys in MFMA k-slot order
-// (prism_transpose_tiles).  m2 = lse * log2(e) with rows that saw no valid key
-// at +inf (prism_lse_to_m2).
+// Layouts (per head, tile order): Q, K, V, dO row-major [S][D]; m2 = lse *
+// log2(e) with rows that saw no valid key at +inf (prism_lse_to_m2).
 //
 // MI355X design, shared by both kernels:
 //  * one workgroup of 8 waves per PAIR of tiles (2p, 2p+1), one workgroup per
 //    CU (two waves per SIMD), walking the sorted union of the two tiles' lists
 //    (prism_pair_union);
-//  * the operand tiles of the next list entry are copied HBM -> LDS by
-//    global_load_lds_dwordx4 while the current entry is multiplied
-//    (double-buffered stages, one barrier per entry, no VGPR staging);
+//  * the operand tiles of list entry j + 2 are copied HBM -> LDS by
+//    global_load_lds_dwordx4 while entry j is multiplied (three stages, one
+//    barrier per entry, no VGPR staging);
+//  * all operands come from row-major tiles: row reads (ds_read_b128) for the
+//    S / dP products, transposing reads (ds_read_b64_tr_b16) for the products
+//    that contract over the tile's rows (see RowTile), so no transposed
+//    copies of Q, K or dO are made;
 //  * the eight waves split the work of each (tile, tile) product in two
 //    halves of the contracted dimension, so every wave holds half-size
 //    partial accumulators; the two partials are added in a fixed order
@@ -43,7 +45,7 @@
 namespace {
 
 struct BwdArgs {
-  const uint16_t *q, *qt, *k, *kt, *v, *do_, *dot;
+  const uint16_t *q, *k, *v, *do_;
   const float* m2;          // [BH, S] base-2 row max (lse * log2 e, +inf for empty rows)
   const float* delta;       // [BH, S]
   const uint8_t* kv_valid;  // [S] tile order or null (dK/dV)
@@ -58,28 +60,40 @@ struct BwdArgs {
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kStages = 3;  // entry j + 2 is copied while entry j is multiplied
 
 template <int D>
 struct BwdTiles {
-  static constexpr int RW = 2 * D, RPB = RW + 16, R_KB = 64 * RPB / 1024;  // row-major [64][D]
-  static constexpr int TW = 128, TPB = TW + 16, T_KB = D * TPB / 1024;     // transposed [D][64]
-  static_assert(64 * RPB % 1024 == 0 && D * TPB % 1024 == 0, "tiles must fill whole KB");
-  // dQ stage: K, V (row-major), K^T
-  static constexpr int DQ_KB = 2 * R_KB + T_KB;
-  static constexpr int DQ_SLOTS = (DQ_KB + 7) / 8;
-  // dK/dV stage: Q, dO (row-major), Q^T, dO^T, then m2 and delta rows (256 B each)
-  static constexpr int DKDV_KB = 2 * R_KB + 2 * T_KB;
-  static constexpr int DKDV_BYTES = DKDV_KB * 1024 + 512;
-  static constexpr int DKDV_SLOTS = (DKDV_KB + 7) / 8;
+  using RT = RowTile<D>;
+  // dQ stage: K, V; dK/dV stage: Q, dO, then the m2 and delta rows (256 B each)
+  static constexpr int DQ_STAGE = 2 * RT::BYTES;
+  static constexpr int DKDV_STAGE = 2 * RT::BYTES + 512;
+  static constexpr int SLOTS = 2 * RT::KB / 8;  // KB-instructions per wave and stage
+  static_assert(2 * RT::KB % 8 == 0, "stage must split evenly over 8 waves");
+  static constexpr int NDT = D / 32;
+  static constexpr int DKDV_RED = 4 * 64 * 2 * NDT * 16 * 4;  // qh = 1 partials of dK and dV
+  static constexpr int DQ_RED = 4 * 64 * NDT * 16 * 4;
+  static constexpr int DKDV_LDS = kStages * DKDV_STAGE > DKDV_RED ? kStages * DKDV_STAGE : DKDV_RED;
+  static constexpr int DQ_LDS = kStages * DQ_STAGE > DQ_RED ? kStages * DQ_STAGE : DQ_RED;
+  static_assert(DKDV_LDS <= 160 * 1024 && DQ_LDS <= 160 * 1024, "LDS budget");
 };
+
+// Wait for the copy of the entry about to be used: with three stages the copy
+// of the next entry (issued one iteration later) may stay in flight; `cnt` is
+// the number of copy instructions this wave issues per entry.
+template <int CNT>
+__device__ __forceinline__ void stage_wait(bool next_in_flight) {
+  if (next_in_flight) dma_wait_le<CNT>();
+  else dma_wait_le<0>();
+}
 
 template <int D>
 __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   using T = BwdTiles<D>;
-  constexpr int NS = D / 16, NDT = D / 32;
-  constexpr int SB = T::DKDV_BYTES;
-  __shared__ __align__(16) uint8_t smem[2 * SB];
-  static_assert(4 * 64 * 2 * NDT * 16 * 4 <= 2 * SB, "reduction buffer must fit the stages");
+  using RT = typename T::RT;
+  constexpr int P = RT::P, NS = D / 16, NDT = D / 32;
+  constexpr int SB = T::DKDV_STAGE;
+  __shared__ __align__(16) uint8_t smem[T::DKDV_LDS];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
@@ -93,36 +107,38 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   const float* m2h = a.m2 + (int64_t)bh * a.S;
   const float* dlh = a.delta + (int64_t)bh * a.S;
 
-  // DMA plan: wave w issues KB-instructions w, w + 8, ... (Q, dO, Q^T, dO^T);
+  // DMA plan: wave w issues KB-instructions w, w + 8, ... (Q then dO);
   // wave 7 also copies the m2 row and wave 6 the delta row of the entry.
-  uint32_t soff[T::DKDV_SLOTS];
+  uint32_t soff[T::SLOTS];
 #pragma unroll
-  for (int s = 0; s < T::DKDV_SLOTS; ++s) {
-    const int i = w + 8 * s;
-    soff[s] = i < 2 * T::R_KB ? padded_src_offset<T::RW>(i % T::R_KB, lane)
-                              : padded_src_offset<T::TW>((i - 2 * T::R_KB) % T::T_KB, lane);
-  }
+  for (int s = 0; s < T::SLOTS; ++s) soff[s] = RT::src_offset((w + 8 * s) % RT::KB, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int qtile, int st) {
     const int64_t toff = hoff + (int64_t)qtile * 64 * D;
-    const void* src4[4] = {uniform_ptr(a.q + toff), uniform_ptr(a.do_ + toff), uniform_ptr(a.qt + toff),
-                           uniform_ptr(a.dot + toff)};
+    const void* qb = uniform_ptr(a.q + toff);
+    const void* db = uniform_ptr(a.do_ + toff);
     const uint32_t base = lds0 + (uint32_t)(st * SB);
 #pragma unroll
-    for (int s = 0; s < T::DKDV_SLOTS; ++s) {
+    for (int s = 0; s < T::SLOTS; ++s) {
       const int i = w + 8 * s;
-      const int which = i < T::R_KB ? 0 : i < 2 * T::R_KB ? 1 : i < 2 * T::R_KB + T::T_KB ? 2 : 3;
-      if (s + 1 < T::DKDV_SLOTS || i < T::DKDV_KB) dma_b128(soff[s], src4[which], base + (uint32_t)i * 1024u);
+      dma_b128(soff[s], i < RT::KB ? qb : db, base + (uint32_t)i * 1024u);
     }
     if (w >= 6) {
       const float* rowsrc = (w == 7 ? m2h : dlh) + (int64_t)qtile * 64;
-      dma_b32((uint32_t)lane * 4u, uniform_ptr(rowsrc), base + T::DKDV_KB * 1024u + (w == 7 ? 0u : 256u));
+      dma_b32((uint32_t)lane * 4u, uniform_ptr(rowsrc), base + 2u * RT::BYTES + (w == 7 ? 0u : 256u));
     }
   };
+  RowOperand rop;                // Q / dO rows 32 qh + l32
+  rop.init<P>(32 * qh, l32, g);
+  TrOperand top;                 // Q^T / dO^T over query rows 32 qh .. 32 qh + 31
+  top.init<P>(32 * qh, lane);
 
-  int e_cur = n > 0 ? sload_i32(U) : 0;
-  int e_nxt = n > 1 ? sload_i32(U + 1) : 0;
-  if (n > 0) issue(e_cur >> 3, 0);
+  // entries j .. j + 2 (wave-uniform ring)
+  int e0 = n > 0 ? sload_i32(U) : 0;
+  int e1 = n > 1 ? sload_i32(U + 1) : 0;
+  int e2 = n > 2 ? sload_i32(U + 2) : 0;
+  if (n > 0) issue(e0 >> 3, 0);
+  if (n > 1) issue(e1 >> 3, 1);
 
   const int64_t key = (int64_t)(2 * pair + tk) * 64 + 32 * kh + l32;
   bf16x8 kf[NS], vf[NS];
@@ -144,27 +160,28 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) { dk[dt] = f32x16_zero(); dv[dt] = f32x16_zero(); }
 
+  int st = 0;  // stage of entry j
   for (int j = 0; j < n; ++j) {
-    dma_wait_all();
+    if (w >= 6) stage_wait<T::SLOTS + 1>(j + 1 < n);
+    else stage_wait<T::SLOTS>(j + 1 < n);
     __syncthreads();
-    const int e = e_cur;
-    if (j + 1 < n) issue(e_nxt >> 3, (j + 1) & 1);
-    e_cur = e_nxt;
-    e_nxt = j + 2 < n ? sload_i32(U + j + 2) : 0;
+    const int e = e0;
+    if (j + 2 < n) issue(e2 >> 3, st == 0 ? 2 : st - 1);
+    e0 = e1;
+    e1 = e2;
+    e2 = j + 3 < n ? sload_i32(U + j + 3) : 0;
+    const uint8_t* sQ = smem + st * SB;
+    st = st == 2 ? 0 : st + 1;
     if (!(e & mybit)) continue;
 
-    const uint8_t* sQ = smem + (j & 1) * SB;
-    const uint8_t* sDO = sQ + T::R_KB * 1024;
-    const uint8_t* sQT = sDO + T::R_KB * 1024;
-    const uint8_t* sDOT = sQT + T::T_KB * 1024;
-    const float* sM = reinterpret_cast<const float*>(sDOT + T::T_KB * 1024);
+    const uint8_t* sDO = sQ + RT::BYTES;
+    const float* sM = reinterpret_cast<const float*>(sQ + 2 * RT::BYTES);
     const float* sDl = sM + 64;
     f32x16 sacc = f32x16_zero(), pacc = f32x16_zero();
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const int off = (32 * qh + l32) * T::RPB + 32 * s + 16 * g;
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sQ + off), kf[s], sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sDO + off), vf[s], pacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sQ, s), kf[s], sacc, 0, 0, 0);
+      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sDO, s), vf[s], pacc, 0, 0, 0);
     }
     // P and dS for query rows 32qh + 8j + 4g + i (register r = 4j + i), column = this lane's key
 #pragma unroll
@@ -184,14 +201,12 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
     }
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      const int tt = 2 * qh + t2;
       const bf16x8 pb = b_from_acc(&sacc, t2);
       const bf16x8 sb = b_from_acc(&pacc, t2);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const int off = (32 * dt + l32) * T::TPB + 32 * tt + 16 * g;
-        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sDOT + off), pb, dv[dt], 0, 0, 0);
-        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sQT + off), sb, dk[dt], 0, 0, 0);
+        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sDO, t2, dt), pb, dv[dt], 0, 0, 0);
+        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sQ, t2, dt), sb, dk[dt], 0, 0, 0);
       }
     }
   }
@@ -237,10 +252,10 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
 template <int D>
 __global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
   using T = BwdTiles<D>;
-  constexpr int NS = D / 16, NDT = D / 32;
-  constexpr int SB = T::DQ_KB * 1024;
-  __shared__ __align__(16) uint8_t smem[2 * SB];
-  static_assert(4 * 64 * NDT * 16 * 4 <= 2 * SB, "reduction buffer must fit the stages");
+  using RT = typename T::RT;
+  constexpr int P = RT::P, NS = D / 16, NDT = D / 32;
+  constexpr int SB = T::DQ_STAGE;
+  __shared__ __align__(16) uint8_t smem[T::DQ_LDS];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
@@ -253,30 +268,32 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
   const int64_t hoff = (int64_t)bh * a.S * D;
   const float NINF = -__builtin_inff();
 
-  // DMA plan: wave w issues KB-instructions w, w + 8, ... (K, V, K^T)
-  uint32_t soff[T::DQ_SLOTS];
+  // DMA plan: wave w issues KB-instructions w, w + 8, ... (K then V)
+  uint32_t soff[T::SLOTS];
 #pragma unroll
-  for (int s = 0; s < T::DQ_SLOTS; ++s) {
-    const int i = w + 8 * s;
-    soff[s] = i < 2 * T::R_KB ? padded_src_offset<T::RW>(i % T::R_KB, lane)
-                              : padded_src_offset<T::TW>(i - 2 * T::R_KB, lane);
-  }
+  for (int s = 0; s < T::SLOTS; ++s) soff[s] = RT::src_offset((w + 8 * s) % RT::KB, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int ktile, int st) {
     const int64_t toff = hoff + (int64_t)ktile * 64 * D;
-    const void* src3[3] = {uniform_ptr(a.k + toff), uniform_ptr(a.v + toff), uniform_ptr(a.kt + toff)};
+    const void* kb = uniform_ptr(a.k + toff);
+    const void* vb = uniform_ptr(a.v + toff);
     const uint32_t base = lds0 + (uint32_t)(st * SB);
 #pragma unroll
-    for (int s = 0; s < T::DQ_SLOTS; ++s) {
+    for (int s = 0; s < T::SLOTS; ++s) {
       const int i = w + 8 * s;
-      const int which = i < T::R_KB ? 0 : i < 2 * T::R_KB ? 1 : 2;
-      if (s + 1 < T::DQ_SLOTS || i < T::DQ_KB) dma_b128(soff[s], src3[which], base + (uint32_t)i * 1024u);
+      dma_b128(soff[s], i < RT::KB ? kb : vb, base + (uint32_t)i * 1024u);
     }
   };
+  RowOperand rop;                // K / V rows 32 kh + l32
+  rop.init<P>(32 * kh, l32, g);
+  TrOperand top;                 // K^T over key rows 32 kh .. 32 kh + 31
+  top.init<P>(32 * kh, lane);
 
-  int e_cur = n > 0 ? sload_i32(U) : 0;
-  int e_nxt = n > 1 ? sload_i32(U + 1) : 0;
-  if (n > 0) issue(e_cur >> 3, 0);
+  int e0 = n > 0 ? sload_i32(U) : 0;
+  int e1 = n > 1 ? sload_i32(U + 1) : 0;
+  int e2 = n > 2 ? sload_i32(U + 2) : 0;
+  if (n > 0) issue(e0 >> 3, 0);
+  if (n > 1) issue(e1 >> 3, 1);
 
   const int64_t qrow = (int64_t)(2 * pair + tq) * 64 + 32 * qh + l32;
   bf16x8 qf[NS], df[NS];
@@ -298,24 +315,25 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) dq[dt] = f32x16_zero();
 
+  int st = 0;
   for (int j = 0; j < n; ++j) {
-    dma_wait_all();
+    stage_wait<T::SLOTS>(j + 1 < n);
     __syncthreads();
-    const int e = e_cur;
-    if (j + 1 < n) issue(e_nxt >> 3, (j + 1) & 1);
-    e_cur = e_nxt;
-    e_nxt = j + 2 < n ? sload_i32(U + j + 2) : 0;
+    const int e = e0;
+    if (j + 2 < n) issue(e2 >> 3, st == 0 ? 2 : st - 1);
+    e0 = e1;
+    e1 = e2;
+    e2 = j + 3 < n ? sload_i32(U + j + 3) : 0;
+    const uint8_t* sK = smem + st * SB;
+    st = st == 2 ? 0 : st + 1;
     if (!(e & mybit)) continue;
 
-    const uint8_t* sK = smem + (j & 1) * SB;
-    const uint8_t* sV = sK + T::R_KB * 1024;
-    const uint8_t* sKT = sV + T::R_KB * 1024;
+    const uint8_t* sV = sK + RT::BYTES;
     f32x16 sacc = f32x16_zero(), pacc = f32x16_zero();
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const int off = (32 * kh + l32) * T::RPB + 32 * s + 16 * g;
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sK + off), qf[s], sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sV + off), df[s], pacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sK, s), qf[s], sacc, 0, 0, 0);
+      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sV, s), df[s], pacc, 0, 0, 0);
     }
     // element r: key 32kh + 8(r >> 2) + 4g + (r & 3), query = this lane's column
     if (e & 4) {
@@ -333,13 +351,10 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
     }
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      const int tt = 2 * kh + t2;
       const bf16x8 sb = b_from_acc(&pacc, t2);
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const int off = (32 * dt + l32) * T::TPB + 32 * tt + 16 * g;
-        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(sKT + off), sb, dq[dt], 0, 0, 0);
-      }
+      for (int dt = 0; dt < NDT; ++dt)
+        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sK, t2, dt), sb, dq[dt], 0, 0, 0);
     }
   }
 
@@ -407,17 +422,16 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
   return PRISM_OK;
 }
 
-int prism_bsa_bwd_dkdv(const void* q, const void* qt, const void* k, const void* v, const void* do_, const void* dot,
-                       const float* m2, const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid,
-                       const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk,
-                       void* dv, hipStream_t stream) {
+int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
+                       const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid, const int64_t* ustart,
+                       const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk, void* dv,
+                       hipStream_t stream) {
   int rc = check_common(q, k, BH, S, D, "prism_bsa_bwd_dkdv");
   if (rc) return rc;
-  PRISM_REQUIRE(qt && v && do_ && dot && m2 && delta && ustart && ulen && ucols && dk && dv,
-                "prism_bsa_bwd_dkdv: null pointer");
+  PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dk && dv, "prism_bsa_bwd_dkdv: null pointer");
   BwdArgs a = {};
-  a.q = (const uint16_t*)q; a.qt = (const uint16_t*)qt; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
-  a.do_ = (const uint16_t*)do_; a.dot = (const uint16_t*)dot; a.m2 = m2; a.delta = delta; a.kv_valid = kv_valid;
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
+  a.m2 = m2; a.delta = delta; a.kv_valid = kv_valid;
   a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
@@ -427,15 +441,15 @@ int prism_bsa_bwd_dkdv(const void* q, const void* qt, const void* k, const void*
   return PRISM_OK;
 }
 
-int prism_bsa_bwd_dq(const void* q, const void* k, const void* kt, const void* v, const void* do_, const float* m2,
-                     const float* delta, int BH, int64_t S, int D, const uint64_t* tile_masks, const int64_t* ustart,
-                     const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream) {
+int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
+                     int BH, int64_t S, int D, const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen,
+                     const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream) {
   int rc = check_common(q, k, BH, S, D, "prism_bsa_bwd_dq");
   if (rc) return rc;
-  PRISM_REQUIRE(kt && v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq: null pointer");
+  PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq: null pointer");
   BwdArgs a = {};
-  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.kt = (const uint16_t*)kt; a.v = (const uint16_t*)v;
-  a.do_ = (const uint16_t*)do_; a.m2 = m2; a.delta = delta; a.tmask = tile_masks;
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
+  a.m2 = m2; a.delta = delta; a.tmask = tile_masks;
   a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);

@@ -15,16 +15,15 @@
 //    (prism_pair_union), so each K/V tile it stages in LDS serves up to 128
 //    query rows.  Waves 0-1 own tile 2p, waves 2-3 tile 2p+1; a wave whose
 //    tile did not list the current key tile skips the math for it.
-//  * K [64][D] and V^T [D][64] tiles are copied HBM -> LDS by
-//    global_load_lds_dwordx4 (no VGPR staging), double-buffered: the copy of
-//    key tile j+1 is in flight while tile j is multiplied; one barrier per
-//    key tile publishes the next stage.
+//  * K and V tiles [64][D] are copied HBM -> LDS by global_load_lds_dwordx4
+//    (no VGPR staging), double-buffered: the copy of key tile j+1 is in
+//    flight while tile j is multiplied; one barrier per key tile publishes
+//    the next stage.
 //  * S^T = K Q^T puts one query per lane column: softmax statistics stay per
 //    lane (one xor-32 lane swap), and the S^T accumulator is the B operand
-//    of O^T = V^T P^T (no LDS round trip for P).  V^T tiles come from
-//    prism_transpose_tiles with the key order inside each 16-key group
-//    permuted to the MFMA k-slot order, so every operand read is a single
-//    16-byte LDS load.
+//    of O^T = V^T P^T (no LDS round trip for P).  K is read as row operands
+//    (ds_read_b128), V^T straight from the row-major V tile by transposing
+//    reads (ds_read_b64_tr_b16, see RowTile), so V needs no transposed copy.
 //  * key validity: union entries flag tiles that contain padding; only those
 //    load their 64-bit validity word and mask.
 //  * workgroup ids are remapped (xcd_group_remap) so that each XCD (own L2)
@@ -40,7 +39,7 @@ namespace {
 struct FwdArgs {
   const uint16_t* q;       // [BH, S, D] tile order
   const uint16_t* k;       // [BH, S, D] tile order
-  const uint16_t* vt;      // [BH, Nt, D, 64] transposed tiles, MFMA key order
+  const uint16_t* v;       // [BH, S, D] tile order
   const uint64_t* tmask;   // [Nt] key validity per tile, or null
   const int64_t* ustart;   // [BH * Nt/2] pair-union list starts
   const int32_t* ulen;     // [BH * Nt/2]
@@ -54,19 +53,21 @@ struct FwdArgs {
 
 template <int D>
 struct FwdTiles {
-  static constexpr int KW = 2 * D, KPB = KW + 16, K_KB = 64 * KPB / 1024;  // K [64][D], padded rows
-  static constexpr int VW = 128, VPB = VW + 16, V_KB = D * VPB / 1024;     // V^T [D][64], padded rows
-  static constexpr int STAGE_KB = K_KB + V_KB;
-  static constexpr int SLOTS = (STAGE_KB + 3) / 4;                         // KB-instructions per wave
-  static_assert(64 * KPB % 1024 == 0 && D * VPB % 1024 == 0, "tiles must fill whole KB");
+  using RT = RowTile<D>;
+  static constexpr int STAGE = 2 * RT::BYTES;  // K, V
+  static constexpr int STAGE_KB = 2 * RT::KB;
+  static constexpr int SLOTS = STAGE_KB / 4;   // KB-instructions per wave
+  static_assert(STAGE_KB % 4 == 0, "stage must split evenly over 4 waves");
 };
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   using T = FwdTiles<D>;
+  using RT = typename T::RT;
+  constexpr int P = RT::P;
   constexpr int NS = D / 16;   // MFMA k-steps over d
   constexpr int NDT = D / 32;  // 32-row d blocks of O^T
-  __shared__ __align__(16) uint8_t smem[2 * T::STAGE_KB * 1024];
+  __shared__ __align__(16) uint8_t smem[2 * T::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
@@ -78,28 +79,28 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
   const uint16_t* Qh = a.q + (int64_t)bh * a.S * D;
   const uint16_t* Kh = a.k + (int64_t)bh * a.S * D;
-  const uint16_t* VTh = a.vt + (int64_t)bh * a.S * D;
+  const uint16_t* Vh = a.v + (int64_t)bh * a.S * D;
   const float NINF = -__builtin_inff();
 
-  // DMA plan: wave w issues KB-instructions w, w + 4, ... of each stage
+  // DMA plan: wave w issues KB-instructions w, w + 4, ... of each stage (K then V)
   uint32_t soff[T::SLOTS];
 #pragma unroll
-  for (int s = 0; s < T::SLOTS; ++s) {
-    const int i = w + 4 * s;
-    soff[s] = i < T::K_KB ? padded_src_offset<T::KW>(i, lane) : padded_src_offset<T::VW>(i - T::K_KB, lane);
-  }
+  for (int s = 0; s < T::SLOTS; ++s) soff[s] = RT::src_offset((w + 4 * s) % RT::KB, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int kt, int st) {
     const void* kb = uniform_ptr(Kh + (int64_t)kt * 64 * D);
-    const void* vb = uniform_ptr(VTh + (int64_t)kt * 64 * D);
-    const uint32_t base = lds0 + (uint32_t)(st * T::STAGE_KB) * 1024u;
+    const void* vb = uniform_ptr(Vh + (int64_t)kt * 64 * D);
+    const uint32_t base = lds0 + (uint32_t)(st * T::STAGE);
 #pragma unroll
     for (int s = 0; s < T::SLOTS; ++s) {
       const int i = w + 4 * s;
-      const void* src = i < T::K_KB ? kb : vb;
-      if (s + 1 < T::SLOTS || i < T::STAGE_KB) dma_b128(soff[s], src, base + (uint32_t)i * 1024u);
+      dma_b128(soff[s], i < RT::KB ? kb : vb, base + (uint32_t)i * 1024u);
     }
   };
+  RowOperand kop;
+  kop.init<P>(0, l32, g);
+  TrOperand vop;
+  vop.init<P>(0, lane);
 
   int e_cur = n > 0 ? sload_i32(U) : 0;
   int e_nxt = n > 1 ? sload_i32(U + 1) : 0;
@@ -126,15 +127,15 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     e_nxt = j + 2 < n ? sload_i32(U + j + 2) : 0;
     if (!(e & mybit)) continue;
 
-    const uint8_t* sK = smem + (j & 1) * T::STAGE_KB * 1024;
-    const uint8_t* sV = sK + T::K_KB * 1024;
+    const uint8_t* sK = smem + (j & 1) * T::STAGE;
+    const uint8_t* sV = sK + RT::BYTES;
     // S^T[key][q] = K Q^T, two 32-key halves as interleaved MFMA chains
     f32x16 sacc[2] = {f32x16_zero(), f32x16_zero()};
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(sK + (32 * kh + l32) * T::KPB + 32 * s + 16 * g);
+        const bf16x8 ka = kop.load(sK + 32 * kh * P, s);
         sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], sacc[kh], 0, 0, 0);
       }
     if (e & 4) {
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
       const bf16x8 pb = b_from_acc(sacc, tt);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const bf16x8 va = *reinterpret_cast<const bf16x8*>(sV + (32 * dt + l32) * T::VPB + 32 * tt + 16 * g);
+        const bf16x8 va = vop.load<P>(sV, tt, dt);
         acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, acc_o[dt], 0, 0, 0);
       }
     }
@@ -209,16 +210,16 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
 extern "C" {
 
-int prism_bsa_fwd(const void* q, const void* k, const void* vt, int BH, int64_t S, int D, const uint64_t* tile_masks,
+int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S, int D, const uint64_t* tile_masks,
                   const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* o, float* lse,
                   hipStream_t stream) {
-  PRISM_REQUIRE(q && k && vt && ustart && ulen && ucols && o && lse, "prism_bsa_fwd: null pointer");
+  PRISM_REQUIRE(q && k && v && ustart && ulen && ucols && o && lse, "prism_bsa_fwd: null pointer");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_bsa_fwd: head_dim %d unsupported (64, 128)", D);
   PRISM_REQUIRE(S > 0 && S % 128 == 0, "prism_bsa_fwd: S must be a positive multiple of 128");
   PRISM_REQUIRE(BH >= 1, "prism_bsa_fwd: BH must be >= 1");
   PRISM_REQUIRE((int64_t)BH * (S / 128) < (1ll << 31), "prism_bsa_fwd: grid too large");
   FwdArgs a;
-  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.vt = (const uint16_t*)vt; a.tmask = tile_masks;
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.tmask = tile_masks;
   a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64;
   a.npairs = (int)(S / 128);
   a.scale_log2 = sm_scale * 1.4426950408889634f;

@@ -184,34 +184,6 @@ __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs 
   }
 }
 
-// grid (Nt, B*H): tile-order rows [64][D] -> transposed tile [D][64] (bf16)
-// whose 64 positions per row hold the keys in MFMA k-slot order: position j of
-// each 16-key group holds key tslot_key(j) of that group.
-template <int D>
-__global__ __launch_bounds__(256) void transpose_tiles_kernel(const uint16_t* __restrict__ in,
-                                                              uint16_t* __restrict__ out, int64_t S) {
-  constexpr int PITCH = D / 2 + 1;  // uint32 pairs per LDS row, odd pitch: no bank conflicts
-  __shared__ uint32_t sP[64][PITCH];
-  const int tile = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
-  const int64_t base = ((int64_t)bh * S + (int64_t)tile * 64) * D;
-  const uint32_t* src = reinterpret_cast<const uint32_t*>(in + base);
-  for (int i = tid; i < 64 * D / 2; i += 256) {
-    const int row = i / (D / 2), col = i - row * (D / 2);
-    sP[row][col] = src[i];
-  }
-  __syncthreads();
-  // output row d holds keys 0..63: 64 bf16 = 32 uint32
-  uint32_t* dst = reinterpret_cast<uint32_t*>(out + base);
-  for (int i = tid; i < D * 32; i += 256) {
-    const int d = i >> 5, p = (i & 31) * 2;
-    const int kp = (p & ~15) + tslot_key(p & 15);  // keys kp, kp + 1 at positions p, p + 1
-    const uint32_t a0 = sP[kp][d >> 1], a1 = sP[kp + 1][d >> 1];
-    const uint32_t lo = (d & 1) ? (a0 >> 16) : (a0 & 0xffffu);
-    const uint32_t hi = (d & 1) ? (a1 >> 16) : (a1 & 0xffffu);
-    dst[i] = lo | (hi << 16);
-  }
-}
-
 // grid (Nz, B*H): tile-order bf16 rows -> THW rows of dtype TO.
 template <int D, typename TO>
 __global__ __launch_bounds__(kGatherThreads) void scatter_rows_kernel(
@@ -291,18 +263,6 @@ int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, 
     else gather_pool_kernel<64, float><<<grid, kGatherThreads, 0, stream>>>(a);
   }
   PRISM_LAUNCH_CHECK("prism_gather_pool");
-  return PRISM_OK;
-}
-
-int prism_transpose_tiles(const void* in_rows, int BH, int64_t S, int D, void* out_t, hipStream_t stream) {
-  PRISM_REQUIRE(in_rows && out_t, "prism_transpose_tiles: null pointer");
-  PRISM_REQUIRE(S > 0 && S % 64 == 0, "prism_transpose_tiles: S must be a positive multiple of 64");
-  PRISM_REQUIRE(D == 64 || D == 128, "prism_transpose_tiles: head_dim %d unsupported", D);
-  PRISM_REQUIRE(BH >= 1, "prism_transpose_tiles: BH must be >= 1");
-  dim3 grid((unsigned)(S / 64), BH);
-  if (D == 128) transpose_tiles_kernel<128><<<grid, 256, 0, stream>>>((const uint16_t*)in_rows, (uint16_t*)out_t, S);
-  else transpose_tiles_kernel<64><<<grid, 256, 0, stream>>>((const uint16_t*)in_rows, (uint16_t*)out_t, S);
-  PRISM_LAUNCH_CHECK("prism_transpose_tiles");
   return PRISM_OK;
 }
 

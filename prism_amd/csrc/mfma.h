@@ -8,9 +8,8 @@
 // operand of a following MFMA over k = those 64 rows in four 16-row steps
 // tt: step tt uses rows 16tt + {4g..4g+3, 8+4g..8+4g+3} as k-slots 8g..8g+7
 // (a permutation of k inside each 16-row group, applied identically to A).
-// "Transposed tiles" ([D][64] bf16, written by prism_transpose_tiles) store the
-// 64 keys of each row in that k-slot order, so the matching A operand is one
-// contiguous 16-byte load.
+// The matching A operand is read from a row-major tile in LDS by transposing
+// reads (TrOperand in tile_dma.h).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -20,9 +19,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 __device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t* p) {
-  return as_bf16x8(*reinterpret_cast<const uint4*>(p));
-}
-__device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
   return as_bf16x8(*reinterpret_cast<const uint4*>(p));
 }
 __device__ __forceinline__ f32x16 f32x16_zero() {
@@ -48,14 +44,6 @@ __device__ __forceinline__ bf16x8 b_from_acc(const f32x16* acc, int tt) {
   pb.w = pack_bf16(acc[h][4 * j0 + 6], acc[h][4 * j0 + 7]);
   return as_bf16x8(pb);
 }
-// A operand (32 rows x 16 k) of k-step tt from a transposed tile in LDS
-// ([rows][pitch], keys in k-slot order)
-__device__ __forceinline__ bf16x8 a_from_t(const uint16_t* sT, int pitch, int dt, int tt, int l32, int g) {
-  return lds_bf16x8(sT + (32 * dt + l32) * pitch + 16 * tt + 8 * g);
-}
-// key stored at position j (0..15) of a 16-key group of a transposed tile
-__host__ __device__ __forceinline__ int tslot_key(int j) { return 4 * (j >> 3) + (j & 3) + 8 * ((j >> 2) & 1); }
-
 // max(a, b) for non-NaN inputs without NaN canonicalisation (v_med3 with
 // +inf folds into v_max3_f32 chains)
 __device__ __forceinline__ float fmax_nn(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, __builtin_inff()); }

@@ -21,14 +21,14 @@
 // (consume_regs), or the compiler's first-use wait inside the loop would
 // drain the tile copy on every iteration.
 //
-// LDS tiles are padded by 16 bytes per row, which keeps the MFMA operand reads
-// (ds_read_b128 of 32 consecutive rows at one column) free of bank conflicts.
-// A padded tile of R rows x W bytes occupies R * (W + 16) bytes, a whole
-// number of KB for the tiles used here; lanes whose 16-byte LDS slot is a
-// row's padding re-read the first chunk of that row (harmless, L2-resident).
+// The LDS layout of the tiles (padded, swizzled rows) is described with
+// RowTile below; each tile is a whole number of KB, so a stage is filled by a
+// fixed number of KB-instructions spread over the waves.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "mfma.h"
 
 typedef __attribute__((address_space(3))) void prism_lds_void;
 
@@ -78,12 +78,79 @@ __device__ __forceinline__ void consume_regs(const T& x) {
   asm volatile("" ::"v"(x));
 }
 
-// Byte offset, inside a row-major global tile of rows of W bytes, that lane
-// `lane` of KB-instruction `i` fetches for a padded LDS tile (pitch W + 16).
-template <int W>
-__device__ __forceinline__ uint32_t padded_src_offset(int i, int lane) {
-  constexpr int P = W + 16;
-  const int pos = 1024 * i + 16 * lane;
-  const int row = pos / P, col = pos - row * P;
-  return (uint32_t)(row * W + (col < W ? col : 0));
+template <int N>
+__device__ __forceinline__ void dma_wait_le() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
 }
+
+// ------------------------------------------------------------ row tiles
+// A bf16 tile [64][D] is kept row-major in LDS with a pitch of 2D + 64 bytes,
+// 16-byte chunk c of row r stored at chunk (c & ~3) | ((c & 3) ^ ((r >> 2) & 3)).
+// Two read patterns use the same tile without bank conflicts (64 banks):
+//  * RowOperand: an MFMA operand whose contraction runs along the tile's
+//    columns (lane (l32, g) takes 8 elements of row R + l32 at column
+//    16 s + 8 g) -- one ds_read_b128;
+//  * TrOperand: an MFMA operand whose contraction runs along the tile's rows
+//    (lane (l32, g) takes column 32 dt + l32 at the eight rows
+//    16 tt + {4g .. 4g+3, 8+4g .. 8+4g+3}, the k-slot order of an operand
+//    built from an accumulator, see b_from_acc) -- two ds_read_b64_tr_b16.
+//    Within each 16-lane group, lane 16b + 4i + e of ds_read_b64_tr_b16
+//    receives element e of the 8-byte chunks addressed by lanes 16b + 4k + i,
+//    k = 0..3 (in slot k).
+// Every per-step offset is a lane base plus an immediate, and the same tile
+// serves S = Q K^T-type products and the transposed products (dK = dS^T Q,
+// dQ = dS K, O = P V), so no transposed copies are needed.
+template <int D>
+struct RowTile {
+  static constexpr int W = 2 * D, P = W + 64, BYTES = 64 * P, KB = BYTES / 1024;
+  static_assert(BYTES % 1024 == 0, "row tiles fill whole KB");
+  // global byte offset fetched by lane `lane` of KB-instruction i of the tile
+  // (lanes whose slot is row padding re-read the row's first chunk)
+  static __device__ __forceinline__ uint32_t src_offset(int i, int lane) {
+    const int pos = 1024 * i + 16 * lane;
+    const int row = pos / P, slot = (pos - row * P) >> 4;
+    if (slot >= W / 16) return (uint32_t)(row * W);
+    const int c = (slot & ~3) | ((slot & 3) ^ ((row >> 2) & 3));
+    return (uint32_t)(row * W + 16 * c);
+  }
+};
+
+struct RowOperand {
+  uint32_t even, odd;  // byte offsets in the tile for even / odd k-steps s
+  // rows R + l32 (R a multiple of 4, may be wave-uniform runtime)
+  template <int P>
+  __device__ __forceinline__ void init(int R, int l32, int g) {
+    const int x = g ^ ((l32 >> 2) & 3);
+    even = (uint32_t)((R + l32) * P + 16 * x);
+    odd = (uint32_t)((R + l32) * P + 16 * (x ^ 2));
+  }
+  __device__ __forceinline__ bf16x8 load(const uint8_t* tile, int s) const {
+    return *reinterpret_cast<const bf16x8*>(tile + ((s & 1) ? odd : even) + 64 * (s >> 1));
+  }
+};
+
+typedef short prism_v4s __attribute__((ext_vector_type(4)));
+typedef short prism_v8s __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) prism_v4s prism_lds_v4s;
+
+struct TrOperand {
+  uint32_t h0, h1;  // byte offsets of rows 16tt + 4g + k and 16tt + 8 + 4g + k (tt = 0)
+  // R0: first tile row of k-step tt = 0 (a multiple of 16, may be wave-uniform)
+  template <int P>
+  __device__ __forceinline__ void init(int R0, int lane) {
+    const int b = lane >> 4, k = (lane >> 2) & 3, i = lane & 3;
+    const int x0 = (2 * (b & 1) + (i >> 1)) ^ (b >> 1);
+    const int rowb = (R0 + 4 * (b >> 1) + k) * P + 8 * (i & 1);
+    h0 = (uint32_t)(rowb + 16 * x0);
+    h1 = (uint32_t)(rowb + 8 * P + 16 * (x0 ^ 2));
+  }
+  template <int P>
+  __device__ __forceinline__ bf16x8 load(const uint8_t* tile, int tt, int dt) const {
+    const uint8_t* p0 = tile + h0 + 16 * P * tt + 64 * dt;
+    const uint8_t* p1 = tile + h1 + 16 * P * tt + 64 * dt;
+    const prism_v4s r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((prism_lds_v4s*)(p0));
+    const prism_v4s r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((prism_lds_v4s*)(p1));
+    const prism_v8s v = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8, v);
+  }
+};

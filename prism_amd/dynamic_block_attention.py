@@ -62,7 +62,6 @@ class _Plan:
         gk = ops.gather_pool(k, lay, valid_mask, rows=True, pool=True)
         gv = ops.gather_pool(v, lay, valid_mask, rows=True)
         self.q_re, self.k_re, self.v_re = gq["rows"], gk["rows"], gv["rows"]
-        self.vt = ops.transpose_tiles(self.v_re)
         masked = valid_mask is not None
         self.kv_valid = gq["valid_re"] if masked else None
         self.block_count = gq["block_count"]
@@ -96,7 +95,7 @@ class _DynBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _Plan, sm_scale: float):
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.tmasks, plan.qunion, sm_scale)
+        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale)
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
@@ -110,15 +109,12 @@ class _DynBSA(torch.autograd.Function):
         lay = plan.lay
         gd = ops.gather_pool(do.contiguous(), lay, None, rows=True, dot_with=o_re)
         do_re, delta = gd["rows"], gd["rowdot"]
-        dot = ops.transpose_tiles(do_re)
-        qt = ops.transpose_tiles(plan.q_re)
-        kt = ops.transpose_tiles(plan.k_re)
         if plan.kunion is None:
             plan.klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, plan.B * plan.H, lay.Nt)
             plan.kunion = ops.pair_union(*plan.klists, lay.Nt)
         m2 = ops.lse_to_m2(lse)
-        dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, qt, plan.k_re, kt, plan.v_re, do_re, dot, m2, delta,
-                                          plan.kv_valid, plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale)
+        dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid,
+                                          plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale)
         tq, tk, tv = ctx.in_dtypes
         dq = ops.scatter_rows(dq_re, lay, tq)
         dk = ops.scatter_rows(dk_re, lay, tk)

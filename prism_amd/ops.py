@@ -210,16 +210,6 @@ def gather_pool(x: torch.Tensor, lay: ZoneLayout, valid: Optional[torch.Tensor] 
     return out
 
 
-def transpose_tiles(rows: torch.Tensor) -> torch.Tensor:
-    """[B,H,S,D] bf16 tile order -> [B,H,S/64,D,64] transposed tiles."""
-    _cuda(rows)
-    rows = rows.contiguous()
-    B, H, S, D = rows.shape
-    out = torch.empty((B, H, S // 64, D, 64), device=rows.device, dtype=torch.bfloat16)
-    _call("prism_transpose_tiles", _p(rows), B * H, S, D, _p(out), _stream())
-    return out
-
-
 def scatter_rows(rows: torch.Tensor, lay: ZoneLayout, out_dtype: torch.dtype) -> torch.Tensor:
     _cuda(rows)
     rows = rows.contiguous()
@@ -368,32 +358,33 @@ def _bf16(t: torch.Tensor, name: str) -> torch.Tensor:
     return t.contiguous()
 
 
-def bsa_fwd(q, k, vt, tmasks, qunion, sm_scale: float):
-    """q, k [B,H,S,D] bf16 tile order, vt [B,H,S/64,D,64]; qunion = pair_union
-    of the per-query-tile key lists -> (o bf16, lse fp32 natural)."""
-    _cuda(q, k, vt, tmasks)
-    q, k, vt = _bf16(q, "q"), _bf16(k, "k"), _bf16(vt, "vt")
+def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float):
+    """q, k, v [B,H,S,D] bf16 tile order; qunion = pair_union of the
+    per-query-tile key lists -> (o bf16, lse fp32 natural)."""
+    _cuda(q, k, v, tmasks)
+    q, k, v = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v")
     B, H, S, D = q.shape
     ustart, ulen, ucols = qunion
     o = torch.empty_like(q)
     lse = torch.empty((B, H, S), device=q.device, dtype=torch.float32)
-    _call("prism_bsa_fwd", _p(q), _p(k), _p(vt), B * H, S, D, _p(tmasks), _p(ustart), _p(ulen), _p(ucols),
+    _call("prism_bsa_fwd", _p(q), _p(k), _p(v), B * H, S, D, _p(tmasks), _p(ustart), _p(ulen), _p(ucols),
           float(sm_scale), _p(o), _p(lse), _stream())
     return o, lse
 
 
-def bsa_bwd(q, qt, k, kt, v, do, dot, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float):
-    """Backward over tile-order tensors; qunion / kunion = pair unions of the
-    per-query-tile key lists and of the per-key-tile query lists.  Returns
+def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float):
+    """Backward over tile-order bf16 tensors; qunion / kunion = pair unions of
+    the per-query-tile key lists and of the per-key-tile query lists.  Returns
     dq, dk, dv (bf16, tile order)."""
-    _cuda(q, qt, k, kt, v, do, dot, m2, delta, kv_valid, tmasks)
+    _cuda(q, k, v, do, m2, delta, kv_valid, tmasks)
+    q, k, v, do = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"), _bf16(do, "do")
     B, H, S, D = q.shape
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     s = _stream()
-    _call("prism_bsa_bwd_dkdv", _p(q), _p(qt), _p(k), _p(v), _p(do), _p(dot), _p(m2), _p(delta), B * H, S, D,
-          _p(kv_valid), _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), float(sm_scale), _p(dk), _p(dv), s)
-    _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(kt), _p(v), _p(do), _p(m2), _p(delta), B * H, S, D,
-          _p(tmasks), _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), float(sm_scale), _p(dq), s)
+    _call("prism_bsa_bwd_dkdv", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, S, D, _p(kv_valid),
+          _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), float(sm_scale), _p(dk), _p(dv), s)
+    _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, S, D, _p(tmasks),
+          _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), float(sm_scale), _p(dq), s)
     return dq, dk, dv

@@ -38,12 +38,6 @@ def host(t: torch.Tensor) -> np.ndarray:
     return t.cpu().numpy()
 
 
-# key held by each of the 64 positions of a transposed-tile row: inside a
-# 16-key group, positions 4-7 and 8-11 swap (MFMA k-slot order)
-TSLOT_PERM = np.array([16 * (p // 16) + [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15][p % 16]
-                       for p in range(64)])
-
-
 def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
     a = np.ascontiguousarray(a)
     b = np.ascontiguousarray(b)
@@ -165,10 +159,6 @@ def test_gather_pool_bitexact(case):
         assert np.array_equal(host(g["rows"]), xf[:, :, src])
         vre = np.ones(len(src), np.uint8) if valid is None else valid[src]
         assert np.array_equal(host(g["valid_re"]), vre)
-        t = host(ops.transpose_tiles(g["rows"]))
-        B, H, S, D = x.shape
-        exp = xf[:, :, src].reshape(B, H, S // 64, 64, D).transpose(0, 1, 2, 4, 3)
-        assert np.array_equal(t, exp[..., TSLOT_PERM])
 
 
 def test_scores_bitexact():
@@ -320,7 +310,7 @@ def test_attention_fwd_bwd_tolerance(case):
     sm = 1 / math.sqrt(D)
     plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
                         sparsity=0.6, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
-    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.vt, plan.tmasks, plan.qunion, sm)
+    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm)
     qf = O.bf16_bits_to_f32(host(plan.q_re)).reshape(B * H, S, D)
     kf = O.bf16_bits_to_f32(host(plan.k_re)).reshape(B * H, S, D)
     vf = O.bf16_bits_to_f32(host(plan.v_re)).reshape(B * H, S, D)
@@ -341,8 +331,7 @@ def test_attention_fwd_bwd_tolerance(case):
     ops._lib.call("prism_bwd_preprocess", o.data_ptr(), do_t.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
     klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, plan.lay.Nt)
     kunion = ops.pair_union(*klists, plan.lay.Nt)
-    dq, dk, dv = ops.bsa_bwd(plan.q_re, ops.transpose_tiles(plan.q_re), plan.k_re, ops.transpose_tiles(plan.k_re),
-                             plan.v_re, do_t, ops.transpose_tiles(do_t), ops.lse_to_m2(lse), delta, plan.kv_valid,
+    dq, dk, dv = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_t, ops.lse_to_m2(lse), delta, plan.kv_valid,
                              plan.tmasks, plan.qunion, kunion, sm)
     dof = O.bf16_bits_to_f32(do).reshape(B * H, S, D)
     dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, og, dof, lse_ref, *lists, kv, sm)
