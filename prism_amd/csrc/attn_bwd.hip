@@ -16,9 +16,9 @@
 //  * one workgroup of 8 waves per PAIR of tiles (2p, 2p+1), one workgroup per
 //    CU (two waves per SIMD), walking the sorted union of the two tiles' lists
 //    (prism_pair_union);
-//  * the operand tiles of list entry j + 2 are copied HBM -> LDS by
-//    global_load_lds_dwordx4 while entry j is multiplied (three stages, one
-//    barrier per entry, no VGPR staging);
+//  * the operand tiles of list entry j + NST - 1 are copied HBM -> LDS by
+//    global_load_lds_dwordx4 while entry j is multiplied (NST = 3 stages for
+//    dK/dV, 4 for dQ; one barrier per entry, no VGPR staging);
 //  * all operands come from row-major tiles: row reads (ds_read_b128) for the
 //    S / dP products, transposing reads (ds_read_b64_tr_b16) for the products
 //    that contract over the tile's rows (see RowTile), so no transposed
@@ -34,9 +34,10 @@
 // qh = w >> 2).  S = Q K^T and dP = dO V^T keep one key per lane column, so P
 // and dS feed the B operand of dV^T = dO^T P and dK^T = Q^T dS straight from
 // the accumulators.
-// dQ: wave w owns query rows [32 qh, 32 qh + 32) of tile 2p + tq and keys
-// [32 kh, 32 kh + 32) of every listed key tile (qh = w & 1,
-// tq = (w >> 1) & 1, kh = w >> 2).  S^T = K Q^T and dP^T = V dO^T keep one
+// dQ: two 4-wave workgroups per CU (their phases drift apart, so one's
+// exponentials overlap the other's MFMA work); wave w owns query rows
+// [32 qh, 32 qh + 32) of tile 2p + tq over all 64 keys of every listed key
+// tile (qh = w & 1, tq = w >> 1).  S^T = K Q^T and dP^T = V dO^T keep one
 // query per lane column; dQ^T = K^T dS^T.
 #include "common.h"
 #include "mfma.h"
@@ -60,7 +61,8 @@ struct BwdArgs {
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kStages = 3;  // entry j + 2 is copied while entry j is multiplied
+constexpr int kStagesDkdv = 3;  // entry j + 2 is copied while entry j is multiplied
+constexpr int kStagesDq = 2;    // two 4-wave workgroups per CU, double-buffered each
 
 template <int D>
 struct BwdTiles {
@@ -72,20 +74,10 @@ struct BwdTiles {
   static_assert(2 * RT::KB % 8 == 0, "stage must split evenly over 8 waves");
   static constexpr int NDT = D / 32;
   static constexpr int DKDV_RED = 4 * 64 * 2 * NDT * 16 * 4;  // qh = 1 partials of dK and dV
-  static constexpr int DQ_RED = 4 * 64 * NDT * 16 * 4;
-  static constexpr int DKDV_LDS = kStages * DKDV_STAGE > DKDV_RED ? kStages * DKDV_STAGE : DKDV_RED;
-  static constexpr int DQ_LDS = kStages * DQ_STAGE > DQ_RED ? kStages * DQ_STAGE : DQ_RED;
+  static constexpr int DKDV_LDS = kStagesDkdv * DKDV_STAGE > DKDV_RED ? kStagesDkdv * DKDV_STAGE : DKDV_RED;
+  static constexpr int DQ_LDS = kStagesDq * DQ_STAGE;
   static_assert(DKDV_LDS <= 160 * 1024 && DQ_LDS <= 160 * 1024, "LDS budget");
 };
-
-// Wait for the copy of the entry about to be used: with three stages the copy
-// of the next entry (issued one iteration later) may stay in flight; `cnt` is
-// the number of copy instructions this wave issues per entry.
-template <int CNT>
-__device__ __forceinline__ void stage_wait(bool next_in_flight) {
-  if (next_in_flight) dma_wait_le<CNT>();
-  else dma_wait_le<0>();
-}
 
 template <int D>
 __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
@@ -133,12 +125,11 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   TrOperand top;                 // Q^T / dO^T over query rows 32 qh .. 32 qh + 31
   top.init<P>(32 * qh, lane);
 
-  // entries j .. j + 2 (wave-uniform ring)
-  int e0 = n > 0 ? sload_i32(U) : 0;
-  int e1 = n > 1 ? sload_i32(U + 1) : 0;
-  int e2 = n > 2 ? sload_i32(U + 2) : 0;
-  if (n > 0) issue(e0 >> 3, 0);
-  if (n > 1) issue(e1 >> 3, 1);
+  EntryRing<kStagesDkdv> ring;
+  ring.init(U, n);
+#pragma unroll
+  for (int k = 0; k + 1 < kStagesDkdv; ++k)
+    if (k < n) issue(ring.e[k] >> 3, k);
 
   const int64_t key = (int64_t)(2 * pair + tk) * 64 + 32 * kh + l32;
   bf16x8 kf[NS], vf[NS];
@@ -162,16 +153,13 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
 
   int st = 0;  // stage of entry j
   for (int j = 0; j < n; ++j) {
-    if (w >= 6) stage_wait<T::SLOTS + 1>(j + 1 < n);
-    else stage_wait<T::SLOTS>(j + 1 < n);
+    if (w >= 6) stage_wait<kStagesDkdv, T::SLOTS + 1>(n - 1 - j);
+    else stage_wait<kStagesDkdv, T::SLOTS>(n - 1 - j);
     __syncthreads();
-    const int e = e0;
-    if (j + 2 < n) issue(e2 >> 3, st == 0 ? 2 : st - 1);
-    e0 = e1;
-    e1 = e2;
-    e2 = j + 3 < n ? sload_i32(U + j + 3) : 0;
+    if (j + kStagesDkdv - 1 < n) issue(ring.e[kStagesDkdv - 1] >> 3, stage_ahead<kStagesDkdv>(st));
+    const int e = ring.advance(U, n, j);
     const uint8_t* sQ = smem + st * SB;
-    st = st == 2 ? 0 : st + 1;
+    st = st + 1 == kStagesDkdv ? 0 : st + 1;
     if (!(e & mybit)) continue;
 
     const uint8_t* sDO = sQ + RT::BYTES;
@@ -250,17 +238,18 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
 }
 
 template <int D>
-__global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   using T = BwdTiles<D>;
   using RT = typename T::RT;
   constexpr int P = RT::P, NS = D / 16, NDT = D / 32;
   constexpr int SB = T::DQ_STAGE;
-  __shared__ __align__(16) uint8_t smem[T::DQ_LDS];
+  constexpr int SLOTS = 2 * RT::KB / 4;  // KB-instructions per wave and stage (4 waves)
+  __shared__ __align__(16) uint8_t smem[kStagesDq * SB];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
-  const int qh = w & 1, tq = (w >> 1) & 1, kh = w >> 2;
-  const int logical = xcd_group_remap<32>((int)blockIdx.x, (int)gridDim.x);
+  const int qh = w & 1, tq = w >> 1;
+  const int logical = xcd_group_remap<64>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
@@ -268,10 +257,10 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
   const int64_t hoff = (int64_t)bh * a.S * D;
   const float NINF = -__builtin_inff();
 
-  // DMA plan: wave w issues KB-instructions w, w + 8, ... (K then V)
-  uint32_t soff[T::SLOTS];
+  // DMA plan: wave w issues KB-instructions w, w + 4, ... (K then V)
+  uint32_t soff[SLOTS];
 #pragma unroll
-  for (int s = 0; s < T::SLOTS; ++s) soff[s] = RT::src_offset((w + 8 * s) % RT::KB, lane);
+  for (int s = 0; s < SLOTS; ++s) soff[s] = RT::src_offset((w + 4 * s) % RT::KB, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int ktile, int st) {
     const int64_t toff = hoff + (int64_t)ktile * 64 * D;
@@ -279,21 +268,21 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
     const void* vb = uniform_ptr(a.v + toff);
     const uint32_t base = lds0 + (uint32_t)(st * SB);
 #pragma unroll
-    for (int s = 0; s < T::SLOTS; ++s) {
-      const int i = w + 8 * s;
+    for (int s = 0; s < SLOTS; ++s) {
+      const int i = w + 4 * s;
       dma_b128(soff[s], i < RT::KB ? kb : vb, base + (uint32_t)i * 1024u);
     }
   };
-  RowOperand rop;                // K / V rows 32 kh + l32
-  rop.init<P>(32 * kh, l32, g);
-  TrOperand top;                 // K^T over key rows 32 kh .. 32 kh + 31
-  top.init<P>(32 * kh, lane);
+  RowOperand rop;  // K / V rows l32 (+ 32 kh as an immediate)
+  rop.init<P>(0, l32, g);
+  TrOperand top;   // K^T over key rows 0 .. 63
+  top.init<P>(0, lane);
 
-  int e0 = n > 0 ? sload_i32(U) : 0;
-  int e1 = n > 1 ? sload_i32(U + 1) : 0;
-  int e2 = n > 2 ? sload_i32(U + 2) : 0;
-  if (n > 0) issue(e0 >> 3, 0);
-  if (n > 1) issue(e1 >> 3, 1);
+  EntryRing<kStagesDq> ring;
+  ring.init(U, n);
+#pragma unroll
+  for (int k = 0; k + 1 < kStagesDq; ++k)
+    if (k < n) issue(ring.e[k] >> 3, k);
 
   const int64_t qrow = (int64_t)(2 * pair + tq) * 64 + 32 * qh + l32;
   bf16x8 qf[NS], df[NS];
@@ -315,75 +304,62 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) dq[dt] = f32x16_zero();
 
-  int st = 0;
+  int st = 0;  // stage of entry j
   for (int j = 0; j < n; ++j) {
-    stage_wait<T::SLOTS>(j + 1 < n);
+    stage_wait<kStagesDq, SLOTS>(n - 1 - j);
     __syncthreads();
-    const int e = e0;
-    if (j + 2 < n) issue(e2 >> 3, st == 0 ? 2 : st - 1);
-    e0 = e1;
-    e1 = e2;
-    e2 = j + 3 < n ? sload_i32(U + j + 3) : 0;
+    if (j + kStagesDq - 1 < n) issue(ring.e[kStagesDq - 1] >> 3, stage_ahead<kStagesDq>(st));
+    const int e = ring.advance(U, n, j);
     const uint8_t* sK = smem + st * SB;
-    st = st == 2 ? 0 : st + 1;
+    st = st + 1 == kStagesDq ? 0 : st + 1;
     if (!(e & mybit)) continue;
 
     const uint8_t* sV = sK + RT::BYTES;
-    f32x16 sacc = f32x16_zero(), pacc = f32x16_zero();
+    f32x16 sacc[2] = {f32x16_zero(), f32x16_zero()}, pacc[2] = {f32x16_zero(), f32x16_zero()};
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sK, s), qf[s], sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sV, s), df[s], pacc, 0, 0, 0);
-    }
-    // element r: key 32kh + 8(r >> 2) + 4g + (r & 3), query = this lane's column
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sK + 32 * kh * P, s), qf[s], sacc[kh], 0, 0, 0);
+        pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sV + 32 * kh * P, s), df[s], pacc[kh], 0, 0, 0);
+      }
+    // element (kh, r): key 32kh + 8(r >> 2) + 4g + (r & 3), query = this lane's column
     if (e & 4) {
-      const uint32_t bits = (uint32_t)(sload_u64(a.tmask + (e >> 3)) >> (32 * kh + 4 * g));
+      const uint64_t mm = sload_u64(a.tmask + (e >> 3)) >> (4 * g);
+      const uint32_t lo = (uint32_t)mm, hi = (uint32_t)(mm >> 32);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int b = 8 * (r >> 2) + (r & 3);
-        sacc[r] = ((bits >> b) & 1u) ? sacc[r] : NINF;
+        sacc[0][r] = ((lo >> b) & 1u) ? sacc[0][r] : NINF;
+        sacc[1][r] = ((hi >> b) & 1u) ? sacc[1][r] : NINF;
       }
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(__builtin_fmaf(sacc[r], a.scale_log2, -mq));
-      pacc[r] = p * (pacc[r] - dlt);
-    }
+    for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      const bf16x8 sb = b_from_acc(&pacc, t2);
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(__builtin_fmaf(sacc[kh][r], a.scale_log2, -mq));
+        pacc[kh][r] = p * (pacc[kh][r] - dlt);
+      }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const bf16x8 sb = b_from_acc(pacc, tt);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
-        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sK, t2, dt), sb, dq[dt], 0, 0, 0);
+        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sK, tt, dt), sb, dq[dt], 0, 0, 0);
     }
   }
 
-  // add the two key-half partials in a fixed order (kh = 0 + kh = 1)
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(smem);
-  const int slot = w & 3;
-  if (kh == 1) {
+  uint16_t* dqr = a.dq + hoff + qrow * D;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[((slot * NDT + dt) * 16 + r) * 64 + lane] = dq[dt][r];
-  }
-  __syncthreads();
-  if (kh == 0) {
-    uint16_t* dqr = a.dq + hoff + qrow * D;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dq[dt][r] += red[((slot * NDT + dt) * 16 + r) * 64 + lane];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        uint2 o;
-        o.x = pack_bf16(dq[dt][4 * jj + 0] * a.sm_scale, dq[dt][4 * jj + 1] * a.sm_scale);
-        o.y = pack_bf16(dq[dt][4 * jj + 2] * a.sm_scale, dq[dt][4 * jj + 3] * a.sm_scale);
-        *reinterpret_cast<uint2*>(dqr + 32 * dt + 8 * jj + 4 * g) = o;
-      }
+    for (int jj = 0; jj < 4; ++jj) {
+      uint2 o;
+      o.x = pack_bf16(dq[dt][4 * jj + 0] * a.sm_scale, dq[dt][4 * jj + 1] * a.sm_scale);
+      o.y = pack_bf16(dq[dt][4 * jj + 2] * a.sm_scale, dq[dt][4 * jj + 3] * a.sm_scale);
+      *reinterpret_cast<uint2*>(dqr + 32 * dt + 8 * jj + 4 * g) = o;
     }
-  }
 }
 
 // delta[row] = sum_d o[row][d] * do[row][d]: one wave per row, 4 rows per block
@@ -453,8 +429,8 @@ int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do
   a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
-  if (D == 128) bsa_bwd_dq_kernel<128><<<blocks, 512, 0, stream>>>(a);
-  else bsa_bwd_dq_kernel<64><<<blocks, 512, 0, stream>>>(a);
+  if (D == 128) bsa_bwd_dq_kernel<128><<<blocks, 256, 0, stream>>>(a);
+  else bsa_bwd_dq_kernel<64><<<blocks, 256, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_bsa_bwd_dq");
   return PRISM_OK;
 }

@@ -18,7 +18,10 @@
 //  * K and V tiles [64][D] are copied HBM -> LDS by global_load_lds_dwordx4
 //    (no VGPR staging), double-buffered: the copy of key tile j+1 is in
 //    flight while tile j is multiplied; one barrier per key tile publishes
-//    the next stage.
+//    the next stage.  (Two independent workgroups per CU drift out of phase,
+//    so one's softmax overlaps the other's MFMA work; a single 8-wave
+//    workgroup with a deeper pipeline runs its waves in lock-step and was
+//    slower.)
 //  * S^T = K Q^T puts one query per lane column: softmax statistics stay per
 //    lane (one xor-32 lane swap), and the S^T accumulator is the B operand
 //    of O^T = V^T P^T (no LDS round trip for P).  K is read as row operands
@@ -51,6 +54,8 @@ struct FwdArgs {
   float* lse;              // [BH, S] natural log
 };
 
+constexpr int kStages = 2;  // two workgroups per CU: 2 x 2 stages of K and V fill the LDS
+
 template <int D>
 struct FwdTiles {
   using RT = RowTile<D>;
@@ -67,7 +72,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   constexpr int P = RT::P;
   constexpr int NS = D / 16;   // MFMA k-steps over d
   constexpr int NDT = D / 32;  // 32-row d blocks of O^T
-  __shared__ __align__(16) uint8_t smem[2 * T::STAGE];
+  __shared__ __align__(16) uint8_t smem[kStages * T::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
@@ -102,9 +107,11 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   TrOperand vop;
   vop.init<P>(0, lane);
 
-  int e_cur = n > 0 ? sload_i32(U) : 0;
-  int e_nxt = n > 1 ? sload_i32(U + 1) : 0;
-  if (n > 0) issue(e_cur >> 3, 0);
+  EntryRing<kStages> ring;
+  ring.init(U, n);
+#pragma unroll
+  for (int k = 0; k + 1 < kStages; ++k)
+    if (k < n) issue(ring.e[k] >> 3, k);
 
   const int64_t qrow = (int64_t)(2 * pair + (w >> 1)) * 64 + 32 * (w & 1) + l32;
   bf16x8 qf[NS];
@@ -118,26 +125,35 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   for (int dt = 0; dt < NDT; ++dt) acc_o[dt] = f32x16_zero();
   float m = NINF, l = 1.0f;
 
+  int st = 0;  // stage of entry j
   for (int j = 0; j < n; ++j) {
-    dma_wait_all();
+    stage_wait<kStages, T::SLOTS>(n - 1 - j);
     __syncthreads();
-    const int e = e_cur;
-    if (j + 1 < n) issue(e_nxt >> 3, (j + 1) & 1);
-    e_cur = e_nxt;
-    e_nxt = j + 2 < n ? sload_i32(U + j + 2) : 0;
+    if (j + kStages - 1 < n) issue(ring.e[kStages - 1] >> 3, stage_ahead<kStages>(st));
+    const int e = ring.advance(U, n, j);
+    const uint8_t* sK = smem + st * T::STAGE;
+    st = st + 1 == kStages ? 0 : st + 1;
     if (!(e & mybit)) continue;
 
-    const uint8_t* sK = smem + (j & 1) * T::STAGE;
     const uint8_t* sV = sK + RT::BYTES;
-    // S^T[key][q] = K Q^T, two 32-key halves as interleaved MFMA chains
+    // S^T[key][q] = K Q^T, two 32-key halves as interleaved MFMA chains; all
+    // K operands are read first so the LDS latency is paid once
+    bf16x8 kfr[2][NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) kfr[kh][s] = kop.load(sK + 32 * kh * P, s);
     f32x16 sacc[2] = {f32x16_zero(), f32x16_zero()};
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const bf16x8 ka = kop.load(sK + 32 * kh * P, s);
-        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], sacc[kh], 0, 0, 0);
-      }
+      for (int kh = 0; kh < 2; ++kh) sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[kh][s], qf[s], sacc[kh], 0, 0, 0);
+    // V^T operands of the P V product, in flight while the softmax runs
+    bf16x8 vfr[4][NDT];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) vfr[tt][dt] = vop.load<P>(sV, tt, dt);
     if (e & 4) {
       // this lane's keys are 32kh + 8j + 4g + i: bit (32kh + 8j + i) of vmask >> 4g
       const uint64_t mm = sload_u64(a.tmask + (e >> 3)) >> (4 * g);
@@ -161,35 +177,40 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     const float m_new = move ? mx : m;
     const float alpha = move ? fast_exp2(m - m_new) : 1.0f;
     const float mb = m_new == NINF ? 0.0f : m_new;
-    float ls = 0.0f;
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(__builtin_fmaf(sacc[kh][r], a.scale_log2, -mb));
-        sacc[kh][r] = p;
-        ls += p;
-      }
-    ls = xor32_add(ls);
-    l = __builtin_fmaf(l, alpha, ls);
-    m = m_new;
     if (__builtin_amdgcn_ballot_w64(move)) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[dt][r] *= alpha;
     }
-
-    // O^T[d][q] += V^T P^T over four 16-key steps
+    // P and O^T[d][q] += V^T P^T one 16-key step at a time: the exponentials
+    // of step tt + 1 run on the VALU while the MFMAs of step tt execute
+    float ls = 0.0f;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
+      const int h = tt >> 1, r0 = 8 * (tt & 1);
+#pragma unroll
+      for (int r = r0; r < r0 + 8; ++r) {
+        const float p = fast_exp2(__builtin_fmaf(sacc[h][r], a.scale_log2, -mb));
+        sacc[h][r] = p;
+        ls += p;
+      }
       const bf16x8 pb = b_from_acc(sacc, tt);
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const bf16x8 va = vop.load<P>(sV, tt, dt);
-        acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, acc_o[dt], 0, 0, 0);
-      }
+      for (int dt = 0; dt < NDT; ++dt) acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[tt][dt], pb, acc_o[dt], 0, 0, 0);
     }
+    // scheduling: first step's VALU, then alternate one MFMA with the next
+    // step's VALU work
+    __builtin_amdgcn_sched_group_barrier(0x002, 28, 0);
+#pragma unroll
+    for (int i = 0; i < 3 * NDT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 28 / NDT, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NDT, 0);
+    ls = xor32_add(ls);
+    l = __builtin_fmaf(l, alpha, ls);
+    m = m_new;
   }
 
   const float inv = 1.0f / l;

@@ -83,6 +83,53 @@ __device__ __forceinline__ void dma_wait_le() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
 }
 
+// ------------------------------------------------------------ stage pipeline
+// The attention kernels walk a list of entries (prism_pair_union) with an
+// NST-stage ring of LDS stages: the tiles of entry j + NST - 1 are copied while
+// entry j is multiplied.  At the top of iteration j the copies of entries
+// j+1 .. min(j+NST-2, n-1) may stay in flight; CNT = copy instructions per
+// entry issued by this wave.
+template <int NST, int CNT>
+__device__ __forceinline__ void stage_wait(int after) {  // after = n - 1 - j
+  static_assert(NST >= 2 && NST <= 4, "2 to 4 stages");
+  if constexpr (NST >= 4) {
+    if (after >= 2) {
+      dma_wait_le<2 * CNT>();
+      return;
+    }
+  }
+  if constexpr (NST >= 3) {
+    if (after >= 1) {
+      dma_wait_le<CNT>();
+      return;
+    }
+  }
+  dma_wait_le<0>();
+}
+
+// Wave-uniform ring of the next NST list entries (scalar registers).
+template <int NST>
+struct EntryRing {
+  int e[NST];  // entries j .. j + NST - 1 (0 past the end of the list)
+  __device__ __forceinline__ void init(const int32_t* U, int n) {
+#pragma unroll
+    for (int k = 0; k < NST; ++k) e[k] = k < n ? sload_i32(U + k) : 0;
+  }
+  // entry j; shifts the ring to j + 1
+  __device__ __forceinline__ int advance(const int32_t* U, int n, int j) {
+    const int cur = e[0];
+#pragma unroll
+    for (int k = 0; k + 1 < NST; ++k) e[k] = e[k + 1];
+    e[NST - 1] = j + NST < n ? sload_i32(U + j + NST) : 0;
+    return cur;
+  }
+};
+// stage holding entry j + NST - 1 when entry j is in stage st
+template <int NST>
+__device__ __forceinline__ int stage_ahead(int st) {
+  return st == 0 ? NST - 1 : st - 1;
+}
+
 // ------------------------------------------------------------ row tiles
 // A bf16 tile [64][D] is kept row-major in LDS with a pitch of 2D + 64 bytes,
 // 16-byte chunk c of row r stored at chunk (c & ~3) | ((c & 3) ^ ((r >> 2) & 3)).
