@@ -188,6 +188,78 @@ def cpu_baseline(plan, inp, budget_s=12.0):
                       f"({done_pairs} kept tile pairs) of the same plan, {t_used:.1f} s"}
 
 
+# ------------------------------------------------------------------ HBM traffic
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_c4.json")
+COPY_BYTES = 2 << 30
+
+
+def copy_calibration():
+    """One device-to-device copy of COPY_BYTES (reads and writes exactly that
+    many bytes): the reference dispatch that scales the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE counters to bytes."""
+    import torch
+    x = torch.empty(COPY_BYTES // 4, device="cuda", dtype=torch.float32).fill_(1.0)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES}), flush=True)
+
+
+def _counter_means(csv_path: str, counter: str):
+    """kernel name -> mean counter value per dispatch (rocprofv3 --output-format csv)."""
+    import csv
+    acc = {}
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            acc.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def summarize_counters(fetch_csv, write_csv, calib_fetch_csv, calib_write_csv):
+    """Write TRAFFIC_FILE: HBM bytes per launch of each prism kernel from the
+    FETCH_SIZE and WRITE_SIZE runs, each scaled so that the calibration copy of
+    COPY_BYTES reads and writes exactly COPY_BYTES."""
+    names = {"bsa_fwd_kernel": "prism_bsa_fwd", "bsa_bwd_dkdv_kernel": "prism_bsa_bwd_dkdv",
+             "bsa_bwd_dq_kernel": "prism_bsa_bwd_dq", "select_kernel": "prism_select_tiles",
+             "gather_pool_kernel": "prism_gather_pool", "scatter_rows_kernel": "prism_scatter_rows",
+             "block_scores_kernel": "prism_block_scores", "a2v_norms_kernel": "prism_a2v_norms",
+             "zone_stats_kernel": "prism_zone_stats", "pair_union_kernel": "prism_pair_union"}
+    cf = [v for k, v in _counter_means(calib_fetch_csv, "FETCH_SIZE").items() if "copy" in k]
+    cw = [v for k, v in _counter_means(calib_write_csv, "WRITE_SIZE").items() if "copy" in k]
+    f_scale = COPY_BYTES / (max(cf) * 1024.0)
+    w_scale = COPY_BYTES / (max(cw) * 1024.0)
+    fetch = _counter_means(fetch_csv, "FETCH_SIZE")
+    write = _counter_means(write_csv, "WRITE_SIZE")
+    out = {"copy_bytes": COPY_BYTES, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+           "unit": "bytes per launch", "kernels": {}}
+    for k, fv in fetch.items():
+        entry = next((v for sub, v in names.items() if sub in k), None)
+        if entry is None or k not in write:
+            continue
+        fb, wb = fv * 1024.0 * f_scale, write[k] * 1024.0 * w_scale
+        out["kernels"][entry] = {"fetch_bytes": round(fb), "write_bytes": round(wb),
+                                 "hbm_bytes_per_launch": round(fb + wb)}
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out), flush=True)
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by the copy calibration),
+    or None when no summary for it exists."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 # ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser()
@@ -198,7 +270,17 @@ def main():
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run one plain device copy of 2 GiB (reference dispatch for the HBM counters)")
+    ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CALIB_FETCH_CSV", "CALIB_WRITE_CSV"),
+                    help="write the HBM traffic summary from rocprofv3 counter CSVs and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.summarize_counters:
+        summarize_counters(*args.summarize_counters)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path shards by "
               "head across GPUs and is not run multi-GPU here", file=sys.stderr)
@@ -306,7 +388,8 @@ def main():
     dom_ms = kt[dom][1]
     roof = {"kernel": dom, "bound": "mfma", "achieved": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12, 2),
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "traffic": None}
+            "frac": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "traffic": measured_traffic(dom)}
     att_ms = sum(kt[n][1] for n in attn if n in kt)
 
     dense = None

@@ -107,20 +107,39 @@ __device__ __forceinline__ void stage_wait(int after) {  // after = n - 1 - j
   dma_wait_le<0>();
 }
 
-// Wave-uniform ring of the next NST list entries (scalar registers).
+// Wave-uniform ring of the next NST list entries.  The list is read 64
+// entries at a time into one VGPR (lane i holds entry 64c + i) and entries are
+// extracted with v_readlane, so there is no per-entry load on the critical
+// path.  The next window is loaded 64 entries ahead; the compiler's wait for
+// it (first use at the window switch) drains the copies in flight once per 64
+// entries.
 template <int NST>
 struct EntryRing {
-  int e[NST];  // entries j .. j + NST - 1 (0 past the end of the list)
+  int e[NST];   // entries j .. j + NST - 1 (0 past the end of the list)
+  int win_cur;  // lane i: entry 64 c + i
+  int win_nxt;  // lane i: entry 64 (c + 1) + i
+  // entries are requested in order, and the window switches exactly when the
+  // requested index reaches a multiple of 64, so entry k is always in win_cur
+  __device__ __forceinline__ int get(int k) const { return __builtin_amdgcn_readlane(win_cur, k & 63); }
   __device__ __forceinline__ void init(const int32_t* U, int n) {
+    const int lane = (int)(threadIdx.x & 63);
+    win_cur = lane < n ? U[lane] : 0;
+    win_nxt = 64 + lane < n ? U[64 + lane] : 0;
 #pragma unroll
-    for (int k = 0; k < NST; ++k) e[k] = k < n ? sload_i32(U + k) : 0;
+    for (int k = 0; k < NST; ++k) e[k] = k < n ? get(k) : 0;
   }
   // entry j; shifts the ring to j + 1
   __device__ __forceinline__ int advance(const int32_t* U, int n, int j) {
     const int cur = e[0];
 #pragma unroll
     for (int k = 0; k + 1 < NST; ++k) e[k] = e[k + 1];
-    e[NST - 1] = j + NST < n ? sload_i32(U + j + NST) : 0;
+    const int k = j + NST;
+    if ((k & 63) == 0 && k < n) {
+      const int lane = (int)(threadIdx.x & 63);
+      win_cur = win_nxt;
+      win_nxt = k + 64 + lane < n ? U[k + 64 + lane] : 0;
+    }
+    e[NST - 1] = k < n ? get(k) : 0;
     return cur;
   }
 };
