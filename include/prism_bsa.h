@@ -108,13 +108,38 @@ int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, 
 int prism_scatter_rows(const void* in_rows, int B, int H, int64_t S, int D, const int64_t* shape_ids, int T,
                        int Hg, int Wg, void* out, int out_dtype, hipStream_t stream);
 
+/* Uniform chunk layout (the fixed-shape BSA of flash_attn_bsa_3d and
+ * flash_attn_bsa_cross, bsa_interface.py:1123-1176, 1276-1392):
+ * rearrange_THW_to_3d_block (bsa_interface.py:1105-1109) fused with the
+ * padding of the grid to a multiple of the chunk (:1263-1273, :1318-1367) and
+ * with (masked_)mean_pooling_compression (:164-201).
+ * x: [B,H,T*Hg*Wg,D] THW order over the input grid; the padded grid Tp x Hp x Wp
+ * (multiples of ct x ch x cw, chunk of 64 or 128 tokens) is cut into chunks
+ * n = (nt*Nh + nh)*Nw + nw, each owning rows [n*csz, (n+1)*csz) in
+ * (it*ch + ih)*cw + iw order; tokens outside the input grid and rows in
+ * [Tp*Hp*Wp, S_out) are padding (zero rows, invalid).  S_out: rows per head of
+ * the outputs, a multiple of 128.  valid: [T*Hg*Wg] uint8 or NULL.  Outputs as
+ * prism_gather_pool with N_b = Tp*Hp*Wp / csz blocks (means over the valid
+ * tokens of each chunk, count clamped to 1). */
+int prism_chunk_gather_pool(const void* x, int dtype, int B, int H, int D, const uint8_t* valid, int T, int Hg,
+                            int Wg, int Tp, int Hp, int Wp, int ct, int ch, int cw, int64_t S_out, void* out_rows,
+                            float* block_mean, int32_t* block_count, int32_t* tile_count, uint8_t* valid_re,
+                            const void* dot_with, float* rowdot, hipStream_t stream);
+
+/* rearrange_3d_block_to_THW (bsa_interface.py:1111-1115) plus the unpadding
+ * slice (:1372-1380): tile-order bf16 rows [B,H,S_out,D] of the chunk layout
+ * above -> [B,H,T*Hg*Wg,D] THW rows of out_dtype (padding rows dropped). */
+int prism_chunk_scatter_rows(const void* in_rows, int B, int H, int D, int T, int Hg, int Wg, int Tp, int Hp, int Wp,
+                             int ct, int ch, int cw, int64_t S_out, void* out, int out_dtype, hipStream_t stream);
+
 /* ------------------------------------------------------------------ selection */
 
 /* cal_score (bsa_interface.py:203-207) in fp32 with the invalid-key fill of
- * dynamic_block_attention.py:276-279 (block_count[j] == 0 -> -inf; NULL = none).
- * qc, kc: [BH, N, D] fp32; scores: [BH, N, N] fp32. */
-int prism_block_scores(const float* qc, const float* kc, const int32_t* block_count, int BH, int64_t N, int D,
-                       float* scores, hipStream_t stream);
+ * dynamic_block_attention.py:276-279 (block_count[j] == 0 -> -inf; NULL = none,
+ * as in the uniform path, bsa_interface.py:611-631).
+ * qc: [BH, Nq, D], kc: [BH, Nk, D] fp32; scores: [BH, Nq, Nk] fp32. */
+int prism_block_scores(const float* qc, const float* kc, const int32_t* block_count, int BH, int64_t Nq, int64_t Nk,
+                       int D, float* scores, hipStream_t stream);
 
 /* Per-row block selection fused with the block -> tile expansion:
  *   mode 0: get_select_indices_topk_from_score (bsa_interface.py:235-248), k = k_lo;
@@ -123,7 +148,8 @@ int prism_block_scores(const float* qc, const float* kc, const int32_t* block_co
  * ub as the reference derives it; thr = cumulative threshold in 2^-60 fixed
  * point (smallest X with fl32(X) 2^-60 >= p).  Expansion and padded-tile
  * filtering: dynamic_block_attention.py:297-319 (tile_count NULL = keep all).
- * tiles: [rows, tcap] ascending tile ids, ntiles: [rows];
+ * tiles: [rows, tcap] ascending tile ids (tcap >= the tiles of the widest
+ * selection: tiles per block x selected blocks), ntiles: [rows];
  * sel_blocks: [rows, bcap] ascending block ids (NULL to skip), nsel: [rows]. */
 int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, int64_t k_lo, int64_t ub,
                        float scale, uint64_t thr, const int32_t* block_first_tile, const int32_t* tile_count,
@@ -140,29 +166,30 @@ int prism_tile_rows(const int32_t* ntiles, const int32_t* block_id_of_tile, cons
                     int64_t Nt, int64_t N_b, int64_t tcap, int64_t* qstart, int32_t* qlen, hipStream_t stream);
 
 /* create_indices_k_from_indices_q_varlen (bsa_interface.py:147-161) as a
- * bitmap transpose.  bitmap: workspace of BH*Nt*ceil(Nt/32) uint32.
- * Output per key tile (row bh*Nt + k): kstart = row*kcap, klen, kcols
- * ascending query tiles. */
-int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH, int64_t Nt,
-                          uint32_t* bitmap, int64_t kcap, int64_t* kstart, int32_t* klen, int32_t* kcols,
-                          hipStream_t stream);
+ * bitmap transpose.  Input rows bh*Ntq + t list key tiles < Ntk.
+ * bitmap: workspace of BH*Ntk*ceil(Ntq/32) uint32.  Output per key tile
+ * (row bh*Ntk + k): kstart = row*kcap (kcap >= Ntq), klen, kcols ascending
+ * query tiles. */
+int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH, int64_t Ntq,
+                          int64_t Ntk, uint32_t* bitmap, int64_t kcap, int64_t* kstart, int32_t* klen,
+                          int32_t* kcols, hipStream_t stream);
 
 /* ------------------------------------------------------------------ attention */
 
 /* Work lists of the paired-tile attention kernels.  Every attention kernel runs
  * one workgroup per pair of tiles (2p, 2p+1) and walks the sorted union of the
  * two tiles' lists.  For pair p (rows 2p, 2p+1 of a per-row list; rows =
- * BH*Nt, Nt even): ucols[ustart[p] .. + ulen[p]) ascending entries
+ * BH*row_tiles, row_tiles even; entries are tiles < col_tiles):
+ * ucols[ustart[p] .. + ulen[p]) ascending entries
  * tile << 3 | partial << 2 | in_row_2p+1 << 1 | in_row_2p, where partial =
  * (tile_masks != NULL && tile_masks[tile] != all ones), tile_masks from
- * prism_tile_masks.  ustart[p] = p * ucap,
- * ucap >= Nt.  Used on the per-query-tile key lists (forward, dQ; the
+ * prism_tile_masks.  ustart[p] = p * ucap, ucap >= col_tiles.  Used on the per-query-tile key lists (forward, dQ; the
  * reference's block_indices, bsa_interface.py:328-385) and on the per-key-tile
  * query lists of prism_transpose_lists (dK/dV; bsa_interface.py:437-447).
  * No counterpart routine in the reference: its kernels take one list per tile. */
-int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t Nt,
-                     const uint64_t* tile_masks, int64_t ucap, int64_t* ustart, int32_t* ulen, int32_t* ucols,
-                     hipStream_t stream);
+int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
+                     int64_t col_tiles, const uint64_t* tile_masks, int64_t ucap, int64_t* ustart, int32_t* ulen,
+                     int32_t* ucols, hipStream_t stream);
 
 /* Key validity per 64-token tile (the reference's kv_valid_mask,
  * bsa_interface.py:328-385, flash_attn_bsa_varlen_mask.py:263-295) packed as
@@ -175,15 +202,17 @@ int prism_tile_masks(const uint8_t* valid, int64_t Nt, uint64_t* masks, hipStrea
 int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
 
 /* attn_fwd_bsa_varlen_triton (bsa_interface.py:328-385) with
- * _attn_fwd_bsa_varlen_align (flash_attn_bsa_varlen_mask.py:191-319), chunk 64.
- * S must be a multiple of 128 (query tiles are processed in pairs).
- * q, k, v: [BH,S,D] bf16 tile order; ustart/ulen/ucols: prism_pair_union of the
- * per-query-tile key lists with the same tile_masks (prism_tile_masks of the
- * key validity, or NULL when no key is padded).  o: [BH,S,D] bf16; lse: [BH,S] fp32 natural log (-inf for rows
- * without a valid key; their o is 0). */
-int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S, int D, const uint64_t* tile_masks,
-                  const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* o,
-                  float* lse, hipStream_t stream);
+ * _attn_fwd_bsa_varlen_align (flash_attn_bsa_varlen_mask.py:191-319), on
+ * 64-token tiles (larger chunks are lists of their tiles).  Sq, Sk (query and
+ * key rows per head; equal for self-attention) must be multiples of 128
+ * (tiles are processed in pairs).  q: [BH,Sq,D], k, v: [BH,Sk,D] bf16 tile
+ * order; ustart/ulen/ucols: prism_pair_union of the per-query-tile key lists
+ * with the same tile_masks (prism_tile_masks of the key validity, or NULL when
+ * no key is padded).  o: [BH,Sq,D] bf16; lse: [BH,Sq] fp32 natural log (-inf
+ * for rows without a valid key; their o is 0). */
+int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
+                  const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen, const int32_t* ucols,
+                  float sm_scale, void* o, float* lse, hipStream_t stream);
 
 /* _attn_bwd_preprocess (common.py:110-127): delta[r] = sum_d o[r][d] * do[r][d]
  * over rows of bf16 [rows, D] tensors; fp32 out. */
@@ -191,21 +220,23 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 
 /* dK, dV of attn_bwd_bsa_varlen_triton (bsa_interface.py:387-487;
  * _attn_bwd_dkdv_bsa_varlen_wrapper, flash_attn_bsa_varlen_mask.py:562-704).
- * q, k, v, do_: [BH,S,D] bf16 tile order; m2 from prism_lse_to_m2; delta from
- * prism_gather_pool or prism_bwd_preprocess; kv_valid: [S] uint8 tile order
- * or NULL; ustart/ulen/ucols: prism_pair_union of the per-key-tile query
- * lists of prism_transpose_lists (tile_masks NULL).  dk, dv: [BH,S,D] bf16. */
+ * q, do_: [BH,Sq,D], k, v: [BH,Sk,D] bf16 tile order; m2 [BH,Sq] from
+ * prism_lse_to_m2; delta [BH,Sq] from prism_gather_pool or
+ * prism_bwd_preprocess; kv_valid: [Sk] uint8 tile order or NULL;
+ * ustart/ulen/ucols: prism_pair_union of the per-key-tile query lists of
+ * prism_transpose_lists (tile_masks NULL).  dk, dv: [BH,Sk,D] bf16. */
 int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
-                       const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid, const int64_t* ustart,
-                       const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk, void* dv,
-                       hipStream_t stream);
+                       const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint8_t* kv_valid,
+                       const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk,
+                       void* dv, hipStream_t stream);
 
 /* dQ of attn_bwd_bsa_varlen_triton (bsa_interface.py:489-523;
  * _attn_bwd_dq_bsa_varlen_align_wrapper, flash_attn_bsa_varlen_mask.py:879-1014).
- * Lists and tile_masks as for prism_bsa_fwd; dq: [BH,S,D] bf16. */
+ * Shapes as for prism_bsa_bwd_dkdv; lists and tile_masks as for
+ * prism_bsa_fwd; dq: [BH,Sq,D] bf16. */
 int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
-                     int BH, int64_t S, int D, const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen,
-                     const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream);
+                     int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart,
+                     const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream);
 
 #ifdef __cplusplus
 }

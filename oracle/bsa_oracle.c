@@ -491,19 +491,19 @@ void oc_block_pool(const void *x, int dtype, int B, int H, int64_t S, int D,
  * dynamic_block_attention.py:278-279.  Canonical: fp32 fmaf chain over d in
  * increasing order from +0.  scores: [BH, N, N]. */
 void oc_block_scores(const float *qc, const float *kc, const int32_t *block_count,
-                     int BH, int64_t N, int D, float *scores) {
+                     int BH, int64_t Nq, int64_t Nk, int D, float *scores) {
     for (int bh = 0; bh < BH; ++bh)
-        for (int64_t i = 0; i < N; ++i) {
-            const float *q = qc + ((int64_t)bh * N + i) * D;
-            for (int64_t j = 0; j < N; ++j) {
+        for (int64_t i = 0; i < Nq; ++i) {
+            const float *q = qc + ((int64_t)bh * Nq + i) * D;
+            for (int64_t j = 0; j < Nk; ++j) {
                 float s;
                 if (block_count && block_count[j] == 0) s = -INFINITY;
                 else {
-                    const float *k = kc + ((int64_t)bh * N + j) * D;
+                    const float *k = kc + ((int64_t)bh * Nk + j) * D;
                     s = 0.0f;
                     for (int d = 0; d < D; ++d) s = fmaf(q[d], k[d], s);
                 }
-                scores[((int64_t)bh * N + i) * N + j] = s;
+                scores[((int64_t)bh * Nq + i) * Nk + j] = s;
             }
         }
 }
@@ -612,15 +612,16 @@ void oc_expand_tiles(const int64_t *sel, const int32_t *nsel, int64_t rows, int6
  * (bsa_interface.py:147-161) as a list transpose.  Input: per q tile
  * (row = bh*Nt + t) a list at qstart[row], length qlen[row].  Output: per k
  * tile the ascending q tiles at row*Nt, klen[row]. */
+/* rows bh*Ntq + t list key tiles < Ntk; output rows bh*Ntk + k, stride Ntq */
 void oc_transpose_lists(const int64_t *qstart, const int32_t *qlen, const int32_t *qcols,
-                        int BH, int64_t Nt, int32_t *kcols, int32_t *klen) {
-    for (int64_t i = 0; i < (int64_t)BH * Nt; ++i) klen[i] = 0;
+                        int BH, int64_t Ntq, int64_t Ntk, int32_t *kcols, int32_t *klen) {
+    for (int64_t i = 0; i < (int64_t)BH * Ntk; ++i) klen[i] = 0;
     for (int bh = 0; bh < BH; ++bh)
-        for (int64_t t = 0; t < Nt; ++t) {
-            int64_t row = (int64_t)bh * Nt + t;
+        for (int64_t t = 0; t < Ntq; ++t) {
+            int64_t row = (int64_t)bh * Ntq + t;
             for (int i = 0; i < qlen[row]; ++i) {
-                int64_t kr = (int64_t)bh * Nt + qcols[qstart[row] + i];
-                kcols[kr * Nt + klen[kr]++] = (int32_t)t;
+                int64_t kr = (int64_t)bh * Ntk + qcols[qstart[row] + i];
+                kcols[kr * Ntq + klen[kr]++] = (int32_t)t;
             }
         }
 }

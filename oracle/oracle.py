@@ -61,7 +61,9 @@ def lib():
 
 
 def _p(a: Optional[np.ndarray]):
-    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+    # data_as keeps a reference to the array, so a temporary made inside an
+    # argument list (np.ascontiguousarray copy) lives until the call returns
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
 def _dtype_code(a: np.ndarray) -> int:
@@ -221,15 +223,127 @@ def block_pool(x: np.ndarray, shape_ids, grid, valid=None):
     return out, bc, tc
 
 
+# ---------------------------------------------------------------- uniform chunk layout
+def padded_grid(grid, chunk):
+    """Grid rounded up to multiples of the chunk (bsa_interface.py:1318-1331)."""
+    return tuple(-(-g // c) * c for g, c in zip(grid, chunk))
+
+
+def chunk_source_index(grid, pgrid, chunk, rows: Optional[int] = None) -> np.ndarray:
+    """rearrange_THW_to_3d_block (bsa_interface.py:1105-1109) as a source
+    index over the padded grid: src[p] = THW token (of the unpadded grid) of
+    rearranged row p, -1 for padding (tokens outside the grid, and rows
+    p >= Tp*Hp*Wp up to ``rows``)."""
+    T, H, W = grid
+    Tp, Hp, Wp = pgrid
+    ct, ch, cw = chunk
+    t = np.arange(Tp)[:, None, None]
+    h = np.arange(Hp)[None, :, None]
+    w = np.arange(Wp)[None, None, :]
+    tok = np.where((t < T) & (h < H) & (w < W), (t * H + h) * W + w, -1)
+    src = tok.reshape(Tp // ct, ct, Hp // ch, ch, Wp // cw, cw).transpose(0, 2, 4, 1, 3, 5).reshape(-1)
+    if rows is not None and rows > src.size:
+        src = np.concatenate([src, np.full(rows - src.size, -1, src.dtype)])
+    return src.astype(np.int64)
+
+
+def chunk_pool(x: np.ndarray, src: np.ndarray, valid: Optional[np.ndarray], csz: int, n_blocks: int):
+    """(masked_)mean_pooling_compression (bsa_interface.py:164-201) of the
+    rearranged rows: per chunk, the fp32 sum of its valid rows taken in row
+    order, divided by max(count, 1).  x: [B,H,S_in,D] float32 (bf16 values
+    widened).  Returns (means [B,H,n_blocks,D] fp32, counts [n_blocks])."""
+    x = np.asarray(x, np.float32)
+    rows = src[: n_blocks * csz].reshape(n_blocks, csz)
+    ok = rows >= 0
+    if valid is not None:
+        ok &= np.asarray(valid).astype(bool)[np.maximum(rows, 0)]
+    B, H, _, D = x.shape
+    acc = np.zeros((B, H, n_blocks, D), np.float32)
+    for j in range(csz):
+        xj = x[:, :, np.maximum(rows[:, j], 0), :]
+        acc = np.where(ok[None, None, :, j, None], acc + xj, acc)
+    cnt = ok.sum(axis=1).astype(np.int32)
+    mean = acc / np.maximum(cnt, 1).astype(np.float32)[None, None, :, None]
+    return mean.astype(np.float32), cnt
+
+
+def chunk_rows(x: np.ndarray, src: np.ndarray) -> np.ndarray:
+    """Rearranged rows [B,H,len(src),D] with zero rows at padding."""
+    out = np.zeros(x.shape[:2] + (src.size, x.shape[3]), x.dtype)
+    ok = src >= 0
+    out[:, :, ok] = x[:, :, src[ok]]
+    return out
+
+
+def chunk_kblock_tiles(n_blocks: int, csz: int, Nt: int) -> np.ndarray:
+    """[n_blocks + 1, 2] tiles of each chunk (second = Nt for 64-token chunks),
+    the kblock_tiles form expand_tiles takes."""
+    b = np.arange(n_blocks + 1, dtype=np.int64)
+    if csz == 64:
+        kbt = np.stack([b, np.full_like(b, Nt)], 1)
+    else:
+        kbt = np.stack([2 * b, 2 * b + 1], 1)
+    kbt[n_blocks] = Nt
+    return kbt
+
+
+def uniform_pipeline(q, k, q_grid, k_grid, chunk_q, chunk_k, *, sparsity=0.875, cdf_threshold_p=None,
+                     q_valid=None, k_valid=None, q_pad_rows=None, k_pad_rows=None, skip_padded_queries=False):
+    """Selection half of _attention_bsa.forward (bsa_interface.py:600-640) on
+    the uniform chunk layout: rearranged rows, pooled means, fp32 scores (no
+    invalid-key fill), selection, per-query-tile key-tile lists.  q/k:
+    [B,H,S,D] THW float32; q_valid/k_valid: THW validity or None (padding of
+    the grid is always invalid); *_pad_rows: rows per head (multiple of 128)."""
+    B, H, _, D = q.shape
+    sm_scale = 1.0 / (D ** 0.5)
+    side = {}
+    for name, x, grid, chunk, valid, rows in (("q", q, q_grid, chunk_q, q_valid, q_pad_rows),
+                                               ("k", k, k_grid, chunk_k, k_valid, k_pad_rows)):
+        pg = padded_grid(grid, chunk)
+        csz = int(np.prod(chunk))
+        Sp = int(np.prod(pg))
+        rows = rows or -(-Sp // 128) * 128
+        src = chunk_source_index(grid, pg, chunk, rows)
+        nb = Sp // csz
+        mean, cnt = chunk_pool(x, src, valid, csz, nb)
+        okrow = src >= 0
+        if valid is not None:
+            okrow &= np.asarray(valid).astype(bool)[np.maximum(src, 0)]
+        side[name] = dict(pgrid=pg, csz=csz, src=src, nb=nb, mean=mean, count=cnt, rows=rows, Nt=rows // TILE,
+                          valid_re=okrow.astype(np.uint8),
+                          tile_count=okrow.reshape(-1, TILE).sum(1).astype(np.int32),
+                          masked=valid is not None or bool((src[:Sp] < 0).any()) or rows > Sp)
+    sq, sk = side["q"], side["k"]
+    scores = block_scores(sq["mean"].reshape(B * H, sq["nb"], D), sk["mean"].reshape(B * H, sk["nb"], D), None)
+    sel, nsel = select(scores, sparsity, cdf_threshold_p, sm_scale)
+    kbt = chunk_kblock_tiles(sk["nb"], sk["csz"], sk["Nt"])
+    tiles, ntiles = expand_tiles(sel, nsel, kbt, sk["Nt"], sk["tile_count"] if sk["masked"] else None)
+    tcap = tiles.shape[1]
+    tpb_q = sq["csz"] // TILE
+    Ntq = sq["Nt"]
+    bid = np.minimum(np.arange(Ntq) // tpb_q, sq["nb"] - 1)
+    rows_q = (np.arange(B * H)[:, None] * sq["nb"] + bid[None, :]).reshape(-1)
+    qstart = rows_q * tcap
+    qlen = ntiles[rows_q].astype(np.int32)
+    empty_q = sq["tile_count"] == 0
+    pad_tiles = np.arange(Ntq) * TILE >= int(np.prod(sq["pgrid"]))
+    drop = pad_tiles | (empty_q if (skip_padded_queries and sq["masked"]) else np.zeros(Ntq, bool))
+    qlen = np.where(np.tile(drop, B * H), 0, qlen).astype(np.int32)
+    return dict(q=sq, k=sk, scores=scores, sel=sel, nsel=nsel, tiles=tiles, ntiles=ntiles, qstart=qstart, qlen=qlen,
+                qcols=tiles.reshape(-1))
+
+
 def block_scores(qc: np.ndarray, kc: np.ndarray, block_count: Optional[np.ndarray]):
     """cal_score + invalid-key fill (bsa_interface.py:203-207,
-    dynamic_block_attention.py:276-279).  qc, kc: [BH, N, D] fp32."""
-    BH, N, D = qc.shape
-    out = np.zeros((BH, N, N), np.float32)
+    dynamic_block_attention.py:276-279).  qc: [BH, Nq, D], kc: [BH, Nk, D]
+    fp32 -> [BH, Nq, Nk]."""
+    BH, Nq, D = qc.shape
+    Nk = kc.shape[1]
+    out = np.zeros((BH, Nq, Nk), np.float32)
     bc = None if block_count is None else np.ascontiguousarray(block_count, dtype=np.int32)
     lib().oc_block_scores(_p(np.ascontiguousarray(qc, dtype=np.float32)),
-                          _p(np.ascontiguousarray(kc, dtype=np.float32)), _p(bc), BH, ctypes.c_int64(N), D,
-                          _p(out))
+                          _p(np.ascontiguousarray(kc, dtype=np.float32)), _p(bc), BH, ctypes.c_int64(Nq),
+                          ctypes.c_int64(Nk), D, _p(out))
     return out
 
 
@@ -276,15 +390,17 @@ def expand_tiles(sel, nsel, kblock_tiles, Nt, tile_count=None):
     return tiles, nt
 
 
-def transpose_lists(qstart, qlen, qcols, BH, Nt):
-    """k-tile -> ascending q-tile lists (bsa_interface.py:147-161)."""
-    kcols = np.full(BH * Nt * Nt, -1, np.int32)
-    klen = np.zeros(BH * Nt, np.int32)
+def transpose_lists(qstart, qlen, qcols, BH, Nt, Ntk=None):
+    """k-tile -> ascending q-tile lists (bsa_interface.py:147-161).  Nt query
+    tiles per head listing key tiles < Ntk (default Nt)."""
+    Ntk = Nt if Ntk is None else Ntk
+    kcols = np.full(BH * Ntk * Nt, -1, np.int32)
+    klen = np.zeros(BH * Ntk, np.int32)
     lib().oc_transpose_lists(_p(np.ascontiguousarray(qstart, dtype=np.int64)),
                              _p(np.ascontiguousarray(qlen, dtype=np.int32)),
                              _p(np.ascontiguousarray(qcols, dtype=np.int32)), BH, ctypes.c_int64(Nt),
-                             _p(kcols), _p(klen))
-    return kcols.reshape(BH * Nt, Nt), klen
+                             ctypes.c_int64(Ntk), _p(kcols), _p(klen))
+    return kcols.reshape(BH * Ntk, Nt), klen
 
 
 def tile_masks(valid: np.ndarray) -> np.ndarray:

@@ -1,10 +1,15 @@
 """Kernel-level API of the block-sparse attention path, MI355X implementation.
 
 Mirrors the functions of hymm/models/modules/block_sparse_attention/bsa_interface.py
-that the dynamic path uses (names, argument meaning, return layout), backed by
-libprism_bsa.so.  Only the tile-64 ("align") attention variant exists: it is
-the one the dynamic path reaches (chunk 64, dynamic_block_attention.py:322-326);
-other chunk sizes raise ValueError.
+(names, argument meaning, return layout), backed by libprism_bsa.so:
+  * the helpers the dynamic path uses: cal_score, the three selection
+    helpers, attn_fwd_bsa_varlen / attn_bwd_bsa_varlen over given per-tile
+    lists (64-token tiles, the "align" variant the dynamic path reaches,
+    dynamic_block_attention.py:322-326; other chunk sizes raise ValueError),
+    create_indices_k_from_indices_q_varlen;
+  * the uniform-shape entry points flash_attn_bsa, flash_attn_bsa_3d and
+    flash_attn_bsa_cross (prism_amd.uniform_block_attention; chunks of 64 or
+    128 tokens).
 """
 from __future__ import annotations
 
@@ -13,6 +18,7 @@ from typing import Optional
 import torch
 
 from . import ops
+from .uniform_block_attention import flash_attn_bsa, flash_attn_bsa_3d, flash_attn_bsa_cross  # noqa: F401
 
 
 def cal_score(q: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
@@ -76,9 +82,9 @@ def attn_fwd_bsa_varlen(q, k, v, sm_scale, block_indices, block_indices_lens, ch
     Returns (o [B,H,S,D], lse [B,H,S] natural log)."""
     _check_chunks(chunk_size_q, chunk_size_k)
     qstart, qlen, qcols = _lists_from_dense(block_indices, block_indices_lens)
-    Nt = q.shape[2] // 64
+    Ntq, Ntk = q.shape[2] // 64, k.shape[2] // 64
     tm = ops.tile_masks(ops._u8(kv_valid_mask))
-    qunion = ops.pair_union(qstart, qlen, qcols, Nt, tm)
+    qunion = ops.pair_union(qstart, qlen, qcols, Ntq, tm, col_tiles=Ntk)
     return ops.bsa_fwd(q, k, v, tm, qunion, sm_scale)
 
 
@@ -86,15 +92,14 @@ def create_indices_k_from_indices_q_varlen(block_indices: torch.Tensor, N_cols_m
     """Per-key-tile ascending query lists (bsa_interface.py:147-161).
     Returns ([B,H,N_cols,M] padded with M, lens [B,H,N_cols])."""
     B, H, M, W = block_indices.shape
-    if M != N_cols_mask:
-        raise ValueError("square tile lists only (query tiles == key tiles)")
-    lens = (block_indices < N_cols_mask).sum(-1).to(torch.int32)
+    N = int(N_cols_mask)
+    lens = (block_indices < N).sum(-1).to(torch.int32)
     qstart, qlen, qcols = _lists_from_dense(block_indices, lens)
-    kstart, klen, kcols = ops.transpose_lists(qstart, qlen, qcols, B * H, M)
-    kc = kcols.view(B, H, M, M)
+    kstart, klen, kcols = ops.transpose_lists(qstart, qlen, qcols, B * H, M, N)
+    kc = kcols.view(B, H, N, M)
     pos = torch.arange(M, device=kc.device).view(1, 1, 1, M)
-    kc = torch.where(pos < klen.view(B, H, M, 1), kc, torch.full_like(kc, M)).to(torch.int64)
-    return kc, klen.view(B, H, M)
+    kc = torch.where(pos < klen.view(B, H, N, 1), kc, torch.full_like(kc, M)).to(torch.int64)
+    return kc, klen.view(B, H, N)
 
 
 def attn_bwd_bsa_varlen(do, q, k, v, o, dq, dk, dv, sm_scale, lse, block_indices, block_indices_lens,
@@ -104,17 +109,17 @@ def attn_bwd_bsa_varlen(do, q, k, v, o, dq, dk, dv, sm_scale, lse, block_indices
     natural-log LSE returned by the forward."""
     _check_chunks(chunk_size_q, chunk_size_k)
     B, H, S, D = q.shape
-    Nt = S // 64
+    Ntq, Ntk = S // 64, k.shape[2] // 64
     qstart, qlen, qcols = _lists_from_dense(block_indices, block_indices_lens)
     do = do.to(torch.bfloat16).contiguous()
     o = o.to(torch.bfloat16).contiguous()
     delta = torch.empty((B, H, S), device=q.device, dtype=torch.float32)
     ops._call("prism_bwd_preprocess", o.data_ptr(), do.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
-    klists = ops.transpose_lists(qstart, qlen, qcols, B * H, Nt)
+    klists = ops.transpose_lists(qstart, qlen, qcols, B * H, Ntq, Ntk)
     kv = ops._u8(kv_valid_mask)
     tm = ops.tile_masks(kv)
-    qunion = ops.pair_union(qstart, qlen, qcols, Nt, tm)
-    kunion = ops.pair_union(*klists, Nt)
+    qunion = ops.pair_union(qstart, qlen, qcols, Ntq, tm, col_tiles=Ntk)
+    kunion = ops.pair_union(*klists, Ntk, None, col_tiles=Ntq)
     m2 = ops.lse_to_m2(lse)
     g_q, g_k, g_v = ops.bsa_bwd(q, k, v, do, m2, delta, kv, tm, qunion, kunion, sm_scale)
     dq.copy_(g_q)
@@ -126,5 +131,5 @@ def attn_bwd_bsa_varlen(do, q, k, v, o, dq, dk, dv, sm_scale, lse, block_indices
 __all__ = [
     "cal_score", "get_select_indices_topk_from_score", "get_select_indices_cdf_from_score",
     "get_select_indices_cdf_topk_from_score", "attn_fwd_bsa_varlen", "attn_bwd_bsa_varlen",
-    "create_indices_k_from_indices_q_varlen",
+    "create_indices_k_from_indices_q_varlen", "flash_attn_bsa", "flash_attn_bsa_3d", "flash_attn_bsa_cross",
 ]

@@ -9,29 +9,28 @@
 //   inner loop :479-541).  Both passes are deterministic (no atomics), as in the
 //   reference.
 //
-// Layouts (per head, tile order): Q, K, V, dO row-major [S][D]; m2 = lse *
-// log2(e) with rows that saw no valid key at +inf (prism_lse_to_m2).
+// Layouts (per head, tile order): Q, dO row-major [Sq][D], K, V [Sk][D]
+// (Sq = Sk for self-attention); m2 = lse * log2(e) with rows that saw no valid
+// key at +inf (prism_lse_to_m2).
 //
 // MI355X design, shared by both kernels:
-//  * one workgroup of 8 waves per PAIR of tiles (2p, 2p+1), one workgroup per
-//    CU (two waves per SIMD), walking the sorted union of the two tiles' lists
-//    (prism_pair_union);
+//  * one workgroup per PAIR of tiles (2p, 2p+1) walking the sorted union of
+//    the two tiles' lists (prism_pair_union);
 //  * the operand tiles of list entry j + NST - 1 are copied HBM -> LDS by
 //    global_load_lds_dwordx4 while entry j is multiplied (NST = 3 stages for
-//    dK/dV, 4 for dQ; one barrier per entry, no VGPR staging);
+//    dK/dV, 2 for dQ; one barrier per entry, no VGPR staging);
 //  * all operands come from row-major tiles: row reads (ds_read_b128) for the
 //    S / dP products, transposing reads (ds_read_b64_tr_b16) for the products
 //    that contract over the tile's rows (see RowTile), so no transposed
 //    copies of Q, K or dO are made;
-//  * the eight waves split the work of each (tile, tile) product in two
-//    halves of the contracted dimension, so every wave holds half-size
-//    partial accumulators; the two partials are added in a fixed order
-//    through LDS at the end (deterministic);
 //  * workgroup ids are remapped per XCD (xcd_group_remap: runs of
 //    neighbouring pairs per L2, one head region at a time GPU-wide).
-// dK/dV: wave w owns keys [32 kh, 32 kh + 32) of tile 2p + tk and query rows
-// [32 qh, 32 qh + 32) of every listed query tile (kh = w & 1, tk = (w >> 1) & 1,
-// qh = w >> 2).  S = Q K^T and dP = dO V^T keep one key per lane column, so P
+// dK/dV: one 8-wave workgroup per CU (two waves per SIMD).  The waves split
+// each (tile, tile) product in two halves of the query rows, so every wave
+// holds half-size partial accumulators; the two partials are added in a
+// fixed order through LDS at the end (deterministic).  Wave w owns keys
+// [32 kh, 32 kh + 32) of tile 2p + tk and query rows [32 qh, 32 qh + 32) of
+// every listed query tile (kh = w & 1, tk = (w >> 1) & 1, qh = w >> 2).  S = Q K^T and dP = dO V^T keep one key per lane column, so P
 // and dS feed the B operand of dV^T = dO^T P and dK^T = Q^T dS straight from
 // the accumulators.
 // dQ: two 4-wave workgroups per CU (their phases drift apart, so one's
@@ -47,15 +46,15 @@ namespace {
 
 struct BwdArgs {
   const uint16_t *q, *k, *v, *do_;
-  const float* m2;          // [BH, S] base-2 row max (lse * log2 e, +inf for empty rows)
-  const float* delta;       // [BH, S]
-  const uint8_t* kv_valid;  // [S] tile order or null (dK/dV)
-  const uint64_t* tmask;    // [Nt] per-tile key validity or null (dQ)
+  const float* m2;          // [BH, Sq] base-2 row max (lse * log2 e, +inf for empty rows)
+  const float* delta;       // [BH, Sq]
+  const uint8_t* kv_valid;  // [Sk] tile order or null (dK/dV)
+  const uint64_t* tmask;    // [Sk/64] per-tile key validity or null (dQ)
   const int64_t* ustart;    // pair-union lists
   const int32_t* ulen;
   const int32_t* ucols;
-  int64_t S, Nt;
-  int npairs;
+  int64_t Sq, Sk;
+  int npairs;               // tile pairs per head of the side the grid walks
   float sm_scale, scale_log2;
   uint16_t *dq, *dk, *dv;
 };
@@ -95,9 +94,9 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
   const int mybit = 1 << tk;
-  const int64_t hoff = (int64_t)bh * a.S * D;
-  const float* m2h = a.m2 + (int64_t)bh * a.S;
-  const float* dlh = a.delta + (int64_t)bh * a.S;
+  const int64_t qoff = (int64_t)bh * a.Sq * D, koff = (int64_t)bh * a.Sk * D;
+  const float* m2h = a.m2 + (int64_t)bh * a.Sq;
+  const float* dlh = a.delta + (int64_t)bh * a.Sq;
 
   // DMA plan: wave w issues KB-instructions w, w + 8, ... (Q then dO);
   // wave 7 also copies the m2 row and wave 6 the delta row of the entry.
@@ -106,7 +105,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   for (int s = 0; s < T::SLOTS; ++s) soff[s] = RT::src_offset((w + 8 * s) % RT::KB, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int qtile, int st) {
-    const int64_t toff = hoff + (int64_t)qtile * 64 * D;
+    const int64_t toff = qoff + (int64_t)qtile * 64 * D;
     const void* qb = uniform_ptr(a.q + toff);
     const void* db = uniform_ptr(a.do_ + toff);
     const uint32_t base = lds0 + (uint32_t)(st * SB);
@@ -135,8 +134,8 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   bf16x8 kf[NS], vf[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    kf[s] = ld_bf16x8(a.k + hoff + key * D + 16 * s + 8 * g);
-    vf[s] = ld_bf16x8(a.v + hoff + key * D + 16 * s + 8 * g);
+    kf[s] = ld_bf16x8(a.k + koff + key * D + 16 * s + 8 * g);
+    vf[s] = ld_bf16x8(a.v + koff + key * D + 16 * s + 8 * g);
   }
   const bool kvalid = a.kv_valid ? a.kv_valid[key] != 0 : true;
   const float kbias = kvalid ? 0.0f : -__builtin_inff();
@@ -214,8 +213,8 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   }
   __syncthreads();
   if (qh == 0) {
-    uint16_t* dkr = a.dk + hoff + key * D;
-    uint16_t* dvr = a.dv + hoff + key * D;
+    uint16_t* dkr = a.dk + koff + key * D;
+    uint16_t* dvr = a.dv + koff + key * D;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
@@ -254,7 +253,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
   const int mybit = 1 << tq;
-  const int64_t hoff = (int64_t)bh * a.S * D;
+  const int64_t qoff = (int64_t)bh * a.Sq * D, koff = (int64_t)bh * a.Sk * D;
   const float NINF = -__builtin_inff();
 
   // DMA plan: wave w issues KB-instructions w, w + 4, ... (K then V)
@@ -263,7 +262,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   for (int s = 0; s < SLOTS; ++s) soff[s] = RT::src_offset((w + 4 * s) % RT::KB, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int ktile, int st) {
-    const int64_t toff = hoff + (int64_t)ktile * 64 * D;
+    const int64_t toff = koff + (int64_t)ktile * 64 * D;
     const void* kb = uniform_ptr(a.k + toff);
     const void* vb = uniform_ptr(a.v + toff);
     const uint32_t base = lds0 + (uint32_t)(st * SB);
@@ -288,11 +287,11 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   bf16x8 qf[NS], df[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    qf[s] = ld_bf16x8(a.q + hoff + qrow * D + 16 * s + 8 * g);
-    df[s] = ld_bf16x8(a.do_ + hoff + qrow * D + 16 * s + 8 * g);
+    qf[s] = ld_bf16x8(a.q + qoff + qrow * D + 16 * s + 8 * g);
+    df[s] = ld_bf16x8(a.do_ + qoff + qrow * D + 16 * s + 8 * g);
   }
-  const float mq = a.m2[(int64_t)bh * a.S + qrow];
-  const float dlt = a.delta[(int64_t)bh * a.S + qrow];
+  const float mq = a.m2[(int64_t)bh * a.Sq + qrow];
+  const float dlt = a.delta[(int64_t)bh * a.Sq + qrow];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     consume_regs(qf[s]);
@@ -350,7 +349,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
     }
   }
 
-  uint16_t* dqr = a.dq + hoff + qrow * D;
+  uint16_t* dqr = a.dq + qoff + qrow * D;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -375,11 +374,12 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const uint16_t* __r
   if (lane == 0) delta[r] = part;
 }
 
-int check_common(const void* q, const void* k, int BH, int64_t S, int D, const char* who) {
+int check_common(const void* q, const void* k, int BH, int64_t Sq, int64_t Sk, int D, const char* who) {
   PRISM_REQUIRE(q && k, "%s: null pointer", who);
   PRISM_REQUIRE(D == 64 || D == 128, "%s: head_dim %d unsupported (64, 128)", who, D);
-  PRISM_REQUIRE(S > 0 && S % 128 == 0, "%s: S must be a positive multiple of 128", who);
-  PRISM_REQUIRE(BH >= 1 && (int64_t)BH * (S / 128) < (1ll << 31), "%s: BH out of range", who);
+  PRISM_REQUIRE(Sq > 0 && Sq % 128 == 0 && Sk > 0 && Sk % 128 == 0, "%s: Sq and Sk must be positive multiples of 128",
+                who);
+  PRISM_REQUIRE(BH >= 1 && (int64_t)BH * ((Sq > Sk ? Sq : Sk) / 128) < (1ll << 31), "%s: BH out of range", who);
   return PRISM_OK;
 }
 
@@ -399,16 +399,17 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 }
 
 int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
-                       const float* delta, int BH, int64_t S, int D, const uint8_t* kv_valid, const int64_t* ustart,
+                       const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint8_t* kv_valid,
+                       const int64_t* ustart,
                        const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk, void* dv,
                        hipStream_t stream) {
-  int rc = check_common(q, k, BH, S, D, "prism_bsa_bwd_dkdv");
+  int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dkdv");
   if (rc) return rc;
   PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dk && dv, "prism_bsa_bwd_dkdv: null pointer");
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
   a.m2 = m2; a.delta = delta; a.kv_valid = kv_valid;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.Sq = Sq; a.Sk = Sk; a.npairs = (int)(Sk / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
   if (D == 128) bsa_bwd_dkdv_kernel<128><<<blocks, 512, 0, stream>>>(a);
@@ -418,15 +419,15 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
 }
 
 int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
-                     int BH, int64_t S, int D, const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen,
+                     int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen,
                      const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream) {
-  int rc = check_common(q, k, BH, S, D, "prism_bsa_bwd_dq");
+  int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dq");
   if (rc) return rc;
   PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq: null pointer");
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
   a.m2 = m2; a.delta = delta; a.tmask = tile_masks;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64; a.npairs = (int)(S / 128);
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.Sq = Sq; a.Sk = Sk; a.npairs = (int)(Sq / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
   if (D == 128) bsa_bwd_dq_kernel<128><<<blocks, 256, 0, stream>>>(a);

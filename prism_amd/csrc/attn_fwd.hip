@@ -40,18 +40,18 @@
 namespace {
 
 struct FwdArgs {
-  const uint16_t* q;       // [BH, S, D] tile order
-  const uint16_t* k;       // [BH, S, D] tile order
-  const uint16_t* v;       // [BH, S, D] tile order
-  const uint64_t* tmask;   // [Nt] key validity per tile, or null
-  const int64_t* ustart;   // [BH * Nt/2] pair-union list starts
-  const int32_t* ulen;     // [BH * Nt/2]
+  const uint16_t* q;       // [BH, Sq, D] tile order
+  const uint16_t* k;       // [BH, Sk, D] tile order
+  const uint16_t* v;       // [BH, Sk, D] tile order
+  const uint64_t* tmask;   // [Sk/64] key validity per tile, or null
+  const int64_t* ustart;   // [BH * Sq/128] pair-union list starts
+  const int32_t* ulen;     // [BH * Sq/128]
   const int32_t* ucols;    // entries tile << 3 | partial << 2 | in_b << 1 | in_a
-  int64_t S, Nt;
-  int npairs;
+  int64_t Sq, Sk;
+  int npairs;              // query-tile pairs per head
   float scale_log2;        // sm_scale * log2(e)
-  uint16_t* o;             // [BH, S, D]
-  float* lse;              // [BH, S] natural log
+  uint16_t* o;             // [BH, Sq, D]
+  float* lse;              // [BH, Sq] natural log
 };
 
 constexpr int kStages = 2;  // two workgroups per CU: 2 x 2 stages of K and V fill the LDS
@@ -82,9 +82,9 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   const int n = a.ulen[logical];
   const int mybit = 1 << (w >> 1);
 
-  const uint16_t* Qh = a.q + (int64_t)bh * a.S * D;
-  const uint16_t* Kh = a.k + (int64_t)bh * a.S * D;
-  const uint16_t* Vh = a.v + (int64_t)bh * a.S * D;
+  const uint16_t* Qh = a.q + (int64_t)bh * a.Sq * D;
+  const uint16_t* Kh = a.k + (int64_t)bh * a.Sk * D;
+  const uint16_t* Vh = a.v + (int64_t)bh * a.Sk * D;
   const float NINF = -__builtin_inff();
 
   // DMA plan: wave w issues KB-instructions w, w + 4, ... of each stage (K then V)
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   }
 
   const float inv = 1.0f / l;
-  uint16_t* Oq = a.o + ((int64_t)bh * a.S + qrow) * D;
+  uint16_t* Oq = a.o + ((int64_t)bh * a.Sq + qrow) * D;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -224,25 +224,27 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
       u.y = pack_bf16(acc_o[dt][4 * j + 2] * inv, acc_o[dt][4 * j + 3] * inv);
       *reinterpret_cast<uint2*>(Oq + 32 * dt + 8 * j + 4 * g) = u;
     }
-  if (g == 0) a.lse[(int64_t)bh * a.S + qrow] = (m + __log2f(l)) * 0.6931471805599453f;
+  if (g == 0) a.lse[(int64_t)bh * a.Sq + qrow] = (m + __log2f(l)) * 0.6931471805599453f;
 }
 
 }  // namespace
 
 extern "C" {
 
-int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S, int D, const uint64_t* tile_masks,
+int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
+                  const uint64_t* tile_masks,
                   const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* o, float* lse,
                   hipStream_t stream) {
   PRISM_REQUIRE(q && k && v && ustart && ulen && ucols && o && lse, "prism_bsa_fwd: null pointer");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_bsa_fwd: head_dim %d unsupported (64, 128)", D);
-  PRISM_REQUIRE(S > 0 && S % 128 == 0, "prism_bsa_fwd: S must be a positive multiple of 128");
+  PRISM_REQUIRE(Sq > 0 && Sq % 128 == 0 && Sk > 0 && Sk % 128 == 0,
+                "prism_bsa_fwd: Sq and Sk must be positive multiples of 128");
   PRISM_REQUIRE(BH >= 1, "prism_bsa_fwd: BH must be >= 1");
-  PRISM_REQUIRE((int64_t)BH * (S / 128) < (1ll << 31), "prism_bsa_fwd: grid too large");
+  PRISM_REQUIRE((int64_t)BH * (Sq / 128) < (1ll << 31), "prism_bsa_fwd: grid too large");
   FwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.tmask = tile_masks;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.S = S; a.Nt = S / 64;
-  a.npairs = (int)(S / 128);
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.Sq = Sq; a.Sk = Sk;
+  a.npairs = (int)(Sq / 128);
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.o = (uint16_t*)o; a.lse = lse;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);

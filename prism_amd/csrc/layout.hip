@@ -8,10 +8,16 @@
 //   rearrange_kernel     _build_rearrange_index (dynamic_block_attention.py:107-135)
 //   gather_pool_kernel   q/k/v.index_select(2, src_idx) (:250-253) fused with
 //                        masked_mean_pooling_compression (bsa_interface.py:177-201)
-//                        and _logical_block_means (dynamic_block_attention.py:173-188),
-//                        plus the transposed-tile copy the MFMA kernels read and,
-//                        for the backward, delta = rowsum(o * do) (common.py:110-127)
-//   scatter_rows_kernel  o_re.index_select(2, inv_idx) (dynamic_block_attention.py:329)
+//                        and _logical_block_means (dynamic_block_attention.py:173-188)
+//                        and, for the backward, delta = rowsum(o * do)
+//                        (common.py:110-127); with the uniform chunk layout it
+//                        is rearrange_THW_to_3d_block (bsa_interface.py:1105-1109)
+//                        fused with the 3-D / 1-D padding of flash_attn_bsa_cross
+//                        (:1263-1273, :1318-1367) and (masked_)mean_pooling_compression
+//                        (:164-201)
+//   scatter_rows_kernel  o_re.index_select(2, inv_idx) (dynamic_block_attention.py:329),
+//                        rearrange_3d_block_to_THW + unpadding (bsa_interface.py:1111-1115,
+//                        :1372-1380)
 //
 // Tile order: zone z holds rearranged positions [512 z, 512 z + 512); 64-token
 // tile t = position / 64.  Block means are fp32 sums over the block's valid
@@ -92,40 +98,94 @@ __device__ __forceinline__ void load_row(const T* p, float* x) {
 }
 
 struct GatherArgs {
-  const void* x;             // [B,H,S,D] THW order, dtype T
-  const uint8_t* valid;      // [S] THW or null
-  const int64_t* shape_ids;  // [Nz]
-  const int32_t* block_offset;
-  int64_t S;
-  int64_t N_b;
-  int ZH, ZW, Hg, Wg;
-  uint16_t* out_rows;        // [B,H,S,D] bf16 tile order, or null
+  const void* x;             // [B,H,S_in,D] THW order, dtype T
+  const uint8_t* valid;      // [S_in] THW or null
+  int64_t S_in;              // tokens per head in x
+  int64_t S_out;             // rows per head of the tile-order outputs
+  int64_t N_b;               // blocks per head
+  uint16_t* out_rows;        // [B,H,S_out,D] bf16 tile order, or null
   float* block_mean;         // [B,H,N_b,D] fp32, or null
   int32_t* block_count;      // [N_b] or null
-  int32_t* tile_count;       // [Nt] or null
-  uint8_t* valid_re;         // [S] tile order, or null
-  const uint16_t* dot_with;  // [B,H,S,D] bf16 tile order, or null
-  float* rowdot;             // [B,H,S] fp32, or null
+  int32_t* tile_count;       // [S_out/64] or null
+  uint8_t* valid_re;         // [S_out] tile order, or null
+  const uint16_t* dot_with;  // [B,H,S_out,D] bf16 tile order, or null
+  float* rowdot;             // [B,H,S_out] fp32, or null
+};
+
+// Rearranged row r (0..511) of work unit u -> source token, for the two
+// layouts.  token() is -1 for a padding row (no source token); a block is
+// bsz consecutive rows starting at a multiple of bsz.
+//
+// ZoneMap: the dynamic layout.  Unit = zone z (512 rows); its blocks have the
+// zone's candidate shape (local_of_rearr) and are numbered from block_offset[z].
+struct ZoneMap {
+  const int64_t* shape_ids;
+  const int32_t* block_offset;
+  int ZH, ZW, Hg, Wg;
+  int z, c, bsz, boff;
+  __device__ __forceinline__ void init(int unit) {
+    z = unit;
+    c = (int)shape_ids[z];
+    bsz = kCand[c][0] * kCand[c][1] * kCand[c][2];
+    boff = block_offset ? block_offset[z] : 0;  // (the scatter needs no block numbers)
+  }
+  __device__ __forceinline__ int64_t row(int r) const { return (int64_t)z * 512 + r; }
+  __device__ __forceinline__ bool live(int) const { return true; }
+  __device__ __forceinline__ int64_t token(int r) const { return token_of(z, local_of_rearr(c, r), ZH, ZW, Hg, Wg); }
+  __device__ __forceinline__ int64_t block(int r) const { return boff + r / bsz; }
+};
+
+// ChunkMap: the uniform 3-D chunk layout (rearrange_THW_to_3d_block,
+// bsa_interface.py:1105-1109): the padded grid Tp x Hp x Wp is cut into
+// ct x ch x cw chunks, chunk n = (nt Nh + nh) Nw + nw owns rows
+// [n csz, n csz + csz) with offset (it ch + ih) cw + iw.  Tokens outside the
+// input grid T x Hg x Wg (the padding of _pad_1d_for_bsa / the 3-D pads of
+// flash_attn_bsa_cross, bsa_interface.py:1263-1273, 1318-1331) and rows past
+// Tp Hp Wp (tile-pair alignment) are padding.  Unit = 512 consecutive rows.
+struct ChunkMap {
+  int T, Hg, Wg;    // input grid
+  int ct, ch, cw;   // chunk shape
+  int Nh, Nw;       // chunks along padded h, w
+  int64_t Sp;       // Tp Hp Wp
+  int64_t S_out;    // rows per head (>= Sp)
+  int bsz;          // ct ch cw
+  int64_t base;
+  __device__ __forceinline__ void init(int unit) { base = (int64_t)unit * 512; }
+  __device__ __forceinline__ int64_t row(int r) const { return base + r; }
+  __device__ __forceinline__ bool live(int r) const { return base + r < S_out; }
+  __device__ __forceinline__ int64_t token(int r) const {
+    const int64_t p = base + r;
+    if (p >= Sp) return -1;
+    const int64_t n = p / bsz;
+    const int off = (int)(p - n * bsz);
+    const int64_t nt = n / ((int64_t)Nh * Nw);
+    const int nh = (int)((n / Nw) % Nh), nw = (int)(n % Nw);
+    const int it = off / (ch * cw), ih = (off / cw) % ch, iw = off % cw;
+    const int64_t t = nt * ct + it;
+    const int h = nh * ch + ih, w = nw * cw + iw;
+    if (t >= T || h >= Hg || w >= Wg) return -1;
+    return (t * Hg + h) * Wg + w;
+  }
+  __device__ __forceinline__ int64_t block(int r) const { return (base + r) / bsz; }
 };
 
 constexpr int kGatherThreads = 256;  // 4 waves, 128 rearranged rows each
 constexpr int kGatherBatch = 8;      // rows loaded per step (loads in flight)
 
-// grid (Nz, B*H).  Wave w covers rearranged rows [128 w, 128 w + 128) of zone z
-// (two 64-token blocks or one 128-token block; two tiles); lane l owns
-// channels [l*CPL, l*CPL + CPL).
-template <int D, typename T>
-__global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs a) {
+// grid (units, B*H).  Wave w covers rearranged rows [128 w, 128 w + 128) of
+// unit u (blocks of 64 or 128 rows: one or two whole blocks, two tiles); lane
+// l owns channels [l*CPL, l*CPL + CPL).  Padding rows are written as zeros,
+// are invalid, and belong to no block when they lie past the last block.
+template <int D, typename T, typename Map>
+__global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs a, Map m) {
   constexpr int CPL = D / 64;
-  const int z = blockIdx.x;
   const int bh = blockIdx.y;
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c = (int)a.shape_ids[z];
-  const int bsz = kCand[c][0] * kCand[c][1] * kCand[c][2];
-  const int boff = a.block_offset[z];
+  m.init(blockIdx.x);
+  if (!m.live(wid * 128)) return;  // rows per head are a multiple of 128
   const bool first_bh = bh == 0;
-  const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)bh * a.S * D;
-  const int64_t rowbase = (int64_t)bh * a.S + (int64_t)z * 512;
+  const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)bh * a.S_in * D;
+  const int64_t rowbase = (int64_t)bh * a.S_out;
 
   float acc[CPL];
   int cnt = 0, tcnt = 0;
@@ -138,66 +198,76 @@ __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs 
 #pragma unroll
     for (int u = 0; u < kGatherBatch; ++u) {
       const int r = wid * 128 + o0 + u;
-      const int64_t tok = token_of(z, local_of_rearr(c, r), a.ZH, a.ZW, a.Hg, a.Wg);
-      ok[u] = a.valid ? (a.valid[tok] != 0) : true;
-      load_row<T, CPL>(x + tok * D + lane * CPL, xv[u]);
+      const int64_t tok = m.token(r);
+      ok[u] = tok >= 0 && (a.valid ? (a.valid[tok] != 0) : true);
+      if (tok >= 0) {
+        load_row<T, CPL>(x + tok * D + lane * CPL, xv[u]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) xv[u][j] = 0.0f;
+      }
     }
 #pragma unroll
     for (int u = 0; u < kGatherBatch; ++u) {
       const int r = wid * 128 + o0 + u;
+      const int64_t grow = m.row(r);
       if (a.out_rows) {
-        uint16_t* dst = a.out_rows + (rowbase + r) * D + lane * CPL;
+        uint16_t* dst = a.out_rows + (rowbase + grow) * D + lane * CPL;
         if (CPL == 2) *reinterpret_cast<uint32_t*>(dst) = (uint32_t)f2bf(xv[u][0]) | ((uint32_t)f2bf(xv[u][CPL - 1]) << 16);
         else dst[0] = f2bf(xv[u][0]);
       }
       if (a.rowdot) {
-        const uint16_t* y = a.dot_with + (rowbase + r) * D + lane * CPL;
+        const uint16_t* y = a.dot_with + (rowbase + grow) * D + lane * CPL;
         float part = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) part = __builtin_fmaf(xv[u][j], bf2f(y[j]), part);
         part = wave_sum_xor(part);
-        if (lane == 0) a.rowdot[rowbase + r] = part;
+        if (lane == 0) a.rowdot[rowbase + grow] = part;
       }
 #pragma unroll
       for (int j = 0; j < CPL; ++j) acc[j] = ok[u] ? acc[j] + xv[u][j] : acc[j];
       cnt += ok[u] ? 1 : 0;
       tcnt += ok[u] ? 1 : 0;
-      if (first_bh && lane == 0 && a.valid_re) a.valid_re[(int64_t)z * 512 + r] = ok[u] ? 1 : 0;
-      if ((r + 1) % bsz == 0) {  // block complete
-        const int blk = r / bsz;
-        if (a.block_mean) {
-          const float den = (float)(cnt > 0 ? cnt : 1);
-          float* dst = a.block_mean + ((int64_t)bh * a.N_b + boff + blk) * D + lane * CPL;
+      if (first_bh && lane == 0 && a.valid_re) a.valid_re[grow] = ok[u] ? 1 : 0;
+      if ((r + 1) % m.bsz == 0) {  // block complete
+        const int64_t blk = m.block(r);
+        if (blk < a.N_b) {
+          if (a.block_mean) {
+            const float den = (float)(cnt > 0 ? cnt : 1);
+            float* dst = a.block_mean + ((int64_t)bh * a.N_b + blk) * D + lane * CPL;
 #pragma unroll
-          for (int j = 0; j < CPL; ++j) dst[j] = acc[j] / den;
+            for (int j = 0; j < CPL; ++j) dst[j] = acc[j] / den;
+          }
+          if (first_bh && lane == 0 && a.block_count) a.block_count[blk] = cnt;
         }
-        if (first_bh && lane == 0 && a.block_count) a.block_count[boff + blk] = cnt;
         cnt = 0;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
       }
       if ((r & 63) == 63) {  // tile complete
-        if (first_bh && lane == 0 && a.tile_count) a.tile_count[z * 8 + (r >> 6)] = tcnt;
+        if (first_bh && lane == 0 && a.tile_count) a.tile_count[grow >> 6] = tcnt;
         tcnt = 0;
       }
     }
   }
 }
 
-// grid (Nz, B*H): tile-order bf16 rows -> THW rows of dtype TO.
-template <int D, typename TO>
-__global__ __launch_bounds__(kGatherThreads) void scatter_rows_kernel(
-    const uint16_t* __restrict__ in, const int64_t* __restrict__ shape_ids, int64_t S, int ZH, int ZW, int Hg,
-    int Wg, TO* __restrict__ out) {
+// grid (units, B*H): tile-order bf16 rows (S_out per head) -> THW rows of
+// dtype TO (S_in per head); padding rows are dropped.
+template <int D, typename TO, typename Map>
+__global__ __launch_bounds__(kGatherThreads) void scatter_rows_kernel(const uint16_t* __restrict__ in, int64_t S_in,
+                                                                      int64_t S_out, Map m, TO* __restrict__ out) {
   constexpr int CPL = D / 64;
-  const int z = blockIdx.x, bh = blockIdx.y;
+  const int bh = blockIdx.y;
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c = (int)shape_ids[z];
+  m.init(blockIdx.x);
+  if (!m.live(wid * 128)) return;
   for (int o = 0; o < 128; ++o) {
     const int r = wid * 128 + o;
-    const int64_t tok = token_of(z, local_of_rearr(c, r), ZH, ZW, Hg, Wg);
-    const uint16_t* src = in + ((int64_t)bh * S + (int64_t)z * 512 + r) * D + lane * CPL;
-    TO* dst = out + ((int64_t)bh * S + tok) * D + lane * CPL;
+    const int64_t tok = m.token(r);
+    if (tok < 0) continue;
+    const uint16_t* src = in + ((int64_t)bh * S_out + m.row(r)) * D + lane * CPL;
+    TO* dst = out + ((int64_t)bh * S_in + tok) * D + lane * CPL;
     if (sizeof(TO) == 2) {
       if (CPL == 2) *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
       else *reinterpret_cast<uint16_t*>(dst) = src[0];
@@ -206,6 +276,54 @@ __global__ __launch_bounds__(kGatherThreads) void scatter_rows_kernel(
       for (int j = 0; j < CPL; ++j) reinterpret_cast<float*>(dst)[j] = bf2f(src[j]);
     }
   }
+}
+
+template <typename Map>
+void launch_gather(const GatherArgs& a, const Map& m, int dtype, int D, dim3 grid, hipStream_t stream) {
+  if (dtype == PRISM_BF16) {
+    if (D == 128) gather_pool_kernel<128, uint16_t, Map><<<grid, kGatherThreads, 0, stream>>>(a, m);
+    else gather_pool_kernel<64, uint16_t, Map><<<grid, kGatherThreads, 0, stream>>>(a, m);
+  } else {
+    if (D == 128) gather_pool_kernel<128, float, Map><<<grid, kGatherThreads, 0, stream>>>(a, m);
+    else gather_pool_kernel<64, float, Map><<<grid, kGatherThreads, 0, stream>>>(a, m);
+  }
+}
+
+template <typename Map>
+void launch_scatter(const void* in_rows, int64_t S_in, int64_t S_out, const Map& m, void* out, int out_dtype, int D,
+                    dim3 grid, hipStream_t stream) {
+  const uint16_t* in = (const uint16_t*)in_rows;
+  if (out_dtype == PRISM_BF16) {
+    if (D == 128) scatter_rows_kernel<128, uint16_t, Map><<<grid, kGatherThreads, 0, stream>>>(in, S_in, S_out, m, (uint16_t*)out);
+    else scatter_rows_kernel<64, uint16_t, Map><<<grid, kGatherThreads, 0, stream>>>(in, S_in, S_out, m, (uint16_t*)out);
+  } else {
+    if (D == 128) scatter_rows_kernel<128, float, Map><<<grid, kGatherThreads, 0, stream>>>(in, S_in, S_out, m, (float*)out);
+    else scatter_rows_kernel<64, float, Map><<<grid, kGatherThreads, 0, stream>>>(in, S_in, S_out, m, (float*)out);
+  }
+}
+
+ZoneMap zone_map(const int64_t* shape_ids, const int32_t* block_offset, int Hg, int Wg) {
+  ZoneMap m = {};
+  m.shape_ids = shape_ids; m.block_offset = block_offset; m.ZH = Hg / 8; m.ZW = Wg / 8; m.Hg = Hg; m.Wg = Wg;
+  return m;
+}
+
+// validates a chunk geometry; returns PRISM_OK or sets the error
+int chunk_map(int T, int Hg, int Wg, int Tp, int Hp, int Wp, int ct, int ch, int cw, int64_t S_out, const char* who,
+              ChunkMap* m) {
+  PRISM_REQUIRE(T > 0 && Hg > 0 && Wg > 0 && ct > 0 && ch > 0 && cw > 0, "%s: empty grid or chunk", who);
+  PRISM_REQUIRE(Tp >= T && Hp >= Hg && Wp >= Wg && Tp % ct == 0 && Hp % ch == 0 && Wp % cw == 0,
+                "%s: padded grid (%d,%d,%d) must cover the grid and be multiples of the chunk (%d,%d,%d)", who, Tp, Hp,
+                Wp, ct, ch, cw);
+  const int bsz = ct * ch * cw;
+  PRISM_REQUIRE(bsz == 64 || bsz == 128, "%s: chunk of %d tokens unsupported (64 or 128)", who, bsz);
+  const int64_t Sp = (int64_t)Tp * Hp * Wp;
+  PRISM_REQUIRE(S_out >= Sp && S_out % 128 == 0, "%s: rows per head must be a multiple of 128 and >= T*H*W padded",
+                who);
+  *m = ChunkMap{};
+  m->T = T; m->Hg = Hg; m->Wg = Wg; m->ct = ct; m->ch = ch; m->cw = cw; m->Nh = Hp / ch; m->Nw = Wp / cw;
+  m->Sp = Sp; m->S_out = S_out; m->bsz = bsz;
+  return PRISM_OK;
 }
 
 bool grid_ok(int T, int Hg, int Wg) { return T > 0 && Hg > 0 && Wg > 0 && T % 8 == 0 && Hg % 8 == 0 && Wg % 8 == 0; }
@@ -246,22 +364,14 @@ int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, 
   PRISM_REQUIRE(B >= 1 && H >= 1, "prism_gather_pool: B, H must be >= 1");
   PRISM_REQUIRE(dtype == PRISM_F32 || dtype == PRISM_BF16, "prism_gather_pool: bad dtype");
   PRISM_REQUIRE((dot_with == nullptr) == (rowdot == nullptr), "prism_gather_pool: dot_with and rowdot go together");
-  PRISM_REQUIRE(block_mean == nullptr || N_b > 0, "prism_gather_pool: N_b required for pooling");
-  GatherArgs a;
-  a.x = x; a.valid = valid; a.shape_ids = shape_ids; a.block_offset = block_offset; a.S = S; a.N_b = N_b;
-  a.ZH = Hg / 8; a.ZW = Wg / 8; a.Hg = Hg; a.Wg = Wg;
+  PRISM_REQUIRE((block_mean == nullptr && block_count == nullptr) || N_b > 0,
+                "prism_gather_pool: N_b required for pooling and block counts");
+  GatherArgs a = {};
+  a.x = x; a.valid = valid; a.S_in = S; a.S_out = S; a.N_b = N_b;
   a.out_rows = (uint16_t*)out_rows; a.block_mean = block_mean;
   a.block_count = block_count; a.tile_count = tile_count; a.valid_re = valid_re;
   a.dot_with = (const uint16_t*)dot_with; a.rowdot = rowdot;
-  const int Nz = (int)(S / 512);
-  dim3 grid(Nz, B * H);
-  if (dtype == PRISM_BF16) {
-    if (D == 128) gather_pool_kernel<128, uint16_t><<<grid, kGatherThreads, 0, stream>>>(a);
-    else gather_pool_kernel<64, uint16_t><<<grid, kGatherThreads, 0, stream>>>(a);
-  } else {
-    if (D == 128) gather_pool_kernel<128, float><<<grid, kGatherThreads, 0, stream>>>(a);
-    else gather_pool_kernel<64, float><<<grid, kGatherThreads, 0, stream>>>(a);
-  }
+  launch_gather(a, zone_map(shape_ids, block_offset, Hg, Wg), dtype, D, dim3((unsigned)(S / 512), B * H), stream);
   PRISM_LAUNCH_CHECK("prism_gather_pool");
   return PRISM_OK;
 }
@@ -273,16 +383,45 @@ int prism_scatter_rows(const void* in_rows, int B, int H, int64_t S, int D, cons
   PRISM_REQUIRE((int64_t)T * Hg * Wg == S, "prism_scatter_rows: T*H*W != S");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_scatter_rows: head_dim %d unsupported", D);
   PRISM_REQUIRE(out_dtype == PRISM_F32 || out_dtype == PRISM_BF16, "prism_scatter_rows: bad dtype");
-  dim3 grid((unsigned)(S / 512), B * H);
-  const uint16_t* in = (const uint16_t*)in_rows;
-  if (out_dtype == PRISM_BF16) {
-    if (D == 128) scatter_rows_kernel<128, uint16_t><<<grid, kGatherThreads, 0, stream>>>(in, shape_ids, S, Hg / 8, Wg / 8, Hg, Wg, (uint16_t*)out);
-    else scatter_rows_kernel<64, uint16_t><<<grid, kGatherThreads, 0, stream>>>(in, shape_ids, S, Hg / 8, Wg / 8, Hg, Wg, (uint16_t*)out);
-  } else {
-    if (D == 128) scatter_rows_kernel<128, float><<<grid, kGatherThreads, 0, stream>>>(in, shape_ids, S, Hg / 8, Wg / 8, Hg, Wg, (float*)out);
-    else scatter_rows_kernel<64, float><<<grid, kGatherThreads, 0, stream>>>(in, shape_ids, S, Hg / 8, Wg / 8, Hg, Wg, (float*)out);
-  }
+  launch_scatter(in_rows, S, S, zone_map(shape_ids, nullptr, Hg, Wg), out, out_dtype, D,
+                 dim3((unsigned)(S / 512), B * H), stream);
   PRISM_LAUNCH_CHECK("prism_scatter_rows");
+  return PRISM_OK;
+}
+
+int prism_chunk_gather_pool(const void* x, int dtype, int B, int H, int D, const uint8_t* valid, int T, int Hg, int Wg,
+                            int Tp, int Hp, int Wp, int ct, int ch, int cw, int64_t S_out, void* out_rows,
+                            float* block_mean, int32_t* block_count, int32_t* tile_count, uint8_t* valid_re,
+                            const void* dot_with, float* rowdot, hipStream_t stream) {
+  PRISM_REQUIRE(x, "prism_chunk_gather_pool: null pointer");
+  PRISM_REQUIRE(D == 64 || D == 128, "prism_chunk_gather_pool: head_dim %d unsupported (64, 128)", D);
+  PRISM_REQUIRE(B >= 1 && H >= 1, "prism_chunk_gather_pool: B, H must be >= 1");
+  PRISM_REQUIRE(dtype == PRISM_F32 || dtype == PRISM_BF16, "prism_chunk_gather_pool: bad dtype");
+  PRISM_REQUIRE((dot_with == nullptr) == (rowdot == nullptr), "prism_chunk_gather_pool: dot_with and rowdot go together");
+  ChunkMap m;
+  int rc = chunk_map(T, Hg, Wg, Tp, Hp, Wp, ct, ch, cw, S_out, "prism_chunk_gather_pool", &m);
+  if (rc) return rc;
+  GatherArgs a = {};
+  a.x = x; a.valid = valid; a.S_in = (int64_t)T * Hg * Wg; a.S_out = S_out; a.N_b = m.Sp / m.bsz;
+  a.out_rows = (uint16_t*)out_rows; a.block_mean = block_mean;
+  a.block_count = block_count; a.tile_count = tile_count; a.valid_re = valid_re;
+  a.dot_with = (const uint16_t*)dot_with; a.rowdot = rowdot;
+  launch_gather(a, m, dtype, D, dim3((unsigned)((S_out + 511) / 512), B * H), stream);
+  PRISM_LAUNCH_CHECK("prism_chunk_gather_pool");
+  return PRISM_OK;
+}
+
+int prism_chunk_scatter_rows(const void* in_rows, int B, int H, int D, int T, int Hg, int Wg, int Tp, int Hp, int Wp,
+                             int ct, int ch, int cw, int64_t S_out, void* out, int out_dtype, hipStream_t stream) {
+  PRISM_REQUIRE(in_rows && out, "prism_chunk_scatter_rows: null pointer");
+  PRISM_REQUIRE(D == 64 || D == 128, "prism_chunk_scatter_rows: head_dim %d unsupported", D);
+  PRISM_REQUIRE(out_dtype == PRISM_F32 || out_dtype == PRISM_BF16, "prism_chunk_scatter_rows: bad dtype");
+  ChunkMap m;
+  int rc = chunk_map(T, Hg, Wg, Tp, Hp, Wp, ct, ch, cw, S_out, "prism_chunk_scatter_rows", &m);
+  if (rc) return rc;
+  launch_scatter(in_rows, (int64_t)T * Hg * Wg, S_out, m, out, out_dtype, D,
+                 dim3((unsigned)((S_out + 511) / 512), B * H), stream);
+  PRISM_LAUNCH_CHECK("prism_chunk_scatter_rows");
   return PRISM_OK;
 }
 

@@ -23,7 +23,7 @@ constexpr int kUnionWin = 8192;  // tiles per LDS bitmap window (256 words)
 // one 256-thread workgroup per row pair
 __global__ __launch_bounds__(256) void pair_union_kernel(const int64_t* __restrict__ start,
                                                          const int32_t* __restrict__ len,
-                                                         const int32_t* __restrict__ cols, int64_t Nt,
+                                                         const int32_t* __restrict__ cols, int64_t Nc,
                                                          const uint64_t* __restrict__ tile_masks, int64_t ucap,
                                                          int64_t* __restrict__ ustart, int32_t* __restrict__ ulen,
                                                          int32_t* __restrict__ ucols) {
@@ -35,20 +35,20 @@ __global__ __launch_bounds__(256) void pair_union_kernel(const int64_t* __restri
   const int32_t* A = cols + start[rA];
   const int32_t* B = cols + start[rB];
   const int nA = len[rA], nB = len[rB];
-  // list entries index tiles inside one head (0 .. Nt-1), as does tile_masks
+  // list entries index column tiles inside one head (0 .. Nc-1), as does tile_masks
   int32_t* out = ucols + p * ucap;
   int count = 0;
-  for (int64_t w0 = 0; w0 < Nt; w0 += kUnionWin) {
+  for (int64_t w0 = 0; w0 < Nc; w0 += kUnionWin) {
     bmA[tid] = 0u;
     bmB[tid] = 0u;
     __syncthreads();
     for (int i = tid; i < nA; i += 256) {
       const int64_t t = (int64_t)A[i] - w0;
-      if (t >= 0 && t < kUnionWin && A[i] < Nt) atomicOr(&bmA[t >> 5], 1u << (t & 31));
+      if (t >= 0 && t < kUnionWin && A[i] < Nc) atomicOr(&bmA[t >> 5], 1u << (t & 31));
     }
     for (int i = tid; i < nB; i += 256) {
       const int64_t t = (int64_t)B[i] - w0;
-      if (t >= 0 && t < kUnionWin && B[i] < Nt) atomicOr(&bmB[t >> 5], 1u << (t & 31));
+      if (t >= 0 && t < kUnionWin && B[i] < Nc) atomicOr(&bmB[t >> 5], 1u << (t & 31));
     }
     __syncthreads();
     const uint32_t a = bmA[tid], b = bmB[tid];
@@ -103,18 +103,19 @@ __global__ __launch_bounds__(256) void lse_to_m2_kernel(const float* __restrict_
 
 extern "C" {
 
-int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t Nt,
-                     const uint64_t* tile_masks, int64_t ucap, int64_t* ustart, int32_t* ulen, int32_t* ucols,
-                     hipStream_t stream) {
+int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
+                     int64_t col_tiles, const uint64_t* tile_masks, int64_t ucap, int64_t* ustart, int32_t* ulen,
+                     int32_t* ucols, hipStream_t stream) {
   PRISM_REQUIRE(start && len && cols && ustart && ulen && ucols, "prism_pair_union: null pointer");
   PRISM_REQUIRE(rows >= 0 && rows % 2 == 0, "prism_pair_union: rows must be even (pairs of tiles)");
-  PRISM_REQUIRE(Nt > 0 && Nt % 2 == 0 && rows % Nt == 0, "prism_pair_union: rows must be a multiple of an even N_tiles");
-  PRISM_REQUIRE(Nt < (1ll << 28), "prism_pair_union: N_tiles too large for the entry encoding");
-  PRISM_REQUIRE(ucap >= Nt, "prism_pair_union: ucap must be >= N_tiles");
+  PRISM_REQUIRE(row_tiles > 0 && row_tiles % 2 == 0 && rows % row_tiles == 0,
+                "prism_pair_union: rows must be a multiple of an even row_tiles (tiles per head)");
+  PRISM_REQUIRE(col_tiles > 0 && col_tiles < (1ll << 28), "prism_pair_union: col_tiles out of range");
+  PRISM_REQUIRE(ucap >= col_tiles, "prism_pair_union: ucap must be >= col_tiles");
   const int64_t pairs = rows / 2;
   if (pairs == 0) return PRISM_OK;
   PRISM_REQUIRE(pairs < (1ll << 31), "prism_pair_union: too many pairs");
-  pair_union_kernel<<<(unsigned)pairs, 256, 0, stream>>>(start, len, cols, Nt, tile_masks, ucap, ustart, ulen, ucols);
+  pair_union_kernel<<<(unsigned)pairs, 256, 0, stream>>>(start, len, cols, col_tiles, tile_masks, ucap, ustart, ulen, ucols);
   PRISM_LAUNCH_CHECK("prism_pair_union");
   return PRISM_OK;
 }

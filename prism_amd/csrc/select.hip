@@ -30,15 +30,15 @@ namespace {
 constexpr int kSTile = 128, kSChunk = 16;
 
 __global__ __launch_bounds__(256) void block_scores_kernel(const float* __restrict__ qc, const float* __restrict__ kc,
-                                                           const int32_t* __restrict__ block_count, int64_t N, int D,
-                                                           float* __restrict__ scores) {
+                                                           const int32_t* __restrict__ block_count, int64_t Nq,
+                                                           int64_t Nk, int D, float* __restrict__ scores) {
   __shared__ float sA[kSChunk][kSTile + 4];
   __shared__ float sB[kSChunk][kSTile + 4];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const int64_t i0 = (int64_t)blockIdx.y * kSTile, j0 = (int64_t)blockIdx.x * kSTile;
   const int bh = blockIdx.z;
-  const float* A = qc + (int64_t)bh * N * D;
-  const float* Bm = kc + (int64_t)bh * N * D;
+  const float* A = qc + (int64_t)bh * Nq * D;
+  const float* Bm = kc + (int64_t)bh * Nk * D;
   float acc[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -52,8 +52,8 @@ __global__ __launch_bounds__(256) void block_scores_kernel(const float* __restri
       const int idx = tid + u * 256;
       const int row = idx >> 2, c4 = (idx & 3) * 4;
       float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
-      if (i0 + row < N) va = *reinterpret_cast<const float4*>(A + (i0 + row) * D + d0 + c4);
-      if (j0 + row < N) vb = *reinterpret_cast<const float4*>(Bm + (j0 + row) * D + d0 + c4);
+      if (i0 + row < Nq) va = *reinterpret_cast<const float4*>(A + (i0 + row) * D + d0 + c4);
+      if (j0 + row < Nk) vb = *reinterpret_cast<const float4*>(Bm + (j0 + row) * D + d0 + c4);
       sA[c4 + 0][row] = va.x; sA[c4 + 1][row] = va.y; sA[c4 + 2][row] = va.z; sA[c4 + 3][row] = va.w;
       sB[c4 + 0][row] = vb.x; sB[c4 + 1][row] = vb.y; sB[c4 + 2][row] = vb.z; sB[c4 + 3][row] = vb.w;
     }
@@ -78,12 +78,12 @@ __global__ __launch_bounds__(256) void block_scores_kernel(const float* __restri
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int64_t row = i0 + ty * 8 + i;
-    if (row >= N) continue;
-    float* out = scores + ((int64_t)bh * N + row) * N;
+    if (row >= Nq) continue;
+    float* out = scores + ((int64_t)bh * Nq + row) * Nk;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int64_t col = j0 + tx * 8 + j;
-      if (col < N) out[col] = (block_count && block_count[col] == 0) ? ninf : acc[i][j];
+      if (col < Nk) out[col] = (block_count && block_count[col] == 0) ? ninf : acc[i][j];
     }
   }
 }
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     out_carry += tot;
     if (sel) {
       uint32_t p = pos & 0xffffu;
-      for (int32_t t = t0; t < t1; ++t)
+      for (int32_t t = t0; t < t1 && p < a.tcap; ++t)
         if (a.tile_count == nullptr || a.tile_count[t] > 0) trow[p++] = t;
       if (brow) brow[pos >> 16] = (int32_t)j;
     }
@@ -342,20 +342,20 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v)
 
 // one 64-lane group per q row: set bit q in the bitmap row of every listed k tile
 __global__ __launch_bounds__(64) void set_bits_kernel(const int64_t* __restrict__ qstart, const int32_t* __restrict__ qlen,
-                                                      const int32_t* __restrict__ qcols, int64_t Nt, int64_t words,
-                                                      uint32_t* __restrict__ bm) {
+                                                      const int32_t* __restrict__ qcols, int64_t Ntq, int64_t Ntk,
+                                                      int64_t words, uint32_t* __restrict__ bm) {
   const int64_t row = blockIdx.x;
-  const int64_t bh = row / Nt, t = row - bh * Nt;
+  const int64_t bh = row / Ntq, t = row - bh * Ntq;
   const int n = qlen[row];
   const int32_t* cols = qcols + qstart[row];
   for (int i = threadIdx.x; i < n; i += 64) {
     const int64_t k = cols[i];
-    atomicOr(&bm[(bh * Nt + k) * words + (t >> 5)], 1u << (t & 31));
+    if (k >= 0 && k < Ntk) atomicOr(&bm[(bh * Ntk + k) * words + (t >> 5)], 1u << (t & 31));
   }
 }
 
 // one wave per k row: emit the set bits (ascending q tiles)
-__global__ __launch_bounds__(256) void emit_bits_kernel(const uint32_t* __restrict__ bm, int64_t rows, int64_t Nt,
+__global__ __launch_bounds__(256) void emit_bits_kernel(const uint32_t* __restrict__ bm, int64_t rows,
                                                         int64_t words, int64_t kcap, int64_t* __restrict__ kstart,
                                                         int32_t* __restrict__ klen, int32_t* __restrict__ kcols) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -387,13 +387,13 @@ __global__ __launch_bounds__(256) void emit_bits_kernel(const uint32_t* __restri
 
 extern "C" {
 
-int prism_block_scores(const float* qc, const float* kc, const int32_t* block_count, int BH, int64_t N, int D,
-                       float* scores, hipStream_t stream) {
+int prism_block_scores(const float* qc, const float* kc, const int32_t* block_count, int BH, int64_t Nq, int64_t Nk,
+                       int D, float* scores, hipStream_t stream) {
   PRISM_REQUIRE(qc && kc && scores, "prism_block_scores: null pointer");
   PRISM_REQUIRE(D > 0 && D % kSChunk == 0, "prism_block_scores: D=%d must be a multiple of %d", D, kSChunk);
-  PRISM_REQUIRE(BH >= 1 && N >= 1, "prism_block_scores: empty problem");
-  dim3 grid((unsigned)((N + kSTile - 1) / kSTile), (unsigned)((N + kSTile - 1) / kSTile), BH);
-  block_scores_kernel<<<grid, 256, 0, stream>>>(qc, kc, block_count, N, D, scores);
+  PRISM_REQUIRE(BH >= 1 && Nq >= 1 && Nk >= 1, "prism_block_scores: empty problem");
+  dim3 grid((unsigned)((Nk + kSTile - 1) / kSTile), (unsigned)((Nq + kSTile - 1) / kSTile), BH);
+  block_scores_kernel<<<grid, 256, 0, stream>>>(qc, kc, block_count, Nq, Nk, D, scores);
   PRISM_LAUNCH_CHECK("prism_block_scores");
   return PRISM_OK;
 }
@@ -408,7 +408,7 @@ int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, i
                 (long long)N, 64 * kSelThreads);
   PRISM_REQUIRE(k_lo >= 0 && ub >= 0 && ub <= N, "prism_select_tiles: bad k/ub");
   PRISM_REQUIRE(mode == 0 || thr > 0, "prism_select_tiles: threshold must be positive");
-  PRISM_REQUIRE(tcap >= 2 * (mode == 0 ? (k_lo < N ? k_lo : N) : ub), "prism_select_tiles: tcap too small");
+  PRISM_REQUIRE(tcap >= (mode == 0 ? (k_lo < N ? k_lo : N) : ub), "prism_select_tiles: tcap too small");
   PRISM_REQUIRE(sel_blocks == nullptr || bcap >= (mode == 0 ? (k_lo < N ? k_lo : N) : ub),
                 "prism_select_tiles: bcap too small");
   PRISM_REQUIRE(2 * N < 65536, "prism_select_tiles: N too large for the packed scan");
@@ -437,16 +437,17 @@ int prism_tile_rows(const int32_t* ntiles, const int32_t* block_id_of_tile, cons
   return PRISM_OK;
 }
 
-int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH, int64_t Nt,
-                          uint32_t* bitmap, int64_t kcap, int64_t* kstart, int32_t* klen, int32_t* kcols,
+int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH, int64_t Ntq,
+                          int64_t Ntk, uint32_t* bitmap, int64_t kcap, int64_t* kstart, int32_t* klen, int32_t* kcols,
                           hipStream_t stream) {
   PRISM_REQUIRE(qstart && qlen && qcols && bitmap && kstart && klen && kcols, "prism_transpose_lists: null pointer");
-  PRISM_REQUIRE(kcap >= Nt, "prism_transpose_lists: kcap must be >= N_tiles");
-  const int64_t rows = (int64_t)BH * Nt, words = (Nt + 31) / 32;
-  if (rows == 0) return PRISM_OK;
-  fill_u32_kernel<<<1024, 256, 0, stream>>>(bitmap, rows * words, 0u);
-  set_bits_kernel<<<(unsigned)rows, 64, 0, stream>>>(qstart, qlen, qcols, Nt, words, bitmap);
-  emit_bits_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, stream>>>(bitmap, rows, Nt, words, kcap, kstart, klen, kcols);
+  PRISM_REQUIRE(Ntq >= 1 && Ntk >= 1, "prism_transpose_lists: empty tile range");
+  PRISM_REQUIRE(kcap >= Ntq, "prism_transpose_lists: kcap must be >= Ntq");
+  const int64_t qrows = (int64_t)BH * Ntq, krows = (int64_t)BH * Ntk, words = (Ntq + 31) / 32;
+  if (qrows == 0) return PRISM_OK;
+  fill_u32_kernel<<<1024, 256, 0, stream>>>(bitmap, krows * words, 0u);
+  set_bits_kernel<<<(unsigned)qrows, 64, 0, stream>>>(qstart, qlen, qcols, Ntq, Ntk, words, bitmap);
+  emit_bits_kernel<<<(unsigned)((krows + 3) / 4), 256, 0, stream>>>(bitmap, krows, words, kcap, kstart, klen, kcols);
   PRISM_LAUNCH_CHECK("prism_transpose_lists");
   return PRISM_OK;
 }

@@ -221,16 +221,111 @@ def scatter_rows(rows: torch.Tensor, lay: ZoneLayout, out_dtype: torch.dtype) ->
     return out
 
 
+class ChunkLayout:
+    """Uniform chunk layout of one side (queries or keys) of the fixed-shape
+    BSA (flash_attn_bsa_3d / flash_attn_bsa_cross, bsa_interface.py:1123-1392).
+
+    The input grid (T, H, W) is padded up to multiples of the chunk (ct, ch, cw)
+    and cut into chunks in (nt, nh, nw) order (rearrange_THW_to_3d_block,
+    bsa_interface.py:1105-1109); a 1-D sequence is the grid (1, 1, S) with
+    chunk (1, 1, chunk_size).  Rows per head are rounded up to a multiple of
+    128 (the attention kernels process tile pairs); rows past the padded grid
+    are padding.  Chunks hold 64 or 128 tokens (one or two kernel tiles)."""
+
+    def __init__(self, grid, chunk, device):
+        T, H, W = _grid(grid)
+        ct, ch, cw = (int(c) for c in chunk)
+        if min(T, H, W, ct, ch, cw) <= 0:
+            raise ValueError(f"empty grid {grid} or chunk {chunk}")
+        self.csz = ct * ch * cw
+        if self.csz not in (64, 128):
+            raise ValueError(f"chunk {tuple(chunk)} holds {self.csz} tokens; the MI355X kernels take chunks "
+                             "of 64 or 128 tokens")
+        self.grid = (T, H, W)
+        self.chunk = (ct, ch, cw)
+        self.pgrid = (-(-T // ct) * ct, -(-H // ch) * ch, -(-W // cw) * cw)
+        self.S_in = T * H * W
+        self.Sp = self.pgrid[0] * self.pgrid[1] * self.pgrid[2]
+        self.rows = -(-self.Sp // 128) * 128
+        self.N_b = self.Sp // self.csz
+        self.Nt = self.rows // 64
+        self.padded = self.Sp != self.S_in or self.rows != self.Sp
+        tpb = self.csz // 64
+        self.tiles_per_block = tpb
+        # block b owns tiles [tpb b, tpb b + tpb); tiles past the last block
+        # (row padding) point at the last block and get empty lists
+        self.block_first_tile = torch.arange(self.N_b + 1, device=device, dtype=torch.int32) * tpb
+        self.block_id_of_tile = torch.clamp(torch.arange(self.Nt, device=device, dtype=torch.int32) // tpb,
+                                            max=self.N_b - 1)
+
+    def args(self):
+        return (*self.grid, *self.pgrid, *self.chunk, self.rows)
+
+
+def chunk_gather_pool(x: torch.Tensor, lay: ChunkLayout, valid: Optional[torch.Tensor] = None, *, rows: bool = True,
+                      pool: bool = False, counts: bool = False, dot_with: Optional[torch.Tensor] = None):
+    """Rearrange x [B,H,S_in,D] (THW of lay.grid) into lay's chunk order
+    (bf16 rows, lay.rows per head, zero rows at padding) and optionally pool
+    chunk means / counts / rowdot with dot_with.  Returns a dict like
+    gather_pool."""
+    _cuda(x, valid, dot_with)
+    x = x.contiguous()
+    B, H, S, D = x.shape
+    if S != lay.S_in:
+        raise ValueError(f"sequence length {S} != grid {lay.grid} ({lay.S_in} tokens)")
+    dev = x.device
+    out = {}
+    out["rows"] = torch.empty((B, H, lay.rows, D), device=dev, dtype=torch.bfloat16) if rows else None
+    out["block_mean"] = torch.empty((B, H, lay.N_b, D), device=dev, dtype=torch.float32) if pool else None
+    if counts:
+        out["block_count"] = torch.empty(lay.N_b, device=dev, dtype=torch.int32)
+        out["tile_count"] = torch.empty(lay.Nt, device=dev, dtype=torch.int32)
+        out["valid_re"] = torch.empty(lay.rows, device=dev, dtype=torch.uint8)
+    else:
+        out["block_count"] = out["tile_count"] = out["valid_re"] = None
+    rowdot = None
+    if dot_with is not None:
+        dot_with = dot_with.contiguous()
+        if dot_with.dtype != torch.bfloat16 or dot_with.shape != (B, H, lay.rows, D):
+            raise ValueError("chunk_gather_pool: dot_with must be bf16 [B,H,rows,D] in chunk order")
+        rowdot = torch.empty((B, H, lay.rows), device=dev, dtype=torch.float32)
+    out["rowdot"] = rowdot
+    vm = _u8(valid)
+    if vm is not None and vm.numel() != lay.S_in:
+        raise ValueError(f"valid mask has {vm.numel()} entries, grid {lay.grid} has {lay.S_in} tokens")
+    _call("prism_chunk_gather_pool", _p(x), _code(x), B, H, D, _p(vm), *lay.args(), _p(out["rows"]),
+          _p(out["block_mean"]), _p(out["block_count"]), _p(out["tile_count"]), _p(out["valid_re"]), _p(dot_with),
+          _p(rowdot), _stream())
+    return out
+
+
+def chunk_scatter_rows(rows: torch.Tensor, lay: ChunkLayout, out_dtype: torch.dtype) -> torch.Tensor:
+    """Chunk-order bf16 rows [B,H,lay.rows,D] -> THW rows [B,H,S_in,D] of
+    out_dtype (padding dropped)."""
+    _cuda(rows)
+    rows = rows.contiguous()
+    B, H, R, D = rows.shape
+    if R != lay.rows:
+        raise ValueError(f"rows per head {R} != layout rows {lay.rows}")
+    out = torch.empty((B, H, lay.S_in, D), device=rows.device, dtype=out_dtype)
+    _call("prism_chunk_scatter_rows", _p(rows), B, H, D, *lay.args(), _p(out), _code(out), _stream())
+    return out
+
+
 # ------------------------------------------------------------------ selection
 def block_scores(qc: torch.Tensor, kc: torch.Tensor, block_count: Optional[torch.Tensor]) -> torch.Tensor:
-    """[..., N, D] fp32 block means -> [..., N, N] fp32 scores (invalid keys -inf)."""
+    """[..., Nq, D] x [..., Nk, D] fp32 block means -> [..., Nq, Nk] fp32
+    scores (keys with block_count 0 get -inf when block_count is given)."""
     _cuda(qc, kc, block_count)
-    N, D = qc.shape[-2], qc.shape[-1]
-    BH = qc.numel() // (N * D)
+    Nq, D = qc.shape[-2], qc.shape[-1]
+    Nk = kc.shape[-2]
+    BH = qc.numel() // (Nq * D)
+    if kc.shape[-1] != D or kc.numel() != BH * Nk * D:
+        raise ValueError("block_scores: q and k means must share batch dims and D")
     qc = qc.contiguous().float()
     kc = kc.contiguous().float()
-    out = torch.empty((*qc.shape[:-1], N), device=qc.device, dtype=torch.float32)
-    _call("prism_block_scores", _p(qc), _p(kc), _p(block_count), BH, N, D, _p(out), _stream())
+    out = torch.empty((*qc.shape[:-1], Nk), device=qc.device, dtype=torch.float32)
+    _call("prism_block_scores", _p(qc), _p(kc), _p(block_count), BH, Nq, Nk, D, _p(out), _stream())
     return out
 
 
@@ -266,15 +361,16 @@ def selection_params(N: int, sparsity: Optional[float], cdf_threshold: Optional[
 
 
 def select_tiles(scores: torch.Tensor, sparsity, cdf_threshold, sm_scale: float, block_first_tile: torch.Tensor,
-                 tile_count: Optional[torch.Tensor], want_blocks: bool = False):
-    """Per-row selection + tile expansion.  scores: [..., N, N] fp32.
+                 tile_count: Optional[torch.Tensor], want_blocks: bool = False, tiles_per_block: int = 2):
+    """Per-row selection + tile expansion.  scores: [..., Nq, N] fp32 (N key
+    blocks of at most tiles_per_block tiles).
     Returns dict(tiles [rows, tcap] int32, ntiles [rows], sel_blocks, nsel, tcap)."""
     _cuda(scores, block_first_tile, tile_count)
     N = scores.shape[-1]
     rows = scores.numel() // N
     mode, k_lo, ub = selection_params(N, sparsity, cdf_threshold)
     width = min(k_lo, N) if mode == 0 else ub
-    tcap = max(2 * width, 1)
+    tcap = max(tiles_per_block * width, 1)
     dev = scores.device
     tiles = torch.empty((rows, tcap), device=dev, dtype=torch.int32)
     ntiles = torch.empty(rows, device=dev, dtype=torch.int32)
@@ -299,35 +395,39 @@ def tile_rows(ntiles: torch.Tensor, block_id_of_tile: torch.Tensor, BH: int, Nt:
     return qstart, qlen
 
 
-def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tensor, BH: int, Nt: int):
-    """Per-query-tile key lists -> per-key-tile ascending query lists."""
+def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tensor, BH: int, Nt: int,
+                    Ntk: Optional[int] = None):
+    """Per-query-tile key lists (Nt query tiles per head, key tiles < Ntk,
+    default Nt) -> per-key-tile ascending query lists."""
     _cuda(qstart, qlen, qcols)
+    Ntq, Ntk = int(Nt), int(Nt if Ntk is None else Ntk)
     dev = qstart.device
-    words = (Nt + 31) // 32
-    bitmap = torch.empty(BH * Nt * words, device=dev, dtype=torch.int32)
-    kstart = torch.empty(BH * Nt, device=dev, dtype=torch.int64)
-    klen = torch.empty(BH * Nt, device=dev, dtype=torch.int32)
-    kcols = torch.empty(BH * Nt * Nt, device=dev, dtype=torch.int32)
-    _call("prism_transpose_lists", _p(qstart), _p(qlen), _p(qcols), BH, Nt, _p(bitmap), Nt, _p(kstart), _p(klen),
-              _p(kcols), _stream())
+    words = (Ntq + 31) // 32
+    bitmap = torch.empty(BH * Ntk * words, device=dev, dtype=torch.int32)
+    kstart = torch.empty(BH * Ntk, device=dev, dtype=torch.int64)
+    klen = torch.empty(BH * Ntk, device=dev, dtype=torch.int32)
+    kcols = torch.empty(BH * Ntk * Ntq, device=dev, dtype=torch.int32)
+    _call("prism_transpose_lists", _p(qstart), _p(qlen), _p(qcols), BH, Ntq, Ntk, _p(bitmap), Ntq, _p(kstart),
+          _p(klen), _p(kcols), _stream())
     return kstart, klen, kcols
 
 
 # ------------------------------------------------------------------ attention
 def pair_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt: int,
-               tmasks: Optional[torch.Tensor] = None):
+               tmasks: Optional[torch.Tensor] = None, col_tiles: Optional[int] = None):
     """Sorted union of the lists of each row pair (2p, 2p+1) with membership
     flags (entry = tile << 3 | partial << 2 | in_second << 1 | in_first).
-    Returns (ustart [rows/2] int64, ulen [rows/2] int32, ucols int32)."""
+    Nt: rows (tiles) per head; col_tiles: bound of the listed tiles (default
+    Nt).  Returns (ustart [rows/2] int64, ulen [rows/2] int32, ucols int32)."""
     _cuda(start, length, cols, tmasks)
     rows = start.numel()
     pairs = rows // 2
     dev = start.device
-    ucap = int(Nt)
+    ucap = int(Nt if col_tiles is None else col_tiles)
     ustart = torch.empty(pairs, device=dev, dtype=torch.int64)
     ulen = torch.empty(pairs, device=dev, dtype=torch.int32)
     ucols = torch.empty(max(pairs * ucap, 1), device=dev, dtype=torch.int32)
-    _call("prism_pair_union", _p(start), _p(length), _p(cols), rows, int(Nt), _p(tmasks), ucap, _p(ustart),
+    _call("prism_pair_union", _p(start), _p(length), _p(cols), rows, int(Nt), ucap, _p(tmasks), ucap, _p(ustart),
           _p(ulen), _p(ucols), _stream())
     return ustart, ulen, ucols
 
@@ -358,16 +458,24 @@ def _bf16(t: torch.Tensor, name: str) -> torch.Tensor:
     return t.contiguous()
 
 
+def _attn_shapes(q, k, v):
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    if k.shape != (B, H, Sk, D) or v.shape != k.shape:
+        raise ValueError(f"attention shapes differ: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    return B, H, Sq, Sk, D
+
+
 def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float):
-    """q, k, v [B,H,S,D] bf16 tile order; qunion = pair_union of the
-    per-query-tile key lists -> (o bf16, lse fp32 natural)."""
+    """q [B,H,Sq,D], k, v [B,H,Sk,D] bf16 tile order; qunion = pair_union of
+    the per-query-tile key lists -> (o bf16, lse fp32 natural)."""
     _cuda(q, k, v, tmasks)
     q, k, v = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v")
-    B, H, S, D = q.shape
+    B, H, Sq, Sk, D = _attn_shapes(q, k, v)
     ustart, ulen, ucols = qunion
     o = torch.empty_like(q)
-    lse = torch.empty((B, H, S), device=q.device, dtype=torch.float32)
-    _call("prism_bsa_fwd", _p(q), _p(k), _p(v), B * H, S, D, _p(tmasks), _p(ustart), _p(ulen), _p(ucols),
+    lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
+    _call("prism_bsa_fwd", _p(q), _p(k), _p(v), B * H, Sq, Sk, D, _p(tmasks), _p(ustart), _p(ulen), _p(ucols),
           float(sm_scale), _p(o), _p(lse), _stream())
     return o, lse
 
@@ -378,13 +486,15 @@ def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: 
     dq, dk, dv (bf16, tile order)."""
     _cuda(q, k, v, do, m2, delta, kv_valid, tmasks)
     q, k, v, do = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"), _bf16(do, "do")
-    B, H, S, D = q.shape
+    B, H, Sq, Sk, D = _attn_shapes(q, k, v)
+    if do.shape != q.shape:
+        raise ValueError("do must have q's shape")
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     s = _stream()
-    _call("prism_bsa_bwd_dkdv", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, S, D, _p(kv_valid),
+    _call("prism_bsa_bwd_dkdv", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(kv_valid),
           _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), float(sm_scale), _p(dk), _p(dv), s)
-    _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, S, D, _p(tmasks),
+    _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(tmasks),
           _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), float(sm_scale), _p(dq), s)
     return dq, dk, dv
