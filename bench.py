@@ -267,6 +267,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
+    ap.add_argument("--path", default="dynamic", choices=("dynamic", "uniform"),
+                    help="dynamic: _run_bsa_dynamic (the headline); uniform: the fixed 4x4x4-chunk branch of "
+                         "_run_bsa (flash_attn_bsa_3d) on the same inputs and selection parameters")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -294,6 +297,9 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     log(f"[bench] config {args.config}: generating inputs")
     inp = make_inputs(args.config)
+    if args.path == "uniform":
+        run_uniform(args, inp)
+        return
     B, H, D, S = inp["B"], inp["H"], inp["D"], inp["S"]
     grid = inp["grid"]
     gp, _ = padded_grid(grid)
@@ -432,6 +438,101 @@ def main():
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "dense": dense, "breakdown": breakdown,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def run_uniform(args, inp):
+    """The uniform-shape branch of _run_bsa (4x4x4 chunks, flash_attn_bsa_3d
+    with the grid padded to whole chunks) fwd + bwd on the config's inputs,
+    top-k + cumulative threshold as the headline.  Prints one JSON line of the
+    headline schema with workload "<config>-uniform"."""
+    import torch
+    from prism_amd import ops
+    from prism_amd.adapter import run_bsa_uniform
+    from prism_amd.uniform_block_attention import plan_chunked
+    B, H, D, S = inp["B"], inp["H"], inp["D"], inp["S"]
+    grid = inp["grid"]
+    chunk = (4, 4, 4)
+    lq = ops.ChunkLayout(grid, chunk, "cuda")
+    N_b = lq.N_b
+    if inp["sp_only"] is not None:
+        sparsity, cdf = inp["sp_only"], None
+    else:
+        sparsity, cdf = 1.0 - (inp["topk"] + 0.5) / N_b, inp["cdf"]
+    params = {"sparsity": sparsity, "cdf_threshold": cdf, "chunk_3d_shape_q": list(chunk),
+              "chunk_3d_shape_k": list(chunk)}
+    log(f"[bench] uniform: padded grid {lq.pgrid} N_b={N_b} sparsity={sparsity:.6f} cdf={cdf}")
+    q = inp["q"].clone().requires_grad_(True)
+    k = inp["k"].clone().requires_grad_(True)
+    v = inp["v"].clone().requires_grad_(True)
+    do = inp["do"]
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = run_bsa_uniform(q, k, v, grid, params)
+        out.backward(do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log("[bench] timed steps")
+    with ops.kernel_timing() as tm:
+        st = torch.cuda.Event(enable_timing=True)
+        en = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        st.record()
+        for _ in range(args.steps):
+            step()
+        en.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    ms = st.elapsed_time(en) / args.steps
+    kt = ops.summarize(tm)
+    with torch.no_grad():
+        plan = plan_chunked(q.detach(), k.detach(), v.detach(), lq, lq, sparsity=sparsity, cdf_threshold=cdf,
+                            sm_scale=1 / math.sqrt(D))
+    sum_lens = plan.sum_lens()
+    union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
+    fl = 64 * 64 * D * sum_lens
+    kept_flops = 14 * fl
+    attn = {"prism_bsa_fwd": (4 * fl, 4 * fl), "prism_bsa_bwd_dkdv": (8 * fl, 8 * fl),
+            "prism_bsa_bwd_dq": (2 * fl, 6 * fl)}
+    X_in, X_rows = B * H * S * D * 2, B * H * lq.rows * D * 2
+    hbm = {"prism_chunk_gather_pool": (4 * (X_in + X_rows) + X_rows) / 4,  # q, k, v, dO (+ O for delta)
+           "prism_chunk_scatter_rows": X_rows + X_in,
+           "prism_block_scores": 2 * B * H * N_b * D * 4 + B * H * N_b * N_b * 4,
+           "prism_select_tiles": B * H * N_b * N_b * 4 + 4 * int(plan.sel["ntiles"].sum().item()) + 4 * B * H * N_b}
+    breakdown = {}
+    for name, (n, t) in sorted(kt.items(), key=lambda x: -x[1][0] * x[1][1]):
+        e = {"launches_per_step": n // args.steps, "ms": round(t, 4)}
+        if name in attn:
+            alg, exe = attn[name]
+            e.update(tflops=round(alg / (t * 1e-3) / 1e12, 1), executed_tflops=round(exe / (t * 1e-3) / 1e12, 1),
+                     mfma_frac=round(alg / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+        elif name in hbm:
+            e.update(GBps=round(hbm[name] / (t * 1e-3) / 1e9, 1),
+                     hbm_frac=round(hbm[name] / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
+        breakdown[name] = e
+    dom = max((n for n in kt if n in attn), key=lambda n: kt[n][1])
+    dom_ms = kt[dom][1]
+    att_ms = sum(kt[n][1] for n in attn if n in kt)
+    value = kept_flops / (ms * 1e-3) / 1e12
+    rec = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{args.config}-uniform: flash_attn_bsa_3d, 4x4x4 chunks (_run_bsa uniform branch)",
+                   "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(lq.pgrid), "chunk": list(chunk),
+                   "topk": inp["topk"], "cdf_threshold": cdf, "sparsity": sparsity, "N_b": N_b,
+                   "sum_lens": sum_lens, "density": round(sum_lens / (B * H * lq.Nt * lq.Nt), 4),
+                   "pair_union_efficiency": round(union_eff, 4), "wall_ms_per_step": round(wall_ms, 3),
+                   "attention_ms": round(att_ms, 3),
+                   "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": None, "breakdown": breakdown,
     }
     print(json.dumps(rec), flush=True)
 

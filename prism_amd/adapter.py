@@ -1,6 +1,7 @@
 """Caller-side adapter: the contract of SelfAttention._run_bsa_dynamic
 (hymm/models/modules/wan_video_dit.py:342-432) and the A2V norm computation
-(wan_video_dit.py:739-752), on top of flash_attn_bsa_3d_dynamic.
+(wan_video_dit.py:739-752), on top of flash_attn_bsa_3d_dynamic; and the plain
+uniform-shape branch of SelfAttention._run_bsa (run_bsa_uniform).
 
 Pads T, H, W up to multiples of ZONE_SIZE, builds the valid mask of the
 padded grid, pads the audio norms with zeros, reuses cached shape ids within
@@ -16,6 +17,7 @@ import torch.nn.functional as F
 from . import ops
 from .dynamic_block_attention import flash_attn_bsa_3d_dynamic
 from .dynamic_block_shape import ZONE_SIZE
+from .uniform_block_attention import bsa_chunked
 
 # default bsa_params keys and values read by the reference (wan_video_dit.py:415-421)
 DEFAULT_BSA_PARAMS = {
@@ -112,3 +114,33 @@ class DynamicBlockSparseAttention:
         if need_pad:
             out = out.view(B, n_heads, Tp, Hp, Wp, D)[:, :, :T, :H, :W, :].contiguous().reshape(B, n_heads, T * H * W, D)
         return out
+
+
+# bsa_params keys the uniform branch does not pass to the kernel (wan_video_dit.py:511-520)
+GUIDANCE_ONLY_KEYS = ("audio_boost_gamma", "audio_weighted_lambda", "timestep_gate_mode", "timestep_gate_power",
+                      "timestep_gate_scale", "timestep_gate_threshold", "variance_boost_gamma", "taylor_alpha_f",
+                      "dynamic_block_lambda_a", "dynamic_block_tau_128", "dynamic_block_lambda_128")
+
+
+def run_bsa_uniform(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid_size, bsa_params: dict,
+                    compute_padded_queries: bool = False) -> torch.Tensor:
+    """The plain uniform-shape branch of SelfAttention._run_bsa
+    (wan_video_dit.py:470-507 padding, :674-686 flash_attn_bsa_3d, :688-692
+    unpadding): T, H, W are padded up to multiples of the per-axis maximum of
+    chunk_3d_shape_q / _k (default 4x4x4), the padding is masked, and the
+    output has the unpadded THW shape.  Here the padding, the rearrangement
+    and the unpadding happen inside the chunk gather / scatter kernels (no
+    padded copies of q, k, v or the output)."""
+    B, Hn, S, D = q.shape
+    T, H, W = (int(x) for x in grid_size)
+    assert T * H * W == S
+    kw = {key: val for key, val in bsa_params.items() if key not in GUIDANCE_ONLY_KEYS}
+    cq = tuple(kw.get("chunk_3d_shape_q", (4, 4, 4)))
+    ck = tuple(kw.get("chunk_3d_shape_k", (4, 4, 4)))
+    ct, ch, cw = max(cq[0], ck[0]), max(cq[1], ck[1]), max(cq[2], ck[2])
+    pgrid = (-(-T // ct) * ct, -(-H // ch) * ch, -(-W // cw) * cw)
+    lq = ops.ChunkLayout((T, H, W), cq, q.device, pgrid=pgrid)
+    lk = ops.ChunkLayout((T, H, W), ck, q.device, pgrid=pgrid)
+    return bsa_chunked(q, k, v, lq, lk, sparsity=kw.get("sparsity", 0.875), cdf_threshold=kw.get("cdf_threshold"),
+                       sm_scale=1.0 / (D ** 0.5), compute_padded_queries=compute_padded_queries)
+

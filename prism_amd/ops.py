@@ -232,7 +232,7 @@ class ChunkLayout:
     128 (the attention kernels process tile pairs); rows past the padded grid
     are padding.  Chunks hold 64 or 128 tokens (one or two kernel tiles)."""
 
-    def __init__(self, grid, chunk, device):
+    def __init__(self, grid, chunk, device, pgrid=None):
         T, H, W = _grid(grid)
         ct, ch, cw = (int(c) for c in chunk)
         if min(T, H, W, ct, ch, cw) <= 0:
@@ -243,7 +243,11 @@ class ChunkLayout:
                              "of 64 or 128 tokens")
         self.grid = (T, H, W)
         self.chunk = (ct, ch, cw)
-        self.pgrid = (-(-T // ct) * ct, -(-H // ch) * ch, -(-W // cw) * cw)
+        if pgrid is None:
+            pgrid = (-(-T // ct) * ct, -(-H // ch) * ch, -(-W // cw) * cw)
+        self.pgrid = _grid(pgrid)
+        if any(p < g or p % c for p, g, c in zip(self.pgrid, self.grid, self.chunk)):
+            raise ValueError(f"padded grid {self.pgrid} must cover {self.grid} in whole chunks {self.chunk}")
         self.S_in = T * H * W
         self.Sp = self.pgrid[0] * self.pgrid[1] * self.pgrid[2]
         self.rows = -(-self.Sp // 128) * 128

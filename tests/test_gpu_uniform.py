@@ -265,3 +265,35 @@ def test_uniform_errors():
         flash_attn_bsa_cross(q, q, q, "2d", "1d")
     with pytest.raises(NotImplementedError):
         flash_attn_bsa(q, q, q, 64, 64, 0.5, None, 0.125, score_modifier=torch.ones(1, device=DEV))
+
+
+def test_run_bsa_uniform_matches_padded_reference_flow():
+    """run_bsa_uniform (fused padding) equals the reference's flow of
+    _run_bsa: F.pad to whole chunks + valid mask + flash_attn_bsa_3d + slice
+    (wan_video_dit.py:470-507, :674-692), bit for bit, gradients included."""
+    import torch.nn.functional as F
+    from prism_amd.adapter import run_bsa_uniform
+    from prism_amd.uniform_block_attention import flash_attn_bsa_3d
+    B, H, D = 1, 2, 128
+    grid = (5, 10, 14)
+    pg = (8, 12, 16)
+    S = int(np.prod(grid))
+    rng = np.random.default_rng(51)
+    qh, kh, vh, doh = (bf16(rng.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(4))
+    params = {"sparsity": 0.6, "cdf_threshold": 0.9, "chunk_3d_shape_q": [4, 4, 4], "chunk_3d_shape_k": [4, 4, 4],
+              "variance_boost_gamma": 1.0}
+    q1, k1, v1 = (dev(a).requires_grad_(True) for a in (qh, kh, vh))
+    o1 = run_bsa_uniform(q1, k1, v1, grid, params)
+    o1.backward(dev(doh))
+    q2, k2, v2 = (dev(a).requires_grad_(True) for a in (qh, kh, vh))
+    pad = lambda t: F.pad(t.view(B, H, *grid, D), (0, 0, 0, pg[2] - grid[2], 0, pg[1] - grid[1], 0, pg[0] - grid[0])
+                          ).reshape(B, H, -1, D)
+    t_, h_, w_ = torch.meshgrid(*(torch.arange(g, device=DEV) for g in pg), indexing="ij")
+    vm = ((t_ < grid[0]) & (h_ < grid[1]) & (w_ < grid[2])).reshape(-1)
+    o2p = flash_attn_bsa_3d(pad(q2), pad(k2), pad(v2), pg, pg, sparsity=0.6, cdf_threshold=0.9,
+                            chunk_3d_shape_q=(4, 4, 4), chunk_3d_shape_k=(4, 4, 4), valid_mask=vm)
+    o2 = o2p.view(B, H, *pg, D)[:, :, :grid[0], :grid[1], :grid[2]].reshape(B, H, S, D)
+    o2.backward(dev(doh))
+    assert bits_equal(host(o1), host(o2))
+    for a, b in ((q1, q2), (k1, k2), (v1, v2)):
+        assert bits_equal(host(a.grad), host(b.grad))
