@@ -178,7 +178,8 @@ int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int3
 
 /* Work lists of the paired-tile attention kernels.  Every attention kernel runs
  * one workgroup per pair of tiles (2p, 2p+1) and walks the sorted union of the
- * two tiles' lists.  For pair p (rows 2p, 2p+1 of a per-row list; rows =
+ * two tiles' lists.  For pair p (rows 2p, 2p+1 of a per-row list, or the
+ * rows pairmap[2p], pairmap[2p+1] of the pair's head when pairmap is given; rows =
  * BH*row_tiles, row_tiles even; entries are tiles < col_tiles):
  * ucols[ustart[p] .. + ulen[p]) ascending entries
  * tile << 3 | partial << 2 | in_row_2p+1 << 1 | in_row_2p, where partial =
@@ -188,8 +189,21 @@ int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int3
  * query lists of prism_transpose_lists (dK/dV; bsa_interface.py:437-447).
  * No counterpart routine in the reference: its kernels take one list per tile. */
 int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
-                     int64_t col_tiles, const uint64_t* tile_masks, int64_t ucap, int64_t* ustart, int32_t* ulen,
-                     int32_t* ucols, hipStream_t stream);
+                     int64_t col_tiles, const int32_t* pairmap, const uint64_t* tile_masks, int64_t ucap,
+                     int64_t* ustart, int32_t* ulen, int32_t* ucols, hipStream_t stream);
+
+/* Pairing of the tiles that the paired kernels process together: inside each
+ * group of 8 consecutive tiles of a head (fewer at a head's end), the perfect
+ * matching with the largest summed list overlap |A n B| over its pairs (ties:
+ * the lowest matching index, where matching m pairs the first free tile with
+ * the (m mod (free - 1))-th other free tile, m /= (free - 1), and so on).
+ * Lists as for prism_pair_union.  pairmap [rows]: pair p of a head is the
+ * tiles pairmap[2p], pairmap[2p+1] (indices inside the head), listed by
+ * their first tile.  Pairing changes no result: every tile still walks its
+ * own list in ascending order.  No counterpart in the reference (its kernels
+ * take one tile per program). */
+int prism_pair_tiles(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
+                     int64_t col_tiles, int32_t* pairmap, hipStream_t stream);
 
 /* Key validity per 64-token tile (the reference's kv_valid_mask,
  * bsa_interface.py:328-385, flash_attn_bsa_varlen_mask.py:263-295) packed as
@@ -208,11 +222,12 @@ int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
  * (tiles are processed in pairs).  q: [BH,Sq,D], k, v: [BH,Sk,D] bf16 tile
  * order; ustart/ulen/ucols: prism_pair_union of the per-query-tile key lists
  * with the same tile_masks (prism_tile_masks of the key validity, or NULL when
- * no key is padded).  o: [BH,Sq,D] bf16; lse: [BH,Sq] fp32 natural log (-inf
+ * no key is padded) and the same pairmap (prism_pair_tiles of those lists, or
+ * NULL for tiles 2p, 2p+1).  o: [BH,Sq,D] bf16; lse: [BH,Sq] fp32 natural log (-inf
  * for rows without a valid key; their o is 0). */
 int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
                   const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen, const int32_t* ucols,
-                  float sm_scale, void* o, float* lse, hipStream_t stream);
+                  const int32_t* pairmap, float sm_scale, void* o, float* lse, hipStream_t stream);
 
 /* _attn_bwd_preprocess (common.py:110-127): delta[r] = sum_d o[r][d] * do[r][d]
  * over rows of bf16 [rows, D] tensors; fp32 out. */
@@ -224,11 +239,13 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
  * prism_lse_to_m2; delta [BH,Sq] from prism_gather_pool or
  * prism_bwd_preprocess; kv_valid: [Sk] uint8 tile order or NULL;
  * ustart/ulen/ucols: prism_pair_union of the per-key-tile query lists of
- * prism_transpose_lists (tile_masks NULL).  dk, dv: [BH,Sk,D] bf16. */
+ * prism_transpose_lists (tile_masks NULL), built with the key-tile pairing
+ * pairmap (prism_pair_tiles of those lists, or NULL for tiles 2p, 2p+1).
+ * dk, dv: [BH,Sk,D] bf16. */
 int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
                        const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint8_t* kv_valid,
-                       const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk,
-                       void* dv, hipStream_t stream);
+                       const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap,
+                       float sm_scale, void* dk, void* dv, hipStream_t stream);
 
 /* dQ of attn_bwd_bsa_varlen_triton (bsa_interface.py:489-523;
  * _attn_bwd_dq_bsa_varlen_align_wrapper, flash_attn_bsa_varlen_mask.py:879-1014).
@@ -236,7 +253,8 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
  * prism_bsa_fwd; dq: [BH,Sq,D] bf16. */
 int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
                      int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart,
-                     const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream);
+                     const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap, float sm_scale, void* dq,
+                     hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -410,9 +410,60 @@ def tile_masks(valid: np.ndarray) -> np.ndarray:
     return (v << np.arange(TILE, dtype=np.uint64)[None, :]).sum(axis=1, dtype=np.uint64)
 
 
-def pair_union(start, length, cols, Nt, masks=None):
-    """For each row pair (2p, 2p+1): the ascending union of the two rows'
-    tile lists, entry = tile << 3 | partial << 2 | in_second << 1 | in_first,
+def _matching(m: int, g: int):
+    """Matching m of g rows: the first free row pairs with the
+    (m mod (free - 1))-th other free row, then m //= free - 1, and so on."""
+    free = list(range(g))
+    pairs = []
+    while free:
+        a = free[0]
+        c = m % (len(free) - 1)
+        m //= len(free) - 1
+        b = free[1 + c]
+        pairs.append((a, b))
+        free = [x for x in free[1:] if x != b]
+    return pairs
+
+
+def pair_tiles(start, length, cols, Nt, col_tiles=None, group=8):
+    """Pairing of the tiles of each group of `group` consecutive tiles of a
+    head that maximises the summed list overlap of its pairs (ties: the lowest
+    matching index of _matching).  Returns pairmap [rows] int32 (indices
+    inside the head); pair p of a head is (pairmap[2p], pairmap[2p+1]).  No
+    reference counterpart: it only chooses which tiles share a workgroup."""
+    start = np.asarray(start, np.int64)
+    length = np.asarray(length, np.int64)
+    cols = np.asarray(cols, np.int64)
+    col_tiles = Nt if col_tiles is None else col_tiles
+    rows = start.size
+    out = np.zeros(rows, np.int32)
+    for h in range(rows // Nt):
+        for r0 in range(0, Nt, group):
+            g = min(group, Nt - r0)
+            sets = []
+            for i in range(g):
+                r = h * Nt + r0 + i
+                li = cols[start[r]: start[r] + length[r]]
+                sets.append(set(int(x) for x in li if 0 <= x < col_tiles))
+            nm = 1
+            for f in range(g - 1, 0, -2):
+                nm *= f
+            best = None
+            for m in range(nm):
+                pairs = _matching(m, g)
+                total = sum(len(sets[a] & sets[b]) for a, b in pairs)
+                if best is None or total > best[0]:
+                    best = (total, pairs)
+            for k, (a, b) in enumerate(best[1]):
+                out[h * Nt + r0 + 2 * k] = r0 + a
+                out[h * Nt + r0 + 2 * k + 1] = r0 + b
+    return out
+
+
+def pair_union(start, length, cols, Nt, masks=None, pairmap=None):
+    """For each row pair (2p, 2p+1), or the rows pairmap pairs inside each
+    head of Nt rows: the ascending union of the two rows' tile lists,
+    entry = tile << 3 | partial << 2 | in_second << 1 | in_first,
     partial = masks is given and masks[tile] is not all ones.  This is the
     work list of the paired-tile attention kernels (no reference counterpart:
     the reference walks one list per tile, bsa_interface.py:328-523)."""
@@ -421,8 +472,13 @@ def pair_union(start, length, cols, Nt, masks=None):
     cols = np.asarray(cols, np.int64)
     out = []
     for p in range(start.size // 2):
-        a = cols[start[2 * p]: start[2 * p] + length[2 * p]]
-        b = cols[start[2 * p + 1]: start[2 * p + 1] + length[2 * p + 1]]
+        if pairmap is None:
+            ra, rb = 2 * p, 2 * p + 1
+        else:
+            h0 = (2 * p) // Nt * Nt
+            ra, rb = h0 + int(pairmap[2 * p]), h0 + int(pairmap[2 * p + 1])
+        a = cols[start[ra]: start[ra] + length[ra]]
+        b = cols[start[rb]: start[rb] + length[rb]]
         u = np.union1d(a, b)
         e = (u << 3) | np.isin(u, a).astype(np.int64) | (np.isin(u, b).astype(np.int64) << 1)
         if masks is not None:

@@ -53,6 +53,7 @@ struct BwdArgs {
   const int64_t* ustart;    // pair-union lists
   const int32_t* ulen;
   const int32_t* ucols;
+  const int32_t* pairmap;   // tiles of pair p (of the side the grid walks), or null for 2p, 2p + 1
   int64_t Sq, Sk;
   int npairs;               // tile pairs per head of the side the grid walks
   float sm_scale, scale_log2;
@@ -130,7 +131,9 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   for (int k = 0; k + 1 < kStagesDkdv; ++k)
     if (k < n) issue(ring.e[k] >> 3, k);
 
-  const int64_t key = (int64_t)(2 * pair + tk) * 64 + 32 * kh + l32;
+  const int kslot = 2 * pair + tk;
+  const int ktile = a.pairmap ? a.pairmap[(int64_t)bh * 2 * a.npairs + kslot] : kslot;
+  const int64_t key = (int64_t)ktile * 64 + 32 * kh + l32;
   bf16x8 kf[NS], vf[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -283,7 +286,9 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   for (int k = 0; k + 1 < kStagesDq; ++k)
     if (k < n) issue(ring.e[k] >> 3, k);
 
-  const int64_t qrow = (int64_t)(2 * pair + tq) * 64 + 32 * qh + l32;
+  const int qslot = 2 * pair + tq;
+  const int qtile = a.pairmap ? a.pairmap[(int64_t)bh * 2 * a.npairs + qslot] : qslot;
+  const int64_t qrow = (int64_t)qtile * 64 + 32 * qh + l32;
   bf16x8 qf[NS], df[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -401,7 +406,8 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
                        const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint8_t* kv_valid,
                        const int64_t* ustart,
-                       const int32_t* ulen, const int32_t* ucols, float sm_scale, void* dk, void* dv,
+                       const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap, float sm_scale, void* dk,
+                       void* dv,
                        hipStream_t stream) {
   int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dkdv");
   if (rc) return rc;
@@ -409,7 +415,8 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
   a.m2 = m2; a.delta = delta; a.kv_valid = kv_valid;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.Sq = Sq; a.Sk = Sk; a.npairs = (int)(Sk / 128);
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.Sq = Sq; a.Sk = Sk;
+  a.npairs = (int)(Sk / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
   if (D == 128) bsa_bwd_dkdv_kernel<128><<<blocks, 512, 0, stream>>>(a);
@@ -420,14 +427,15 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
 
 int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
                      int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen,
-                     const int32_t* ucols, float sm_scale, void* dq, hipStream_t stream) {
+                     const int32_t* ucols, const int32_t* pairmap, float sm_scale, void* dq, hipStream_t stream) {
   int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dq");
   if (rc) return rc;
   PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq: null pointer");
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
   a.m2 = m2; a.delta = delta; a.tmask = tile_masks;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.Sq = Sq; a.Sk = Sk; a.npairs = (int)(Sq / 128);
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.Sq = Sq; a.Sk = Sk;
+  a.npairs = (int)(Sq / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
   if (D == 128) bsa_bwd_dq_kernel<128><<<blocks, 256, 0, stream>>>(a);

@@ -47,6 +47,7 @@ struct FwdArgs {
   const int64_t* ustart;   // [BH * Sq/128] pair-union list starts
   const int32_t* ulen;     // [BH * Sq/128]
   const int32_t* ucols;    // entries tile << 3 | partial << 2 | in_b << 1 | in_a
+  const int32_t* pairmap;  // [BH * Sq/64]: tiles of pair p are pairmap[2p], pairmap[2p + 1] (or 2p, 2p + 1)
   int64_t Sq, Sk;
   int npairs;              // query-tile pairs per head
   float scale_log2;        // sm_scale * log2(e)
@@ -113,7 +114,9 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   for (int k = 0; k + 1 < kStages; ++k)
     if (k < n) issue(ring.e[k] >> 3, k);
 
-  const int64_t qrow = (int64_t)(2 * pair + (w >> 1)) * 64 + 32 * (w & 1) + l32;
+  const int slot2 = 2 * pair + (w >> 1);
+  const int qtile = a.pairmap ? a.pairmap[(int64_t)bh * 2 * a.npairs + slot2] : slot2;
+  const int64_t qrow = (int64_t)qtile * 64 + 32 * (w & 1) + l32;
   bf16x8 qf[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) qf[s] = ld_bf16x8(Qh + qrow * D + 16 * s + 8 * g);
@@ -233,7 +236,8 @@ extern "C" {
 
 int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
                   const uint64_t* tile_masks,
-                  const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, float sm_scale, void* o, float* lse,
+                  const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap,
+                  float sm_scale, void* o, float* lse,
                   hipStream_t stream) {
   PRISM_REQUIRE(q && k && v && ustart && ulen && ucols && o && lse, "prism_bsa_fwd: null pointer");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_bsa_fwd: head_dim %d unsupported (64, 128)", D);
@@ -243,7 +247,7 @@ int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S
   PRISM_REQUIRE((int64_t)BH * (Sq / 128) < (1ll << 31), "prism_bsa_fwd: grid too large");
   FwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.tmask = tile_masks;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.Sq = Sq; a.Sk = Sk;
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.Sq = Sq; a.Sk = Sk;
   a.npairs = (int)(Sq / 128);
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.o = (uint16_t*)o; a.lse = lse;

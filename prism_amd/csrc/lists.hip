@@ -20,10 +20,12 @@ namespace {
 
 constexpr int kUnionWin = 8192;  // tiles per LDS bitmap window (256 words)
 
-// one 256-thread workgroup per row pair
+// one 256-thread workgroup per row pair; the pair's rows are 2p, 2p + 1 of
+// the head, or pairmap[2p], pairmap[2p + 1] (row indices inside the head)
 __global__ __launch_bounds__(256) void pair_union_kernel(const int64_t* __restrict__ start,
                                                          const int32_t* __restrict__ len,
-                                                         const int32_t* __restrict__ cols, int64_t Nc,
+                                                         const int32_t* __restrict__ cols, int64_t Nr, int64_t Nc,
+                                                         const int32_t* __restrict__ pairmap,
                                                          const uint64_t* __restrict__ tile_masks, int64_t ucap,
                                                          int64_t* __restrict__ ustart, int32_t* __restrict__ ulen,
                                                          int32_t* __restrict__ ucols) {
@@ -31,7 +33,9 @@ __global__ __launch_bounds__(256) void pair_union_kernel(const int64_t* __restri
   __shared__ uint32_t wtot[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t p = blockIdx.x;
-  const int64_t rA = 2 * p, rB = rA + 1;
+  const int64_t head0 = (2 * p) / Nr * Nr;
+  const int64_t rA = pairmap ? head0 + pairmap[2 * p] : 2 * p;
+  const int64_t rB = pairmap ? head0 + pairmap[2 * p + 1] : 2 * p + 1;
   const int32_t* A = cols + start[rA];
   const int32_t* B = cols + start[rB];
   const int nA = len[rA], nB = len[rB];
@@ -82,6 +86,99 @@ __global__ __launch_bounds__(256) void pair_union_kernel(const int64_t* __restri
   }
 }
 
+// ------------------------------------------------------------ tile pairing
+// Tiles are paired inside groups of 8 consecutive tiles of a head (a zone of
+// the dynamic layout; 8 neighbouring chunks of the uniform one; the last
+// group of a head may be smaller, always even).  Every perfect matching of the
+// group is scored by the summed list overlap |A n B| of its pairs, and the
+// best one (lowest matching index on ties) is taken: the paired kernels walk
+// |A u B| = |A| + |B| - |A n B| list entries per pair, so the best matching
+// has the fewest idle wave slots.  Matching m of g rows: the first free row
+// pairs with the (m mod (g-1))-th other free row, then m /= (g-1), and so on.
+constexpr int kGroup = 8;
+constexpr int kPairWin = 8192;  // column tiles per bitmap window
+
+__device__ __forceinline__ int num_matchings(int g) { return g == 8 ? 105 : g == 6 ? 15 : g == 4 ? 3 : 1; }
+
+// rows of matching m of a group of g rows as pairs (pa[k], pb[k]), k < g/2,
+// ordered by their first row
+__device__ __forceinline__ void decode_matching(int m, int g, int* pa, int* pb) {
+  int freel[kGroup];
+  int nf = g;
+  for (int i = 0; i < g; ++i) freel[i] = i;
+  for (int k = 0; k < g / 2; ++k) {
+    const int a = freel[0];
+    const int c = m % (nf - 1);
+    m /= (nf - 1);
+    const int b = freel[1 + c];
+    pa[k] = a;
+    pb[k] = b;
+    // remove positions 0 and 1 + c
+    int w = 0;
+    for (int i = 1; i < nf; ++i)
+      if (i != 1 + c) freel[w++] = freel[i];
+    nf -= 2;
+  }
+}
+
+// one 256-thread workgroup per group of one head
+__global__ __launch_bounds__(256) void pair_tiles_kernel(const int64_t* __restrict__ start,
+                                                         const int32_t* __restrict__ len,
+                                                         const int32_t* __restrict__ cols, int64_t Nr, int64_t Nc,
+                                                         int64_t groups_per_head, int32_t* __restrict__ pairmap) {
+  __shared__ uint32_t bm[kGroup][kPairWin / 32];
+  __shared__ uint32_t inter[kGroup][kGroup];
+  __shared__ uint64_t best_key;
+  const int tid = threadIdx.x;
+  const int64_t hd = blockIdx.x / groups_per_head, grp = blockIdx.x - hd * groups_per_head;
+  const int64_t r0 = grp * kGroup;
+  const int g = (int)(Nr - r0 < kGroup ? Nr - r0 : kGroup);
+  if (tid < kGroup * kGroup) inter[tid / kGroup][tid % kGroup] = 0u;
+  if (tid == 0) best_key = 0ull;
+  for (int64_t w0 = 0; w0 < Nc; w0 += kPairWin) {
+    for (int i = tid; i < kGroup * (kPairWin / 32); i += 256) (&bm[0][0])[i] = 0u;
+    __syncthreads();
+    for (int r = 0; r < g; ++r) {
+      const int64_t row = hd * Nr + r0 + r;
+      const int32_t* A = cols + start[row];
+      const int n = len[row];
+      for (int i = tid; i < n; i += 256) {
+        const int64_t t = (int64_t)A[i] - w0;
+        if (t >= 0 && t < kPairWin && A[i] < Nc) atomicOr(&bm[r][t >> 5], 1u << (t & 31));
+      }
+    }
+    __syncthreads();
+    // |A_a n A_b| for a < b: thread tid takes words tid, tid + 256
+    for (int a = 0; a < g; ++a)
+      for (int b = a + 1; b < g; ++b) {
+        uint32_t c = 0;
+        for (int i = tid; i < kPairWin / 32; i += 256) c += __popc(bm[a][i] & bm[b][i]);
+        c = wave_sum_u32(c);
+        if ((tid & 63) == 0 && c) atomicAdd(&inter[a][b], c);
+      }
+    __syncthreads();
+  }
+  const int nm = num_matchings(g);
+  int pa[kGroup / 2], pb[kGroup / 2];
+  if (tid < nm) {
+    decode_matching(tid, g, pa, pb);
+    uint32_t total = 0;
+    for (int k = 0; k < g / 2; ++k) total += inter[pa[k]][pb[k]];
+    // larger overlap first, then the lower matching index
+    atomicMax((unsigned long long*)&best_key, ((uint64_t)total << 8) | (uint64_t)(255 - tid));
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int m = 255 - (int)(best_key & 255ull);
+    decode_matching(m, g, pa, pb);
+    int32_t* out = pairmap + hd * Nr + r0;
+    for (int k = 0; k < g / 2; ++k) {
+      out[2 * k] = (int32_t)(r0 + pa[k]);
+      out[2 * k + 1] = (int32_t)(r0 + pb[k]);
+    }
+  }
+}
+
 // one wave per tile: bit j of masks[t] = valid[64 t + j] != 0
 __global__ __launch_bounds__(256) void tile_masks_kernel(const uint8_t* __restrict__ valid, int64_t Nt,
                                                          uint64_t* __restrict__ masks) {
@@ -104,8 +201,8 @@ __global__ __launch_bounds__(256) void lse_to_m2_kernel(const float* __restrict_
 extern "C" {
 
 int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
-                     int64_t col_tiles, const uint64_t* tile_masks, int64_t ucap, int64_t* ustart, int32_t* ulen,
-                     int32_t* ucols, hipStream_t stream) {
+                     int64_t col_tiles, const int32_t* pairmap, const uint64_t* tile_masks, int64_t ucap,
+                     int64_t* ustart, int32_t* ulen, int32_t* ucols, hipStream_t stream) {
   PRISM_REQUIRE(start && len && cols && ustart && ulen && ucols, "prism_pair_union: null pointer");
   PRISM_REQUIRE(rows >= 0 && rows % 2 == 0, "prism_pair_union: rows must be even (pairs of tiles)");
   PRISM_REQUIRE(row_tiles > 0 && row_tiles % 2 == 0 && rows % row_tiles == 0,
@@ -115,8 +212,23 @@ int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* co
   const int64_t pairs = rows / 2;
   if (pairs == 0) return PRISM_OK;
   PRISM_REQUIRE(pairs < (1ll << 31), "prism_pair_union: too many pairs");
-  pair_union_kernel<<<(unsigned)pairs, 256, 0, stream>>>(start, len, cols, col_tiles, tile_masks, ucap, ustart, ulen, ucols);
+  pair_union_kernel<<<(unsigned)pairs, 256, 0, stream>>>(start, len, cols, row_tiles, col_tiles, pairmap, tile_masks, ucap, ustart, ulen, ucols);
   PRISM_LAUNCH_CHECK("prism_pair_union");
+  return PRISM_OK;
+}
+
+int prism_pair_tiles(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
+                     int64_t col_tiles, int32_t* pairmap, hipStream_t stream) {
+  PRISM_REQUIRE(start && len && cols && pairmap, "prism_pair_tiles: null pointer");
+  PRISM_REQUIRE(row_tiles > 0 && row_tiles % 2 == 0 && rows % row_tiles == 0,
+                "prism_pair_tiles: rows must be a multiple of an even row_tiles (tiles per head)");
+  PRISM_REQUIRE(col_tiles > 0 && col_tiles < (1ll << 30), "prism_pair_tiles: col_tiles out of range");
+  if (rows == 0) return PRISM_OK;
+  const int64_t groups = (row_tiles + kGroup - 1) / kGroup;
+  const int64_t blocks = rows / row_tiles * groups;
+  PRISM_REQUIRE(blocks < (1ll << 31), "prism_pair_tiles: too many groups");
+  pair_tiles_kernel<<<(unsigned)blocks, 256, 0, stream>>>(start, len, cols, row_tiles, col_tiles, groups, pairmap);
+  PRISM_LAUNCH_CHECK("prism_pair_tiles");
   return PRISM_OK;
 }
 

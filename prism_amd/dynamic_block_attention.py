@@ -79,8 +79,11 @@ class _Plan:
         # pair unions of the per-query-tile key lists (forward, dQ) and the key
         # validity words of padded key tiles
         self.tmasks = ops.tile_masks(self.kv_valid) if masked else None
-        self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks)
+        # pair the query tiles of each zone by list overlap (fewest idle wave slots)
+        self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lay.Nt)
+        self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks, pairmap=self.qpair)
         self.klists = None
+        self.kpair = None
         self.kunion = None
 
     def sum_lens(self) -> int:
@@ -95,7 +98,7 @@ class _DynBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _Plan, sm_scale: float):
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale)
+        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair)
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
@@ -111,10 +114,11 @@ class _DynBSA(torch.autograd.Function):
         do_re, delta = gd["rows"], gd["rowdot"]
         if plan.kunion is None:
             plan.klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, plan.B * plan.H, lay.Nt)
-            plan.kunion = ops.pair_union(*plan.klists, lay.Nt)
+            plan.kpair = ops.pair_tiles(*plan.klists, lay.Nt)
+            plan.kunion = ops.pair_union(*plan.klists, lay.Nt, pairmap=plan.kpair)
         m2 = ops.lse_to_m2(lse)
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid,
-                                          plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale)
+                                          plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale, plan.qpair, plan.kpair)
         tq, tk, tv = ctx.in_dtypes
         dq = ops.scatter_rows(dq_re, lay, tq)
         dk = ops.scatter_rows(dk_re, lay, tk)

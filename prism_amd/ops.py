@@ -417,13 +417,28 @@ def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tenso
 
 
 # ------------------------------------------------------------------ attention
+def pair_tiles(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt: int,
+               col_tiles: Optional[int] = None) -> torch.Tensor:
+    """Pairing of the rows (tiles) of each group of 8 tiles of a head that
+    maximises the summed list overlap of the pairs.  Returns pairmap [rows]
+    int32: pair p of a head is tiles (pairmap[2p], pairmap[2p+1])."""
+    _cuda(start, length, cols)
+    rows = start.numel()
+    out = torch.empty(rows, device=start.device, dtype=torch.int32)
+    _call("prism_pair_tiles", _p(start), _p(length), _p(cols), rows, int(Nt), int(Nt if col_tiles is None else col_tiles),
+          _p(out), _stream())
+    return out
+
+
 def pair_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt: int,
-               tmasks: Optional[torch.Tensor] = None, col_tiles: Optional[int] = None):
-    """Sorted union of the lists of each row pair (2p, 2p+1) with membership
-    flags (entry = tile << 3 | partial << 2 | in_second << 1 | in_first).
-    Nt: rows (tiles) per head; col_tiles: bound of the listed tiles (default
-    Nt).  Returns (ustart [rows/2] int64, ulen [rows/2] int32, ucols int32)."""
-    _cuda(start, length, cols, tmasks)
+               tmasks: Optional[torch.Tensor] = None, col_tiles: Optional[int] = None,
+               pairmap: Optional[torch.Tensor] = None):
+    """Sorted union of the lists of each row pair (2p, 2p+1), or of the tiles
+    pairmap pairs, with membership flags (entry = tile << 3 | partial << 2 |
+    in_second << 1 | in_first).  Nt: rows (tiles) per head; col_tiles: bound of
+    the listed tiles (default Nt).  Returns (ustart [rows/2] int64,
+    ulen [rows/2] int32, ucols int32)."""
+    _cuda(start, length, cols, tmasks, pairmap)
     rows = start.numel()
     pairs = rows // 2
     dev = start.device
@@ -431,8 +446,8 @@ def pair_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt
     ustart = torch.empty(pairs, device=dev, dtype=torch.int64)
     ulen = torch.empty(pairs, device=dev, dtype=torch.int32)
     ucols = torch.empty(max(pairs * ucap, 1), device=dev, dtype=torch.int32)
-    _call("prism_pair_union", _p(start), _p(length), _p(cols), rows, int(Nt), ucap, _p(tmasks), ucap, _p(ustart),
-          _p(ulen), _p(ucols), _stream())
+    _call("prism_pair_union", _p(start), _p(length), _p(cols), rows, int(Nt), ucap, _p(pairmap), _p(tmasks), ucap,
+          _p(ustart), _p(ulen), _p(ucols), _stream())
     return ustart, ulen, ucols
 
 
@@ -470,25 +485,28 @@ def _attn_shapes(q, k, v):
     return B, H, Sq, Sk, D
 
 
-def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float):
+def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float, qpair: Optional[torch.Tensor] = None):
     """q [B,H,Sq,D], k, v [B,H,Sk,D] bf16 tile order; qunion = pair_union of
-    the per-query-tile key lists -> (o bf16, lse fp32 natural)."""
-    _cuda(q, k, v, tmasks)
+    the per-query-tile key lists (with the pairing qpair, or None for
+    neighbouring tiles) -> (o bf16, lse fp32 natural)."""
+    _cuda(q, k, v, tmasks, qpair)
     q, k, v = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v")
     B, H, Sq, Sk, D = _attn_shapes(q, k, v)
     ustart, ulen, ucols = qunion
     o = torch.empty_like(q)
     lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
     _call("prism_bsa_fwd", _p(q), _p(k), _p(v), B * H, Sq, Sk, D, _p(tmasks), _p(ustart), _p(ulen), _p(ucols),
-          float(sm_scale), _p(o), _p(lse), _stream())
+          _p(qpair), float(sm_scale), _p(o), _p(lse), _stream())
     return o, lse
 
 
-def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float):
+def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float,
+            qpair: Optional[torch.Tensor] = None, kpair: Optional[torch.Tensor] = None):
     """Backward over tile-order bf16 tensors; qunion / kunion = pair unions of
-    the per-query-tile key lists and of the per-key-tile query lists.  Returns
+    the per-query-tile key lists and of the per-key-tile query lists, built
+    with the pairings qpair / kpair (None: neighbouring tiles).  Returns
     dq, dk, dv (bf16, tile order)."""
-    _cuda(q, k, v, do, m2, delta, kv_valid, tmasks)
+    _cuda(q, k, v, do, m2, delta, kv_valid, tmasks, qpair, kpair)
     q, k, v, do = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"), _bf16(do, "do")
     B, H, Sq, Sk, D = _attn_shapes(q, k, v)
     if do.shape != q.shape:
@@ -498,7 +516,7 @@ def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: 
     dv = torch.empty_like(v)
     s = _stream()
     _call("prism_bsa_bwd_dkdv", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(kv_valid),
-          _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), float(sm_scale), _p(dk), _p(dv), s)
+          _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), _p(kpair), float(sm_scale), _p(dk), _p(dv), s)
     _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(tmasks),
-          _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), float(sm_scale), _p(dq), s)
+          _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), _p(qpair), float(sm_scale), _p(dq), s)
     return dq, dk, dv

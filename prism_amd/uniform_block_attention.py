@@ -68,15 +68,19 @@ class _ChunkPlan:
                                                qcount)
         self.qcols = sel["tiles"].view(-1)
         self.tmasks = ops.tile_masks(self.kv_valid) if k_masked else None
-        self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lq.Nt, self.tmasks, col_tiles=lk.Nt)
+        self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lq.Nt, lk.Nt)
+        self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lq.Nt, self.tmasks, col_tiles=lk.Nt,
+                                     pairmap=self.qpair)
         self.klists = None
+        self.kpair = None
         self.kunion = None
 
     def key_lists(self):
         if self.kunion is None:
             self.klists = ops.transpose_lists(self.qstart, self.qlen, self.qcols, self.B * self.H, self.lq.Nt,
                                               self.lk.Nt)
-            self.kunion = ops.pair_union(*self.klists, self.lk.Nt, None, col_tiles=self.lq.Nt)
+            self.kpair = ops.pair_tiles(*self.klists, self.lk.Nt, self.lq.Nt)
+            self.kunion = ops.pair_union(*self.klists, self.lk.Nt, None, col_tiles=self.lq.Nt, pairmap=self.kpair)
         return self.kunion
 
     def sum_lens(self) -> int:
@@ -91,7 +95,7 @@ class _ChunkBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _ChunkPlan, sm_scale: float):
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale)
+        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair)
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
@@ -106,7 +110,8 @@ class _ChunkBSA(torch.autograd.Function):
         kunion = plan.key_lists()
         m2 = ops.lse_to_m2(lse)
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, gd["rows"], m2, gd["rowdot"],
-                                          plan.kv_valid, plan.tmasks, plan.qunion, kunion, ctx.sm_scale)
+                                          plan.kv_valid, plan.tmasks, plan.qunion, kunion, ctx.sm_scale, plan.qpair,
+                                          plan.kpair)
         tq, tk, tv = ctx.in_dtypes
         return (ops.chunk_scatter_rows(dq_re, plan.lq, tq), ops.chunk_scatter_rows(dk_re, plan.lk, tk),
                 ops.chunk_scatter_rows(dv_re, plan.lk, tv), None, None)

@@ -72,14 +72,17 @@ def test_invalid_arguments_raise_without_gpu():
     with pytest.raises(ValueError, match="multiples of 8"):
         _lib.call("prism_zone_stats", 1, 0, 1, 64, 64, None, 4, 4, 4, 1, 1, None)
     with pytest.raises(ValueError, match="null pointer"):
-        _lib.call("prism_bsa_fwd", None, None, None, 1, 128, 128, 64, None, None, None, None, 0.1, None, None, None)
+        _lib.call("prism_bsa_fwd", None, None, None, 1, 128, 128, 64, None, None, None, None, None, 0.1, None, None,
+                  None)
     with pytest.raises(ValueError, match="head_dim"):
-        _lib.call("prism_bsa_fwd", 1, 1, 1, 1, 128, 128, 96, None, 1, 1, 1, 0.1, 1, 1, None)
+        _lib.call("prism_bsa_fwd", 1, 1, 1, 1, 128, 128, 96, None, 1, 1, 1, None, 0.1, 1, 1, None)
     with pytest.raises(ValueError, match="multiples of 128"):
-        _lib.call("prism_bsa_bwd_dq", 1, 1, 1, 1, 1, 1, 1, 128, 192, 64, None, 1, 1, 1, 0.1, 1, None)
+        _lib.call("prism_bsa_bwd_dq", 1, 1, 1, 1, 1, 1, 1, 128, 192, 64, None, 1, 1, 1, None, 0.1, 1, None)
+    with pytest.raises(ValueError, match="even row_tiles"):
+        _lib.call("prism_pair_tiles", 1, 1, 1, 10, 5, 5, 1, None)
     with pytest.raises(ValueError, match="64 or 128"):
         _lib.call("prism_chunk_gather_pool", 1, 1, 1, 1, 64, None, 4, 4, 4, 4, 4, 4, 2, 2, 2, 128,
                   None, None, None, None, None, None, None, None)
     with pytest.raises(ValueError, match="multiple of the chunk|multiples of the chunk"):
         _lib.call("prism_chunk_scatter_rows", 1, 1, 1, 64, 4, 4, 4, 4, 4, 6, 4, 4, 4, 128, 1, 1, None)
-    assert _lib.load().prism_abi_version() == 3
+    assert _lib.load().prism_abi_version() == 4

@@ -275,13 +275,20 @@ def test_pair_union_bitexact(case):
     klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, Nt)
     for lists, masks in (((plan.qstart, plan.qlen, plan.qcols), tm), (klists, None)):
         st, ln, cl = (host(t) for t in lists)
-        ustart, ulen, ucols = ops.pair_union(*lists, Nt, None if masks is None else plan.tmasks)
-        ref = O.pair_union(st, ln, cl, Nt, masks)
-        ulen, ustart, ucols = host(ulen), host(ustart), host(ucols)
-        assert len(ref) == len(ulen)
-        for p, r in enumerate(ref):
-            assert ulen[p] == len(r)
-            assert np.array_equal(ucols[ustart[p]: ustart[p] + ulen[p]], r)
+        # the pairing of each group of 8 tiles, and the unions with and without it
+        pm = ops.pair_tiles(*lists, Nt)
+        pm_ref = O.pair_tiles(st, ln, cl, Nt)
+        assert np.array_equal(host(pm), pm_ref)
+        for pairmap, pref in ((None, None), (pm, pm_ref)):
+            ustart, ulen, ucols = ops.pair_union(*lists, Nt, None if masks is None else plan.tmasks, pairmap=pairmap)
+            ref = O.pair_union(st, ln, cl, Nt, masks, pref)
+            ulen, ustart, ucols = host(ulen), host(ustart), host(ucols)
+            assert len(ref) == len(ulen)
+            for p, r in enumerate(ref):
+                assert ulen[p] == len(r)
+                assert np.array_equal(ucols[ustart[p]: ustart[p] + ulen[p]], r)
+        # the pairing never lengthens the work lists
+        assert int(host(ops.pair_union(*lists, Nt, pairmap=pm)[1]).sum()) <= int(host(ops.pair_union(*lists, Nt)[1]).sum())
 
 
 def test_lse_to_m2():
@@ -310,7 +317,11 @@ def test_attention_fwd_bwd_tolerance(case):
     sm = 1 / math.sqrt(D)
     plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
                         sparsity=0.6, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
-    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm)
+    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair)
+    # the tile pairing changes no bit: neighbouring pairs give the same O and LSE
+    q0 = ops.pair_union(plan.qstart, plan.qlen, plan.qcols, plan.lay.Nt, plan.tmasks)
+    o0, lse0 = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, q0, sm)
+    assert bits_equal(host(o), host(o0)) and bits_equal(host(lse), host(lse0))
     qf = O.bf16_bits_to_f32(host(plan.q_re)).reshape(B * H, S, D)
     kf = O.bf16_bits_to_f32(host(plan.k_re)).reshape(B * H, S, D)
     vf = O.bf16_bits_to_f32(host(plan.v_re)).reshape(B * H, S, D)
@@ -330,9 +341,15 @@ def test_attention_fwd_bwd_tolerance(case):
     delta = torch.empty((B, H, S), device=DEV, dtype=torch.float32)
     ops._lib.call("prism_bwd_preprocess", o.data_ptr(), do_t.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
     klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, plan.lay.Nt)
-    kunion = ops.pair_union(*klists, plan.lay.Nt)
-    dq, dk, dv = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_t, ops.lse_to_m2(lse), delta, plan.kv_valid,
-                             plan.tmasks, plan.qunion, kunion, sm)
+    kpair = ops.pair_tiles(*klists, plan.lay.Nt)
+    kunion = ops.pair_union(*klists, plan.lay.Nt, pairmap=kpair)
+    m2 = ops.lse_to_m2(lse)
+    dq, dk, dv = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_t, m2, delta, plan.kv_valid,
+                             plan.tmasks, plan.qunion, kunion, sm, plan.qpair, kpair)
+    grads0 = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_t, m2, delta, plan.kv_valid, plan.tmasks, q0,
+                         ops.pair_union(*klists, plan.lay.Nt), sm)
+    for g, g0 in zip((dq, dk, dv), grads0):
+        assert bits_equal(host(g), host(g0))
     dof = O.bf16_bits_to_f32(do).reshape(B * H, S, D)
     dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, og, dof, lse_ref, *lists, kv, sm)
     for name, g, r in (("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):

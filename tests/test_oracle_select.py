@@ -404,3 +404,48 @@ def test_pair_union_brute_force():
             partial = int(masks[t]) != (1 << 64) - 1
             want.append(t * 8 + (4 if partial else 0) + (2 if t in b else 0) + (1 if t in a else 0))
         assert got[p].tolist() == want
+
+
+def _all_matchings(items):
+    """Every perfect matching of `items` (independent enumeration)."""
+    if not items:
+        yield []
+        return
+    first, rest = items[0], items[1:]
+    for i, b in enumerate(rest):
+        for m in _all_matchings(rest[:i] + rest[i + 1:]):
+            yield [(first, b)] + m
+
+
+def test_pair_tiles_brute_force():
+    """The pairing of each group of 8 tiles (6 at the end of a head of 14)
+    has the largest summed list overlap of all perfect matchings; identical
+    lists (all matchings tie) pair neighbours."""
+    rng = np.random.default_rng(31)
+    Nt, BH, ncols = 14, 2, 40
+    rows = BH * Nt
+    lists = [sorted(rng.choice(ncols, size=int(rng.integers(0, ncols)), replace=False).tolist()) for _ in range(rows)]
+    cap = ncols
+    start = np.arange(rows, dtype=np.int64) * cap
+    length = np.array([len(x) for x in lists], np.int32)
+    cols = np.full(rows * cap, -1, np.int32)
+    for r, x in enumerate(lists):
+        cols[r * cap: r * cap + len(x)] = x
+    pm = O.pair_tiles(start, length, cols, Nt, ncols)
+    for h in range(BH):
+        for r0, g in ((0, 8), (8, 6)):
+            got = [(int(pm[h * Nt + r0 + 2 * k]) - r0, int(pm[h * Nt + r0 + 2 * k + 1]) - r0) for k in range(g // 2)]
+            assert sorted(a for p in got for a in p) == list(range(g))       # a perfect matching of the group
+            assert all(a < b for a, b in got) and [a for a, _ in got] == sorted(a for a, _ in got)
+            sets = [set(lists[h * Nt + r0 + i]) for i in range(g)]
+            score = lambda m: sum(len(sets[a] & sets[b]) for a, b in m)
+            assert score(got) == max(score(m) for m in _all_matchings(list(range(g))))
+    # all lists equal: every matching ties, the first (neighbours) is taken
+    same = O.pair_tiles(np.zeros(8, np.int64), np.full(8, 3, np.int32), np.array([1, 2, 3], np.int32), 8, 4)
+    assert same.tolist() == list(range(8))
+    # paired unions use the pairmap's rows
+    u = O.pair_union(start, length, cols, Nt, None, pm)
+    for p in range(rows // 2):
+        h0 = (2 * p) // Nt * Nt
+        a, b = h0 + pm[2 * p], h0 + pm[2 * p + 1]
+        assert (u[p] >> 3).tolist() == sorted(set(lists[a]) | set(lists[b]))
