@@ -3,9 +3,10 @@
 Default workload = BASELINE config 4 ("2K fwd+bwd, one GPU's head share"):
 B=1, H=5, D=128, bf16, latent grid 21x90x160 (302,400 video tokens, padded
 to 24x96x160) plus 2,000 audio tokens; hybrid top-48 + cumulative 0.9.
-A step = A2V token norms + SelfAttention._run_bsa_dynamic forward (pad,
-zone stats, shapes, gather + pooling, scores, selection, attention, scatter,
-unpad) + its backward, on synthetic inputs already resident in HBM.
+A step = A2V token norms + SelfAttention._run_bsa_dynamic forward (zone
+stats, shapes, gather + pooling, scores, selection, attention, scatter; the
+caller's padding to multiples of 8 and unpadding happen inside the gather and
+scatter kernels) + its backward, on synthetic inputs already resident in HBM.
 
 Prints ONE JSON line.  value = kept-block algorithmic FLOP/s of the step
 ((4 + 10) * 64 * 64 * D * sum_lens per step, FA convention).
@@ -290,7 +291,7 @@ def main():
         sys.exit(2)
 
     import torch
-    from prism_amd import DynamicBlockSparseAttention, a2v_token_norms, plan_dynamic, valid_mask_for
+    from prism_amd import DynamicBlockSparseAttention, a2v_token_norms, plan_dynamic
     from prism_amd import ops
     from prism_amd.adapter import padded_grid
 
@@ -309,12 +310,9 @@ def main():
     dyn = DynamicBlockSparseAttention("ivpq", {"dynamic_block_tau_128": 0.15})
     q0 = inp["q"]
     with torch.no_grad():
-        vm = valid_mask_for(grid, q0.device)
-        pad = lambda t: torch.nn.functional.pad(t.view(B, H, *grid, D), (0, 0, 0, gp[2] - grid[2], 0, gp[1] - grid[1], 0, gp[0] - grid[0])).reshape(B, H, -1, D)
-        npad = torch.nn.functional.pad(norms0.view(*grid), (0, gp[2] - grid[2], 0, gp[1] - grid[1], 0, gp[0] - grid[0])).reshape(-1)
-        from prism_amd.dynamic_block_shape import select_zone_shapes
-        sid = select_zone_shapes(pad(inp["v"]), npad, gp, "ivpq", valid_mask_thw=vm)
-        N_b = ops.ZoneLayout(sid, gp).N_b
+        from prism_amd.dynamic_block_shape import _gradient_and_shapes
+        sid = _gradient_and_shapes(inp["v"], norms0, gp, "ivpq", 0.5, 0.15, 1.0, None, grid)[2]
+        N_b = ops.ZoneLayout(sid, gp, grid).N_b
     if inp["sp_only"] is not None:
         sparsity, cdf = inp["sp_only"], None
     else:
@@ -354,8 +352,8 @@ def main():
 
     # the plan of these inputs (deterministic: identical to the one inside each step)
     with torch.no_grad():
-        plan = plan_dynamic(pad(q.detach()), pad(k.detach()), pad(v.detach()), gp, method="ivpq", sparsity=sparsity,
-                            cdf_threshold=cdf, audio_token_norms=npad, valid_mask=vm)
+        plan = plan_dynamic(q.detach(), k.detach(), v.detach(), gp, method="ivpq", sparsity=sparsity,
+                            cdf_threshold=cdf, audio_token_norms=norms0, input_grid=grid)
     sum_lens = plan.sum_lens()
     Nt, Nb, Sp = plan.lay.Nt, plan.lay.N_b, plan.S
     density = sum_lens / (B * H * Nt * Nt)
@@ -369,13 +367,14 @@ def main():
     # attention kernels: algorithmic FLOPs per launch (executed in parentheses)
     attn = {"prism_bsa_fwd": (4 * fl, 4 * fl), "prism_bsa_bwd_dkdv": (8 * fl, 8 * fl),
             "prism_bsa_bwd_dq": (2 * fl, 6 * fl)}
-    X = B * H * Sp * D * 2  # one bf16 [B,H,S_p,D] tensor
+    X = B * H * Sp * D * 2   # one bf16 [B,H,S_p,D] tile-order tensor (zone grid)
+    Xin = B * H * S * D * 2  # one bf16 [B,H,S,D] THW tensor (input grid)
     nnz_tiles = int(plan.sel["ntiles"].sum().item())
     hbm = {  # algorithmic bytes per launch (average over the step's launches of that entry point)
-        "prism_zone_stats": H * Sp * D * 2 + plan.lay.Nz * 25 * D * 4,
+        "prism_zone_stats": H * S * D * 2 + plan.lay.Nz * 25 * D * 4,
         "prism_a2v_norms": S * inp["res"].shape[-1] * 2 + S * 2,
-        "prism_gather_pool": (4 * 2 * X + X) / 4,  # q, k, v, dO: read + write rows; dO also reads O
-        "prism_scatter_rows": 2 * X,
+        "prism_gather_pool": (4 * (Xin + X) + X) / 4,  # q, k, v, dO: read THW + write rows; dO also reads O
+        "prism_scatter_rows": 2 * Xin,
         "prism_block_scores": 2 * B * H * Nb * D * 4 + B * H * Nb * Nb * 4,
         "prism_select_tiles": B * H * Nb * Nb * 4 + 4 * nnz_tiles + 4 * B * H * Nb,
     }

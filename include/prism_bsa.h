@@ -39,18 +39,29 @@ int prism_abi_version(void);
 
 /* ------------------------------------------------------------------ zone statistics */
 
+/* Input grid and zone grid.  Entry points of the dynamic path take the zone
+ * grid T x Hg x Wg (multiples of 8) and the input grid Tin x Hin x Win inside
+ * it (the caller's unpadded video; Tin = T, Hin = Hg, Win = Wg when the input
+ * is already padded).  Inputs hold S = Tin*Hin*Win tokens per head; zone-grid
+ * positions outside the input grid read as zero, invalid tokens: this is the
+ * zero padding plus valid mask of wan_video_dit.py:342-400 without the padded
+ * copies.  Tile-order rows always cover the zone grid (T*Hg*Wg per head). */
+
 /* compute_zone_aggregates (dynamic_block_shape.py:68-129) applied to the
  * batch-0 head mean of V (dynamic_block_attention.py:236).
- * v: [B,H,S,D] THW order (only batch 0 is read), valid: [S] uint8 or NULL.
- * packed: [Nz, 25*D] fp32 = channel(D) | frame means(8D) | h means(8D) | w means(8D);
- * axis_valid: [Nz, 24] uint8 (t, h, w "has a valid token" flags). */
+ * v: [B,H,S,D] THW order of the input grid (only batch 0 is read), valid: [S]
+ * uint8 or NULL.  packed: [Nz, 25*D] fp32 = channel(D) | frame means(8D) |
+ * h means(8D) | w means(8D); axis_valid: [Nz, 24] uint8 (t, h, w "has a
+ * valid token" flags). */
 int prism_zone_stats(const void* v, int dtype, int H, int64_t S, int D, const uint8_t* valid,
-                     int T, int Hg, int Wg, float* packed, uint8_t* axis_valid, hipStream_t stream);
+                     int T, int Hg, int Wg, int Tin, int Hin, int Win, float* packed, uint8_t* axis_valid,
+                     hipStream_t stream);
 
 /* compute_audio_directional (dynamic_block_shape.py:189-245) before the
- * max-normalisation of a_bar.  norms: [S] THW order.  abar: [Nz]; vhat: [Nz,3]. */
-int prism_audio_zone_stats(const void* norms, int dtype, const uint8_t* valid, int T, int Hg, int Wg,
-                           float* abar, float* vhat, hipStream_t stream);
+ * max-normalisation of a_bar.  norms: [S] THW order of the input grid.
+ * abar: [Nz]; vhat: [Nz,3]. */
+int prism_audio_zone_stats(const void* norms, int dtype, const uint8_t* valid, int T, int Hg, int Wg, int Tin,
+                           int Hin, int Win, float* abar, float* vhat, hipStream_t stream);
 
 /* Per-zone part of compute_effective_gradient (dynamic_block_shape.py:248-289):
  * rho_raw = spatial + temporal variance, aniso = axis variances / their sum. */
@@ -93,20 +104,23 @@ int prism_rearrange_index(const int64_t* shape_ids, int T, int Hg, int Wg, int64
 /* x.index_select(2, src_idx) (dynamic_block_attention.py:250-253) fused with
  * masked_mean_pooling_compression + _logical_block_means
  * (bsa_interface.py:177-201, dynamic_block_attention.py:173-188).
- * x: [B,H,S,D] THW order.  Optional outputs (NULL to skip):
- *   out_rows [B,H,S,D] bf16 tile order; block_mean [B,H,N_b,D] fp32;
- *   block_count [N_b], tile_count [S/64] int32; valid_re [S] uint8 tile order;
- *   rowdot [B,H,S] fp32 = rowsum(x_re * dot_with) with dot_with [B,H,S,D] bf16
+ * x: [B,H,S,D] THW order of the input grid.  With Sz = T*Hg*Wg zone-grid
+ * rows, optional outputs (NULL to skip):
+ *   out_rows [B,H,Sz,D] bf16 tile order; block_mean [B,H,N_b,D] fp32;
+ *   block_count [N_b], tile_count [Sz/64] int32; valid_re [Sz] uint8 tile order;
+ *   rowdot [B,H,Sz] fp32 = rowsum(x_re * dot_with) with dot_with [B,H,Sz,D] bf16
  *   tile order (the delta of common.py:110-127 when x = dO, dot_with = O). */
 int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, const uint8_t* valid,
-                      const int64_t* shape_ids, const int32_t* block_offset, int T, int Hg, int Wg, int64_t N_b,
-                      void* out_rows, float* block_mean, int32_t* block_count, int32_t* tile_count,
-                      uint8_t* valid_re, const void* dot_with, float* rowdot, hipStream_t stream);
+                      const int64_t* shape_ids, const int32_t* block_offset, int T, int Hg, int Wg, int Tin,
+                      int Hin, int Win, int64_t N_b, void* out_rows, float* block_mean, int32_t* block_count,
+                      int32_t* tile_count, uint8_t* valid_re, const void* dot_with, float* rowdot,
+                      hipStream_t stream);
 
-/* o_re.index_select(2, inv_idx) (dynamic_block_attention.py:329): tile-order
- * bf16 rows -> THW order rows of out_dtype. */
+/* o_re.index_select(2, inv_idx) (dynamic_block_attention.py:329) plus the
+ * unpadding of wan_video_dit.py:429-431: tile-order bf16 rows [B,H,T*Hg*Wg,D]
+ * -> rows of out_dtype [B,H,S,D] in THW order of the input grid. */
 int prism_scatter_rows(const void* in_rows, int B, int H, int64_t S, int D, const int64_t* shape_ids, int T,
-                       int Hg, int Wg, void* out, int out_dtype, hipStream_t stream);
+                       int Hg, int Wg, int Tin, int Hin, int Win, void* out, int out_dtype, hipStream_t stream);
 
 /* Uniform chunk layout (the fixed-shape BSA of flash_attn_bsa_3d and
  * flash_attn_bsa_cross, bsa_interface.py:1123-1176, 1276-1392):

@@ -20,16 +20,16 @@ U64 = ctypes.c_uint64
 
 # name -> argtypes (every function returns int; the last argument is the stream)
 SIGNATURES = {
-    "prism_zone_stats": [P, I32, I32, I64, I32, P, I32, I32, I32, P, P, P],
-    "prism_audio_zone_stats": [P, I32, P, I32, I32, I32, P, P, P],
+    "prism_zone_stats": [P, I32, I32, I64, I32, P, I32, I32, I32, I32, I32, I32, P, P, P],
+    "prism_audio_zone_stats": [P, I32, P, I32, I32, I32, I32, I32, I32, P, P, P],
     "prism_zone_gradient": [P, P, I32, I32, P, P, P],
     "prism_zone_shapes": [P, P, P, P, I32, I32, F32, F32, F32, P, P, P, P],
     "prism_assign_shapes": [P, P, I32, I32, F32, F32, P, P],
     "prism_a2v_norms": [P, I32, I64, I32, P, I32, P],
     "prism_zone_layout": [P, I32, P, P, P, P],
     "prism_rearrange_index": [P, I32, I32, I32, P, P, P],
-    "prism_gather_pool": [P, I32, I32, I32, I64, I32, P, P, P, I32, I32, I32, I64, P, P, P, P, P, P, P, P],
-    "prism_scatter_rows": [P, I32, I32, I64, I32, P, I32, I32, I32, P, I32, P],
+    "prism_gather_pool": [P, I32, I32, I32, I64, I32, P, P, P, I32, I32, I32, I32, I32, I32, I64, P, P, P, P, P, P, P, P],
+    "prism_scatter_rows": [P, I32, I32, I64, I32, P, I32, I32, I32, I32, I32, I32, P, I32, P],
     "prism_chunk_gather_pool": [P, I32, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I64,
                                 P, P, P, P, P, P, P, P],
     "prism_chunk_scatter_rows": [P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32, I64, P, I32, P],

@@ -3,16 +3,19 @@
 (wan_video_dit.py:739-752), on top of flash_attn_bsa_3d_dynamic; and the plain
 uniform-shape branch of SelfAttention._run_bsa (run_bsa_uniform).
 
-Pads T, H, W up to multiples of ZONE_SIZE, builds the valid mask of the
-padded grid, pads the audio norms with zeros, reuses cached shape ids within
-one training forward pass (activation-checkpoint recompute), and unpads.
+The reference pads T, H, W up to multiples of ZONE_SIZE, builds the valid
+mask of the padded grid, pads the audio norms with zeros, and unpads the
+output.  Here the kernels read the unpadded tensors directly (grid positions
+outside the input are zero, invalid tokens), so none of those copies is made;
+outputs and gradients equal the pad + call + slice flow bit for bit.  Cached
+shape ids are reused within one training forward pass (activation-checkpoint
+recompute).
 """
 from __future__ import annotations
 
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 
 from . import ops
 from .dynamic_block_attention import flash_attn_bsa_3d_dynamic
@@ -83,19 +86,9 @@ class DynamicBlockSparseAttention:
     def run_bsa_dynamic(self, q_bhsd, k_bhsd, v_bhsd, grid_size, audio_token_norms=None):
         T, H, W = grid_size
         B, n_heads, S, D = q_bhsd.shape
-        (Tp, Hp, Wp), (pt, ph, pw) = padded_grid(grid_size)
-        need_pad = pt > 0 or ph > 0 or pw > 0
-        valid_mask = None
-        audio_p = audio_token_norms
-        if need_pad:
-            valid_mask = valid_mask_for(grid_size, q_bhsd.device)
-
-            def _pad(t):
-                return F.pad(t.view(B, n_heads, T, H, W, D), (0, 0, 0, pw, 0, ph, 0, pt)).reshape(B, n_heads, -1, D)
-
-            q_bhsd, k_bhsd, v_bhsd = _pad(q_bhsd), _pad(k_bhsd), _pad(v_bhsd)
-            if audio_token_norms is not None:
-                audio_p = F.pad(audio_token_norms.reshape(T, H, W), (0, pw, 0, ph, 0, pt)).reshape(-1)
+        if S != T * H * W:
+            raise ValueError(f"sequence length {S} != T*H*W of grid {tuple(grid_size)}")
+        (Tp, Hp, Wp), _ = padded_grid(grid_size)
         grid_padded = (Tp, Hp, Wp)
         cached = None
         if self.training and self._dyn_shape_cache is not None:
@@ -106,13 +99,12 @@ class DynamicBlockSparseAttention:
         out, used = flash_attn_bsa_3d_dynamic(
             q_bhsd, k_bhsd, v_bhsd, grid_padded, method=self.method,
             sparsity=p.get("sparsity", 0.9375), cdf_threshold=p.get("cdf_threshold", None),
-            audio_token_norms=audio_p, valid_mask=valid_mask,
+            audio_token_norms=None if audio_token_norms is None else audio_token_norms.reshape(-1),
             lambda_a=p.get("dynamic_block_lambda_a", 0.5), tau_128=p.get("dynamic_block_tau_128", 0.15),
-            lambda_128=p.get("dynamic_block_lambda_128", 1.0), shape_ids=cached, return_shape_ids=True)
+            lambda_128=p.get("dynamic_block_lambda_128", 1.0), shape_ids=cached, return_shape_ids=True,
+            input_grid=(T, H, W))
         if self.training:
             self._dyn_shape_cache = (self.pass_id, grid_padded, used)
-        if need_pad:
-            out = out.view(B, n_heads, Tp, Hp, Wp, D)[:, :, :T, :H, :W, :].contiguous().reshape(B, n_heads, T * H * W, D)
         return out
 
 

@@ -71,6 +71,24 @@ __device__ __forceinline__ int64_t token_of(int z, int lf, int ZH, int ZW, int H
   return ((int64_t)(zt * 8 + lt) * Hg + zh * 8 + lh) * Wg + zw * 8 + lw;
 }
 
+// The input grid T x H x W inside the zone grid (the zone grid is the input
+// grid rounded up to multiples of 8; positions outside the input are the
+// padding of wan_video_dit.py:342-400, read as zero and invalid).
+struct GridBox {
+  int T, H, W;
+};
+// token of local coordinate lf of zone z in the input grid, or -1 (padding)
+__device__ __forceinline__ int64_t token_in(int z, int lf, int ZH, int ZW, GridBox b) {
+  const int zt = z / (ZH * ZW), zh = (z / ZW) % ZH, zw = z % ZW;
+  const int t = zt * 8 + (lf >> 6), h = zh * 8 + ((lf >> 3) & 7), w = zw * 8 + (lf & 7);
+  if (t >= b.T || h >= b.H || w >= b.W) return -1;
+  return ((int64_t)t * b.H + h) * b.W + w;
+}
+// host check: the input grid is non-empty and fits inside the zone grid
+inline bool box_ok(int T, int Hg, int Wg, int Tin, int Hin, int Win) {
+  return Tin > 0 && Hin > 0 && Win > 0 && Tin <= T && Hin <= Hg && Win <= Wg;
+}
+
 // ------------------------------------------------------------ canonical math
 // canon_exp: Cody-Waite reduction with the Cephes split of ln 2, degree-7
 // Taylor polynomial (Horner, fused), exact power-of-two scale.  x < -87 -> 0.

@@ -121,7 +121,8 @@ struct GatherArgs {
 struct ZoneMap {
   const int64_t* shape_ids;
   const int32_t* block_offset;
-  int ZH, ZW, Hg, Wg;
+  int ZH, ZW;
+  GridBox box;  // input grid (tokens outside it are padding)
   int z, c, bsz, boff;
   __device__ __forceinline__ void init(int unit) {
     z = unit;
@@ -131,7 +132,7 @@ struct ZoneMap {
   }
   __device__ __forceinline__ int64_t row(int r) const { return (int64_t)z * 512 + r; }
   __device__ __forceinline__ bool live(int) const { return true; }
-  __device__ __forceinline__ int64_t token(int r) const { return token_of(z, local_of_rearr(c, r), ZH, ZW, Hg, Wg); }
+  __device__ __forceinline__ int64_t token(int r) const { return token_in(z, local_of_rearr(c, r), ZH, ZW, box); }
   __device__ __forceinline__ int64_t block(int r) const { return boff + r / bsz; }
 };
 
@@ -302,9 +303,9 @@ void launch_scatter(const void* in_rows, int64_t S_in, int64_t S_out, const Map&
   }
 }
 
-ZoneMap zone_map(const int64_t* shape_ids, const int32_t* block_offset, int Hg, int Wg) {
+ZoneMap zone_map(const int64_t* shape_ids, const int32_t* block_offset, int Hg, int Wg, GridBox box) {
   ZoneMap m = {};
-  m.shape_ids = shape_ids; m.block_offset = block_offset; m.ZH = Hg / 8; m.ZW = Wg / 8; m.Hg = Hg; m.Wg = Wg;
+  m.shape_ids = shape_ids; m.block_offset = block_offset; m.ZH = Hg / 8; m.ZW = Wg / 8; m.box = box;
   return m;
 }
 
@@ -354,12 +355,15 @@ int prism_rearrange_index(const int64_t* shape_ids, int T, int Hg, int Wg, int64
 }
 
 int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, const uint8_t* valid,
-                      const int64_t* shape_ids, const int32_t* block_offset, int T, int Hg, int Wg, int64_t N_b,
-                      void* out_rows, float* block_mean, int32_t* block_count, int32_t* tile_count,
-                      uint8_t* valid_re, const void* dot_with, float* rowdot, hipStream_t stream) {
+                      const int64_t* shape_ids, const int32_t* block_offset, int T, int Hg, int Wg, int Tin, int Hin,
+                      int Win, int64_t N_b, void* out_rows, float* block_mean, int32_t* block_count,
+                      int32_t* tile_count, uint8_t* valid_re, const void* dot_with, float* rowdot,
+                      hipStream_t stream) {
   PRISM_REQUIRE(x && shape_ids && block_offset, "prism_gather_pool: null pointer");
   PRISM_REQUIRE(grid_ok(T, Hg, Wg), "prism_gather_pool: grid (%d,%d,%d) must be multiples of 8", T, Hg, Wg);
-  PRISM_REQUIRE((int64_t)T * Hg * Wg == S, "prism_gather_pool: T*H*W != S");
+  PRISM_REQUIRE(box_ok(T, Hg, Wg, Tin, Hin, Win), "prism_gather_pool: input grid (%d,%d,%d) must fit the zone grid",
+                Tin, Hin, Win);
+  PRISM_REQUIRE((int64_t)Tin * Hin * Win == S, "prism_gather_pool: Tin*Hin*Win != S");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_gather_pool: head_dim %d unsupported (64, 128)", D);
   PRISM_REQUIRE(B >= 1 && H >= 1, "prism_gather_pool: B, H must be >= 1");
   PRISM_REQUIRE(dtype == PRISM_F32 || dtype == PRISM_BF16, "prism_gather_pool: bad dtype");
@@ -367,24 +371,28 @@ int prism_gather_pool(const void* x, int dtype, int B, int H, int64_t S, int D, 
   PRISM_REQUIRE((block_mean == nullptr && block_count == nullptr) || N_b > 0,
                 "prism_gather_pool: N_b required for pooling and block counts");
   GatherArgs a = {};
-  a.x = x; a.valid = valid; a.S_in = S; a.S_out = S; a.N_b = N_b;
+  const int64_t S_out = (int64_t)T * Hg * Wg;
+  a.x = x; a.valid = valid; a.S_in = S; a.S_out = S_out; a.N_b = N_b;
   a.out_rows = (uint16_t*)out_rows; a.block_mean = block_mean;
   a.block_count = block_count; a.tile_count = tile_count; a.valid_re = valid_re;
   a.dot_with = (const uint16_t*)dot_with; a.rowdot = rowdot;
-  launch_gather(a, zone_map(shape_ids, block_offset, Hg, Wg), dtype, D, dim3((unsigned)(S / 512), B * H), stream);
+  launch_gather(a, zone_map(shape_ids, block_offset, Hg, Wg, GridBox{Tin, Hin, Win}), dtype, D,
+                dim3((unsigned)(S_out / 512), B * H), stream);
   PRISM_LAUNCH_CHECK("prism_gather_pool");
   return PRISM_OK;
 }
 
 int prism_scatter_rows(const void* in_rows, int B, int H, int64_t S, int D, const int64_t* shape_ids, int T, int Hg,
-                       int Wg, void* out, int out_dtype, hipStream_t stream) {
+                       int Wg, int Tin, int Hin, int Win, void* out, int out_dtype, hipStream_t stream) {
   PRISM_REQUIRE(in_rows && shape_ids && out, "prism_scatter_rows: null pointer");
   PRISM_REQUIRE(grid_ok(T, Hg, Wg), "prism_scatter_rows: grid must be multiples of 8");
-  PRISM_REQUIRE((int64_t)T * Hg * Wg == S, "prism_scatter_rows: T*H*W != S");
+  PRISM_REQUIRE(box_ok(T, Hg, Wg, Tin, Hin, Win), "prism_scatter_rows: input grid must fit the zone grid");
+  PRISM_REQUIRE((int64_t)Tin * Hin * Win == S, "prism_scatter_rows: Tin*Hin*Win != S");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_scatter_rows: head_dim %d unsupported", D);
   PRISM_REQUIRE(out_dtype == PRISM_F32 || out_dtype == PRISM_BF16, "prism_scatter_rows: bad dtype");
-  launch_scatter(in_rows, S, S, zone_map(shape_ids, nullptr, Hg, Wg), out, out_dtype, D,
-                 dim3((unsigned)(S / 512), B * H), stream);
+  const int64_t S_out = (int64_t)T * Hg * Wg;
+  launch_scatter(in_rows, S, S_out, zone_map(shape_ids, nullptr, Hg, Wg, GridBox{Tin, Hin, Win}), out, out_dtype, D,
+                 dim3((unsigned)(S_out / 512), B * H), stream);
   PRISM_LAUNCH_CHECK("prism_scatter_rows");
   return PRISM_OK;
 }

@@ -53,7 +53,7 @@ __device__ __forceinline__ void load_chan(const T* p, float* x) {
 template <int D, typename T>
 __global__ __launch_bounds__(kZoneThreads) void zone_stats_kernel(
     const T* __restrict__ v, int H, int64_t S, const uint8_t* __restrict__ valid,
-    int ZH, int ZW, int Hg, int Wg, float invH, float* __restrict__ packed,
+    int ZH, int ZW, GridBox box, float invH, float* __restrict__ packed,
     uint8_t* __restrict__ axis_valid) {
   constexpr int CPL = D / 64;
   __shared__ float sRC[8][8][D];  // row sums r[lt][lh][d], later col sums c[lt][lw][d]
@@ -65,7 +65,10 @@ __global__ __launch_bounds__(kZoneThreads) void zone_stats_kernel(
   const int tid = threadIdx.x;
   const int lt = tid >> 6, lane = tid & 63;
 
-  sValid[tid] = valid ? valid[token_of(z, tid, ZH, ZW, Hg, Wg)] : (uint8_t)1;
+  {
+    const int64_t tok = token_in(z, tid, ZH, ZW, box);
+    sValid[tid] = tok < 0 ? (uint8_t)0 : valid ? valid[tok] : (uint8_t)1;
+  }
   __syncthreads();
   if (tid < 25) {
     int cnt = 0;
@@ -92,12 +95,12 @@ __global__ __launch_bounds__(kZoneThreads) void zone_stats_kernel(
 #pragma unroll
     for (int lw = 0; lw < 8; ++lw) {
       const int lf = (lt * 8 + lh) * 8 + lw;
-      const int64_t tok = token_of(z, lf, ZH, ZW, Hg, Wg);
+      const int64_t tok = token_in(z, lf, ZH, ZW, box);
       const bool ok = sValid[lf] != 0;
       float acc[CPL];
 #pragma unroll
       for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
-      for (int h = 0; h < H; ++h) {
+      for (int h = 0; h < (tok < 0 ? 0 : H); ++h) {
         float x[CPL];
         load_chan<T, CPL>(v + ((int64_t)h * S + tok) * D + lane * CPL, x);
 #pragma unroll
@@ -173,16 +176,16 @@ __device__ __forceinline__ float masked_var8(const float* a, int stride, const u
 // One 64-lane workgroup per zone.
 template <typename T>
 __global__ __launch_bounds__(64) void audio_zone_kernel(
-    const T* __restrict__ norms, const uint8_t* __restrict__ valid, int ZH, int ZW, int Hg, int Wg,
+    const T* __restrict__ norms, const uint8_t* __restrict__ valid, int ZH, int ZW, GridBox box,
     float* __restrict__ abar, float* __restrict__ vhat) {
   __shared__ float sA[512];
   __shared__ uint8_t sV[512];
   __shared__ float sRow[8][8], sCol[8][8];
   const int z = blockIdx.x, lane = threadIdx.x;
   for (int lf = lane; lf < 512; lf += 64) {
-    const int64_t tok = token_of(z, lf, ZH, ZW, Hg, Wg);
-    sA[lf] = ldf(norms, sizeof(T) == 2 ? PRISM_BF16 : PRISM_F32, tok);
-    sV[lf] = valid ? valid[tok] : (uint8_t)1;
+    const int64_t tok = token_in(z, lf, ZH, ZW, box);
+    sA[lf] = tok < 0 ? 0.0f : ldf(norms, sizeof(T) == 2 ? PRISM_BF16 : PRISM_F32, tok);
+    sV[lf] = tok < 0 ? (uint8_t)0 : valid ? valid[tok] : (uint8_t)1;
   }
   __syncthreads();
   {
@@ -403,37 +406,43 @@ bool grid_ok(int T, int Hg, int Wg) { return T > 0 && Hg > 0 && Wg > 0 && T % 8 
 extern "C" {
 
 int prism_zone_stats(const void* v, int dtype, int H, int64_t S, int D, const uint8_t* valid, int T,
-                     int Hg, int Wg, float* packed, uint8_t* axis_valid, hipStream_t stream) {
+                     int Hg, int Wg, int Tin, int Hin, int Win, float* packed, uint8_t* axis_valid,
+                     hipStream_t stream) {
   PRISM_REQUIRE(v && packed && axis_valid, "prism_zone_stats: null pointer");
   PRISM_REQUIRE(grid_ok(T, Hg, Wg), "prism_zone_stats: grid (%d,%d,%d) must be multiples of 8", T, Hg, Wg);
-  PRISM_REQUIRE((int64_t)T * Hg * Wg == S, "prism_zone_stats: T*H*W != S");
+  PRISM_REQUIRE(box_ok(T, Hg, Wg, Tin, Hin, Win), "prism_zone_stats: input grid (%d,%d,%d) must fit the zone grid",
+                Tin, Hin, Win);
+  PRISM_REQUIRE((int64_t)Tin * Hin * Win == S, "prism_zone_stats: Tin*Hin*Win != S");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_zone_stats: head_dim %d unsupported (64, 128)", D);
   PRISM_REQUIRE(H >= 1, "prism_zone_stats: H must be >= 1");
   PRISM_REQUIRE(dtype == PRISM_F32 || dtype == PRISM_BF16, "prism_zone_stats: bad dtype");
   const int ZH = Hg / 8, ZW = Wg / 8, Nz = (T / 8) * ZH * ZW;
   const float invH = 1.0f / (float)H;
+  const GridBox box{Tin, Hin, Win};
   dim3 grid(Nz), block(kZoneThreads);
   if (dtype == PRISM_BF16) {
-    if (D == 128) zone_stats_kernel<128, uint16_t><<<grid, block, 0, stream>>>((const uint16_t*)v, H, S, valid, ZH, ZW, Hg, Wg, invH, packed, axis_valid);
-    else zone_stats_kernel<64, uint16_t><<<grid, block, 0, stream>>>((const uint16_t*)v, H, S, valid, ZH, ZW, Hg, Wg, invH, packed, axis_valid);
+    if (D == 128) zone_stats_kernel<128, uint16_t><<<grid, block, 0, stream>>>((const uint16_t*)v, H, S, valid, ZH, ZW, box, invH, packed, axis_valid);
+    else zone_stats_kernel<64, uint16_t><<<grid, block, 0, stream>>>((const uint16_t*)v, H, S, valid, ZH, ZW, box, invH, packed, axis_valid);
   } else {
-    if (D == 128) zone_stats_kernel<128, float><<<grid, block, 0, stream>>>((const float*)v, H, S, valid, ZH, ZW, Hg, Wg, invH, packed, axis_valid);
-    else zone_stats_kernel<64, float><<<grid, block, 0, stream>>>((const float*)v, H, S, valid, ZH, ZW, Hg, Wg, invH, packed, axis_valid);
+    if (D == 128) zone_stats_kernel<128, float><<<grid, block, 0, stream>>>((const float*)v, H, S, valid, ZH, ZW, box, invH, packed, axis_valid);
+    else zone_stats_kernel<64, float><<<grid, block, 0, stream>>>((const float*)v, H, S, valid, ZH, ZW, box, invH, packed, axis_valid);
   }
   PRISM_LAUNCH_CHECK("prism_zone_stats");
   return PRISM_OK;
 }
 
-int prism_audio_zone_stats(const void* norms, int dtype, const uint8_t* valid, int T, int Hg, int Wg,
-                           float* abar, float* vhat, hipStream_t stream) {
+int prism_audio_zone_stats(const void* norms, int dtype, const uint8_t* valid, int T, int Hg, int Wg, int Tin,
+                           int Hin, int Win, float* abar, float* vhat, hipStream_t stream) {
   PRISM_REQUIRE(norms && abar && vhat, "prism_audio_zone_stats: null pointer");
   PRISM_REQUIRE(grid_ok(T, Hg, Wg), "prism_audio_zone_stats: grid must be multiples of 8");
+  PRISM_REQUIRE(box_ok(T, Hg, Wg, Tin, Hin, Win), "prism_audio_zone_stats: input grid must fit the zone grid");
+  const GridBox box{Tin, Hin, Win};
   PRISM_REQUIRE(dtype == PRISM_F32 || dtype == PRISM_BF16, "prism_audio_zone_stats: bad dtype");
   const int ZH = Hg / 8, ZW = Wg / 8, Nz = (T / 8) * ZH * ZW;
   if (dtype == PRISM_BF16)
-    audio_zone_kernel<uint16_t><<<Nz, 64, 0, stream>>>((const uint16_t*)norms, valid, ZH, ZW, Hg, Wg, abar, vhat);
+    audio_zone_kernel<uint16_t><<<Nz, 64, 0, stream>>>((const uint16_t*)norms, valid, ZH, ZW, box, abar, vhat);
   else
-    audio_zone_kernel<float><<<Nz, 64, 0, stream>>>((const float*)norms, valid, ZH, ZW, Hg, Wg, abar, vhat);
+    audio_zone_kernel<float><<<Nz, 64, 0, stream>>>((const float*)norms, valid, ZH, ZW, box, abar, vhat);
   PRISM_LAUNCH_CHECK("prism_audio_zone_stats");
   return PRISM_OK;
 }

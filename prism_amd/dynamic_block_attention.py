@@ -52,17 +52,18 @@ class _Plan:
     """Everything the attention kernels need for one call, built under no_grad."""
 
     def __init__(self, q, k, v, grid, shape_ids, valid_mask, sparsity, cdf_threshold, sm_scale,
-                 compute_padded_queries=False):
-        B, H, S, D = q.shape
-        self.B, self.H, self.S, self.D = B, H, S, D
-        self.grid = grid
-        self.lay = ops.ZoneLayout(shape_ids, grid)
+                 compute_padded_queries=False, box=None):
+        B, H, _, D = q.shape
+        self.lay = ops.ZoneLayout(shape_ids, grid, box)
         lay = self.lay
+        self.B, self.H, self.S, self.D = B, H, lay.S, D
+        self.grid = grid
         gq = ops.gather_pool(q, lay, valid_mask, rows=True, pool=True, counts=True)
         gk = ops.gather_pool(k, lay, valid_mask, rows=True, pool=True)
         gv = ops.gather_pool(v, lay, valid_mask, rows=True)
         self.q_re, self.k_re, self.v_re = gq["rows"], gk["rows"], gv["rows"]
-        masked = valid_mask is not None
+        # zone-grid positions outside the input grid are invalid tokens
+        masked = valid_mask is not None or lay.padded
         self.kv_valid = gq["valid_re"] if masked else None
         self.block_count = gq["block_count"]
         self.tile_count = gq["tile_count"]
@@ -128,12 +129,19 @@ class _DynBSA(torch.autograd.Function):
 
 def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold=None, audio_token_norms=None,
                  valid_mask=None, lambda_a=0.5, tau_128=0.15, lambda_128=1.0, shape_ids=None,
-                 compute_padded_queries=False) -> _Plan:
+                 compute_padded_queries=False, input_grid=None) -> _Plan:
     """Steps (1)-(5) of flash_attn_bsa_3d_dynamic: shape ids, layout, pooled
-    scores, selection and tile lists (no attention)."""
+    scores, selection and tile lists (no attention).
+
+    With input_grid (Ti, Hi, Wi) inside grid_padded, q, k, v, the audio norms
+    and valid_mask cover the input grid only (S = Ti Hi Wi): the zero padding
+    and padding mask of wan_video_dit.py:342-400 are applied inside the
+    kernels, with results identical to padding first."""
     B, Hn, S, D = q.shape
     T, H, W = grid_padded
-    assert T * H * W == S
+    box = tuple(input_grid) if input_grid is not None else (T, H, W)
+    assert box[0] * box[1] * box[2] == S
+    assert all(0 < b <= g for b, g in zip(box, (T, H, W)))
     assert T % ZONE_SIZE == 0 and H % ZONE_SIZE == 0 and W % ZONE_SIZE == 0
     if sparsity is None and cdf_threshold is None:
         raise ValueError("Either sparsity or cdf_threshold must be provided")
@@ -143,9 +151,9 @@ def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold
     with torch.no_grad():
         if shape_ids is None:
             shape_ids = _gradient_and_shapes(v.detach(), audio_token_norms, (T, H, W), method, lambda_a, tau_128,
-                                             lambda_128, valid_mask)[2]
+                                             lambda_128, valid_mask, box)[2]
         return _Plan(q.detach(), k.detach(), v.detach(), (T, H, W), shape_ids, valid_mask, sparsity, cdf_threshold,
-                     sm_scale, compute_padded_queries)
+                     sm_scale, compute_padded_queries, box)
 
 
 def flash_attn_bsa_3d_dynamic(
@@ -165,6 +173,7 @@ def flash_attn_bsa_3d_dynamic(
     shape_ids: Optional[torch.Tensor] = None,
     return_shape_ids: bool = False,
     compute_padded_queries: bool = False,
+    input_grid: Optional[Tuple[int, int, int]] = None,
 ):
     """Dynamic-block-shape BSA for video self-attention; returns [B,H,S,D] in
     THW order (dynamic_block_attention.py:194-332).  q, k, v: [B,H,S,D] THW
@@ -177,11 +186,18 @@ def flash_attn_bsa_3d_dynamic(
     all blocks); here their output is 0 unless compute_padded_queries=True.
     Outputs at valid positions and all gradients of valid tokens are the same
     either way when the incoming gradient is 0 at padded positions (as the
-    caller's unpadding makes it)."""
+    caller's unpadding makes it).
+
+    input_grid (not in the reference's signature) takes the caller's unpadded
+    grid: q, k, v [B,H,Ti*Hi*Wi,D], audio norms and valid_mask then cover it,
+    grid_padded is its round-up to multiples of 8, and the output (and the
+    gradients) come back unpadded.  This is the padding, valid mask and
+    unpadding of wan_video_dit.py:342-431 done inside the gather and scatter
+    kernels; the result equals padding first and slicing after, bit for bit."""
     plan = plan_dynamic(q, k, v, grid_padded, method=method, sparsity=sparsity, cdf_threshold=cdf_threshold,
                         audio_token_norms=audio_token_norms, valid_mask=valid_mask, lambda_a=lambda_a,
                         tau_128=tau_128, lambda_128=lambda_128, shape_ids=shape_ids,
-                        compute_padded_queries=compute_padded_queries)
+                        compute_padded_queries=compute_padded_queries, input_grid=input_grid)
     sm_scale = 1.0 / (q.shape[-1] ** 0.5)
     out = _DynBSA.apply(q, k, v, plan, sm_scale)
     if return_shape_ids:

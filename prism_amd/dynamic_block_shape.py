@@ -94,15 +94,17 @@ def compute_audio_directional(audio_norms_thw: Optional[torch.Tensor], ZT: int, 
     return a_norm, vhat[:, 0].contiguous(), vhat[:, 1].contiguous(), vhat[:, 2].contiguous()
 
 
-def _gradient_and_shapes(v, audio_norms_thw, grid, method, lambda_a, tau_128, lambda_128, valid_mask_thw):
+def _gradient_and_shapes(v, audio_norms_thw, grid, method, lambda_a, tau_128, lambda_128, valid_mask_thw, box=None):
+    """Shape ids of the zone grid `grid`; v, the audio norms and the mask cover
+    the input grid `box` inside it (default: grid itself)."""
     if method not in _METHODS:
         raise ValueError(f"unknown dynamic-block method: {method!r}")
     D = v.shape[-1]
-    packed, av = ops.zone_stats(v, grid, valid_mask_thw)
+    packed, av = ops.zone_stats(v, grid, valid_mask_thw, box)
     rho_raw, aniso = ops.zone_gradient(packed, av, D)
     abar = vhat = None
     if audio_norms_thw is not None:
-        abar, vhat = ops.audio_zone_stats(audio_norms_thw.reshape(-1), grid, valid_mask_thw)
+        abar, vhat = ops.audio_zone_stats(audio_norms_thw.reshape(-1), grid, valid_mask_thw, box)
     return ops.zone_shapes(rho_raw, aniso, abar, vhat, method, lambda_a, tau_128, lambda_128)
 
 

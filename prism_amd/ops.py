@@ -84,29 +84,35 @@ def _u8(valid: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
 
 
 # ------------------------------------------------------------------ statistics
-def zone_stats(v: torch.Tensor, grid, valid: Optional[torch.Tensor] = None):
-    """[B,H,S,D] THW -> packed [Nz, 25D] fp32, axis_valid [Nz, 24] uint8."""
+def zone_stats(v: torch.Tensor, grid, valid: Optional[torch.Tensor] = None, box=None):
+    """[B,H,S,D] THW -> packed [Nz, 25D] fp32, axis_valid [Nz, 24] uint8.
+    grid is the zone grid (multiples of 8); box the input grid inside it that
+    v and valid cover (default: the zone grid itself)."""
     _cuda(v, valid)
     v = v.contiguous()
     B, H, S, D = v.shape
     T, Hg, Wg = _grid(grid)
+    Ti, Hi, Wi = _grid(box if box is not None else grid)
     Nz = (T // 8) * (Hg // 8) * (Wg // 8)
     packed = torch.empty((Nz, 25 * D), device=v.device, dtype=torch.float32)
     av = torch.empty((Nz, 24), device=v.device, dtype=torch.uint8)
     vm = _u8(valid)
-    _call("prism_zone_stats", _p(v), _code(v), H, S, D, _p(vm), T, Hg, Wg, _p(packed), _p(av), _stream())
+    _call("prism_zone_stats", _p(v), _code(v), H, S, D, _p(vm), T, Hg, Wg, Ti, Hi, Wi, _p(packed), _p(av),
+          _stream())
     return packed, av
 
 
-def audio_zone_stats(norms: torch.Tensor, grid, valid: Optional[torch.Tensor] = None):
+def audio_zone_stats(norms: torch.Tensor, grid, valid: Optional[torch.Tensor] = None, box=None):
     _cuda(norms, valid)
     norms = norms.contiguous()
     T, Hg, Wg = _grid(grid)
+    Ti, Hi, Wi = _grid(box if box is not None else grid)
     Nz = (T // 8) * (Hg // 8) * (Wg // 8)
     abar = torch.empty(Nz, device=norms.device, dtype=torch.float32)
     vhat = torch.empty((Nz, 3), device=norms.device, dtype=torch.float32)
     vm = _u8(valid)
-    _call("prism_audio_zone_stats", _p(norms), _code(norms), _p(vm), T, Hg, Wg, _p(abar), _p(vhat), _stream())
+    _call("prism_audio_zone_stats", _p(norms), _code(norms), _p(vm), T, Hg, Wg, Ti, Hi, Wi, _p(abar), _p(vhat),
+          _stream())
     return abar, vhat
 
 
@@ -147,15 +153,25 @@ def a2v_norms(residual: torch.Tensor) -> torch.Tensor:
 
 # ------------------------------------------------------------------ geometry
 class ZoneLayout:
-    """Per-call block/tile bookkeeping for one set of shape ids."""
+    """Per-call block/tile bookkeeping for one set of shape ids.
 
-    def __init__(self, shape_ids: torch.Tensor, grid):
+    grid is the zone grid (multiples of 8); box is the input grid inside it
+    (default: the zone grid).  THW tensors of this layout hold S_in =
+    prod(box) tokens per head, tile-order tensors S = prod(grid) rows; grid
+    positions outside the box are padding (zero, invalid)."""
+
+    def __init__(self, shape_ids: torch.Tensor, grid, box=None):
         _cuda(shape_ids)
         self.grid = _grid(grid)
+        self.box = _grid(box) if box is not None else self.grid
         T, Hg, Wg = self.grid
+        if not all(0 < b <= g for b, g in zip(self.box, self.grid)):
+            raise ValueError(f"input grid {self.box} must fit the zone grid {self.grid}")
+        self.padded = self.box != self.grid
         self.Nz = (T // 8) * (Hg // 8) * (Wg // 8)
         self.Nt = self.Nz * 8
         self.S = T * Hg * Wg
+        self.S_in = self.box[0] * self.box[1] * self.box[2]
         self.shape_ids = shape_ids.contiguous().to(torch.int64)
         dev = shape_ids.device
         self.block_offset = torch.empty(self.Nz + 1, device=dev, dtype=torch.int32)
@@ -180,12 +196,17 @@ def rearrange_index(shape_ids: torch.Tensor, grid):
 
 def gather_pool(x: torch.Tensor, lay: ZoneLayout, valid: Optional[torch.Tensor] = None, *, rows: bool = True,
                 pool: bool = False, counts: bool = False, dot_with: Optional[torch.Tensor] = None):
-    """Rearrange x [B,H,S,D] (THW) into tile order (bf16 rows) and optionally
-    pool block means / counts / rowdot with dot_with.  Returns a dict."""
+    """Rearrange x [B,H,S_in,D] (THW order of lay.box) into tile order (bf16
+    rows [B,H,S,D] over lay.grid, padding rows zero) and optionally pool block
+    means / counts / rowdot with dot_with.  Returns a dict."""
     _cuda(x, valid, dot_with)
     x = x.contiguous()
-    B, H, S, D = x.shape
+    B, H, S_in, D = x.shape
+    if S_in != lay.S_in:
+        raise ValueError(f"gather_pool: x has {S_in} tokens, the layout's input grid {lay.box} holds {lay.S_in}")
+    S = lay.S
     T, Hg, Wg = lay.grid
+    Ti, Hi, Wi = lay.box
     dev = x.device
     out = {}
     out["rows"] = torch.empty((B, H, S, D), device=dev, dtype=torch.bfloat16) if rows else None
@@ -199,25 +220,29 @@ def gather_pool(x: torch.Tensor, lay: ZoneLayout, valid: Optional[torch.Tensor] 
     rowdot = None
     if dot_with is not None:
         dot_with = dot_with.contiguous()
-        if dot_with.dtype != torch.bfloat16 or dot_with.shape != x.shape:
-            raise ValueError("gather_pool: dot_with must be bf16 of x's shape (tile order)")
+        if dot_with.dtype != torch.bfloat16 or dot_with.shape != (B, H, S, D):
+            raise ValueError("gather_pool: dot_with must be bf16 [B,H,S,D] in tile order")
         rowdot = torch.empty((B, H, S), device=dev, dtype=torch.float32)
     out["rowdot"] = rowdot
     vm = _u8(valid)
-    _call("prism_gather_pool", _p(x), _code(x), B, H, S, D, _p(vm), _p(lay.shape_ids), _p(lay.block_offset),
-              T, Hg, Wg, lay.N_b, _p(out["rows"]), _p(out["block_mean"]), _p(out["block_count"]),
+    _call("prism_gather_pool", _p(x), _code(x), B, H, S_in, D, _p(vm), _p(lay.shape_ids), _p(lay.block_offset),
+              T, Hg, Wg, Ti, Hi, Wi, lay.N_b, _p(out["rows"]), _p(out["block_mean"]), _p(out["block_count"]),
               _p(out["tile_count"]), _p(out["valid_re"]), _p(dot_with), _p(rowdot), _stream())
     return out
 
 
 def scatter_rows(rows: torch.Tensor, lay: ZoneLayout, out_dtype: torch.dtype) -> torch.Tensor:
+    """Tile-order bf16 rows [B,H,S,D] -> THW order [B,H,S_in,D] of lay.box."""
     _cuda(rows)
     rows = rows.contiguous()
     B, H, S, D = rows.shape
+    if S != lay.S:
+        raise ValueError(f"scatter_rows: {S} rows, the layout holds {lay.S}")
     T, Hg, Wg = lay.grid
-    out = torch.empty((B, H, S, D), device=rows.device, dtype=out_dtype)
-    _call("prism_scatter_rows", _p(rows), B, H, S, D, _p(lay.shape_ids), T, Hg, Wg, _p(out), _code(out),
-              _stream())
+    Ti, Hi, Wi = lay.box
+    out = torch.empty((B, H, lay.S_in, D), device=rows.device, dtype=out_dtype)
+    _call("prism_scatter_rows", _p(rows), B, H, lay.S_in, D, _p(lay.shape_ids), T, Hg, Wg, Ti, Hi, Wi, _p(out),
+          _code(out), _stream())
     return out
 
 

@@ -70,7 +70,12 @@ def test_invalid_arguments_raise_without_gpu():
     """Argument validation happens on the host before any launch."""
     from prism_amd import _lib
     with pytest.raises(ValueError, match="multiples of 8"):
-        _lib.call("prism_zone_stats", 1, 0, 1, 64, 64, None, 4, 4, 4, 1, 1, None)
+        _lib.call("prism_zone_stats", 1, 0, 1, 64, 64, None, 4, 4, 4, 4, 4, 4, 1, 1, None)
+    with pytest.raises(ValueError, match="must fit the zone grid"):
+        _lib.call("prism_gather_pool", 1, 0, 1, 1, 9 * 8 * 8, 64, None, 1, 1, 8, 8, 8, 9, 8, 8, 0,
+                  None, None, None, None, None, None, None, None)
+    with pytest.raises(ValueError, match="Tin\\*Hin\\*Win != S"):
+        _lib.call("prism_scatter_rows", 1, 1, 1, 500, 64, 1, 8, 8, 8, 7, 8, 8, 1, 0, None)
     with pytest.raises(ValueError, match="null pointer"):
         _lib.call("prism_bsa_fwd", None, None, None, 1, 128, 128, 64, None, None, None, None, None, 0.1, None, None,
                   None)
@@ -85,4 +90,4 @@ def test_invalid_arguments_raise_without_gpu():
                   None, None, None, None, None, None, None, None)
     with pytest.raises(ValueError, match="multiple of the chunk|multiples of the chunk"):
         _lib.call("prism_chunk_scatter_rows", 1, 1, 1, 64, 4, 4, 4, 4, 4, 6, 4, 4, 4, 128, 1, 1, None)
-    assert _lib.load().prism_abi_version() == 4
+    assert _lib.load().prism_abi_version() == 5

@@ -175,6 +175,99 @@ def test_adapter_pads_caches_and_unpads():
     assert torch.equal(att._dyn_shape_cache[2], select_ids(v2, gp, pad, npad))
 
 
+def _padder(B, H, grid, gp, D):
+    (T, Hg, Wg), (Tp, Hp, Wp) = grid, gp
+    def pad(t):
+        if t.dim() == 1:
+            return torch.nn.functional.pad(t.view(T, Hg, Wg), (0, Wp - Wg, 0, Hp - Hg, 0, Tp - T)).reshape(-1)
+        return torch.nn.functional.pad(t.view(B, H, T, Hg, Wg, D),
+                                       (0, 0, 0, Wp - Wg, 0, Hp - Hg, 0, Tp - T)).reshape(B, H, -1, D)
+    return pad
+
+
+@pytest.mark.parametrize("grid,D,dtype", [((5, 12, 20), 128, torch.bfloat16), ((8, 9, 16), 64, torch.float32),
+                                          ((3, 8, 8), 128, torch.float32)])
+def test_input_grid_box_kernels_equal_padding(grid, D, dtype):
+    """Every kernel of the dynamic path that reads THW tensors, given the
+    unpadded input grid, equals the same kernel over the zero-padded zone grid
+    with the padding valid mask (wan_video_dit.py:342-400), bit for bit: zone
+    statistics, audio statistics, gather + pooling + counts + rowdot, and the
+    scatter back (with the slice of :429-431).  Also with a caller mask over
+    the input grid."""
+    from prism_amd import ops, select_zone_shapes, valid_mask_for
+    from prism_amd.adapter import padded_grid
+    rng = np.random.default_rng(31)
+    B, H = 2, 3
+    gp, _ = padded_grid(grid)
+    S = int(np.prod(grid))
+    say("box kernels", grid, D, dtype)
+    pad = _padder(B, H, grid, gp, D)
+    x = torch.from_numpy(rng.standard_normal((B, H, S, D)).astype(np.float32)).to("cuda").to(dtype)
+    norms = torch.from_numpy(rng.random(S).astype(np.float32)).to("cuda").to(dtype)
+    vpad = valid_mask_for(grid, "cuda")
+    for own in (None, torch.from_numpy(rng.random(S) > 0.2).to("cuda")):
+        vm_p = vpad if own is None else (vpad & pad(own.to(torch.uint8)).bool())
+        p_b, av_b = ops.zone_stats(x, gp, own, box=grid)
+        p_p, av_p = ops.zone_stats(pad(x), gp, vm_p)
+        assert bits_equal(host(p_b), host(p_p)) and torch.equal(av_b, av_p)
+        a_b, vh_b = ops.audio_zone_stats(norms, gp, own, box=grid)
+        a_p, vh_p = ops.audio_zone_stats(pad(norms), gp, vm_p)
+        assert bits_equal(host(a_b), host(a_p)) and bits_equal(host(vh_b), host(vh_p))
+        sid = select_zone_shapes(pad(x), pad(norms), gp, "ivpq", valid_mask_thw=vm_p)
+        lay_b, lay_p = ops.ZoneLayout(sid, gp, box=grid), ops.ZoneLayout(sid, gp)
+        assert lay_b.padded and lay_b.S == lay_p.S and lay_b.N_b == lay_p.N_b
+        g_b = ops.gather_pool(x, lay_b, own, rows=True, pool=True, counts=True)
+        g_p = ops.gather_pool(pad(x), lay_p, vm_p, rows=True, pool=True, counts=True)
+        for key in ("rows", "block_count", "tile_count", "valid_re"):
+            assert torch.equal(g_b[key], g_p[key]), key
+        assert bits_equal(host(g_b["block_mean"]), host(g_p["block_mean"]))
+        d_b = ops.gather_pool(x, lay_b, None, rows=False, dot_with=g_p["rows"])["rowdot"]
+        d_p = ops.gather_pool(pad(x), lay_p, None, rows=False, dot_with=g_p["rows"])["rowdot"]
+        assert bits_equal(host(d_b), host(d_p))
+        o_b = ops.scatter_rows(g_p["rows"], lay_b, dtype)
+        o_p = ops.scatter_rows(g_p["rows"], lay_p, dtype)
+        assert o_b.shape == (B, H, S, D)
+        Tp, Hp, Wp = gp
+        T, Hg, Wg = grid
+        assert torch.equal(o_b, o_p.view(B, H, Tp, Hp, Wp, D)[:, :, :T, :Hg, :Wg].reshape(B, H, S, D))
+        assert torch.equal(o_b, x.to(torch.bfloat16).to(dtype))  # gather then scatter is the identity
+    with pytest.raises(ValueError, match="tokens"):
+        ops.gather_pool(pad(x), ops.ZoneLayout(sid, gp, box=grid), None)
+
+
+@pytest.mark.parametrize("grid,cpq", [((5, 12, 20), False), ((6, 16, 13), True)])
+def test_input_grid_fwd_bwd_equal_padding(grid, cpq):
+    """flash_attn_bsa_3d_dynamic over the unpadded grid (input_grid) equals the
+    reference caller's flow (pad q, k, v and the audio norms, pass the valid
+    mask, slice the output) bit for bit, output and the gradients of q, k, v."""
+    from prism_amd import flash_attn_bsa_3d_dynamic, valid_mask_for
+    from prism_amd.adapter import padded_grid
+    rng = np.random.default_rng(37)
+    B, H, D = 1, 2, 128
+    gp, _ = padded_grid(grid)
+    S = int(np.prod(grid))
+    say("box fwd/bwd", grid, cpq)
+    pad = _padder(B, H, grid, gp, D)
+    base = [torch.from_numpy(rng.standard_normal((B, H, S, D)).astype(np.float32)).to("cuda").to(torch.bfloat16)
+            for _ in range(3)]
+    norms = torch.from_numpy(rng.random(S).astype(np.float32)).to("cuda").to(torch.bfloat16)
+    do = torch.from_numpy(rng.standard_normal((B, H, S, D)).astype(np.float32)).to("cuda").to(torch.bfloat16)
+    kw = dict(method="ivpq", sparsity=0.6, cdf_threshold=0.8, return_shape_ids=True, compute_padded_queries=cpq)
+    q1, k1, v1 = (t.clone().requires_grad_(True) for t in base)
+    out1, sid1 = flash_attn_bsa_3d_dynamic(q1, k1, v1, gp, audio_token_norms=norms, input_grid=grid, **kw)
+    out1.backward(do)
+    q2, k2, v2 = (t.clone().requires_grad_(True) for t in base)
+    out2, sid2 = flash_attn_bsa_3d_dynamic(pad(q2), pad(k2), pad(v2), gp, audio_token_norms=pad(norms),
+                                           valid_mask=valid_mask_for(grid, "cuda"), **kw)
+    T, Hg, Wg = grid
+    out2 = out2.view(B, H, *gp, D)[:, :, :T, :Hg, :Wg].reshape(B, H, S, D)
+    out2.backward(do)
+    assert torch.equal(sid1, sid2)
+    assert torch.equal(out1, out2)
+    for a, b in ((q1, q2), (k1, k2), (v1, v2)):
+        assert torch.equal(a.grad, b.grad)
+
+
 def select_ids(v, gp, pad, npad):
     from prism_amd import select_zone_shapes, valid_mask_for
     return select_zone_shapes(pad(v), npad, gp, "ivpq", valid_mask_thw=valid_mask_for((5, 12, 20), "cuda"))
