@@ -327,6 +327,9 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
         sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sK + 32 * kh * P, s), qf[s], sacc[kh], 0, 0, 0);
         pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sV + 32 * kh * P, s), df[s], pacc[kh], 0, 0, 0);
       }
+    // exponentials, dS and dQ at raised wave priority (as in the forward
+    // kernel; measured 1% faster; the same in dK/dV was 4% slower)
+    __builtin_amdgcn_s_setprio(1);
     // element (kh, r): key 32kh + 8(r >> 2) + 4g + (r & 3), query = this lane's column
     if (e & 4) {
       const uint64_t mm = sload_u64(a.tmask + (e >> 3)) >> (4 * g);
@@ -352,6 +355,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
       for (int dt = 0; dt < NDT; ++dt)
         dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sK, tt, dt), sb, dq[dt], 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
   }
 
   uint16_t* dqr = a.dq + qoff + qrow * D;
