@@ -19,9 +19,10 @@
 //             w_j = e_j / sum;
 //   cdf     = exact fixed-point prefix sums of floor(w 2^60) in (w desc, index asc)
 //             order; "cdf < p" <=> prefix < thr (thr from the host).
-// The selection never sorts: the crossing element is found by bisection on
-// the fp32 bit pattern of w (order-preserving for w >= 0) with exact integer
-// sums, so the result does not depend on thread order.
+// The selection never sorts: the crossing element is found by a radix search
+// (four 8-bit digits, LDS histograms) on the fp32 bit pattern of w
+// (order-preserving for w >= 0) with exact integer sums, so the result does
+// not depend on thread order.
 #include "common.h"
 
 namespace {
@@ -149,6 +150,62 @@ __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, SelShared& s
   return before + incl - v;
 }
 
+__device__ __forceinline__ uint64_t block_incl_scan_u64(uint64_t v, SelShared& sh) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t lo = __shfl_up((uint32_t)v, off, 64);
+    const uint32_t hi = __shfl_up((uint32_t)(v >> 32), off, 64);
+    if (lane >= off) v += ((uint64_t)hi << 32) | lo;
+  }
+  if (lane == 63) sh.u64[wid] = v;
+  __syncthreads();
+  uint64_t before = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) before += (w < wid) ? sh.u64[w] : 0ull;
+  __syncthreads();
+  return before + v;
+}
+
+// Radix search over the 32-bit keys of one row (4 digits of 8 bits, most
+// significant first): the largest v with S(v) >= thr, where S(v) is the sum
+// of wt over present elements with key >= v (wt = W[e], or 1 to count), for
+// 0 < thr <= S(0).  *above = S(v + 1), the weight strictly above v.  The
+// sums are exact integers, so v is the same as a bisection on S would find.
+// Per digit: an LDS histogram of wt over the elements that match the digits
+// found so far, a suffix scan over the 256 bins, and the largest digit whose
+// suffix reaches thr.
+template <int EPT, bool WEIGHTED>
+__device__ __forceinline__ uint32_t radix_search(const uint32_t* key, const uint64_t* W, uint64_t present, uint64_t thr,
+                                                 uint64_t* above, SelShared& sh, unsigned long long* hist) {
+  const int tid = threadIdx.x;
+  uint32_t prefix = 0;
+  uint64_t acc = 0;  // weight of keys whose decided digits exceed the prefix
+#pragma unroll 1
+  for (int level = 0; level < 4; ++level) {
+    const int shift = 24 - 8 * level;
+    const uint32_t hmask = level == 0 ? 0u : (0xffffffffu << (shift + 8));
+    hist[tid] = 0ull;  // kSelThreads == 256 bins
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if (((present >> e) & 1) && (key[e] & hmask) == prefix)
+        atomicAdd(&hist[(key[e] >> shift) & 255u], WEIGHTED ? (unsigned long long)W[e] : 1ull);
+    __syncthreads();
+    // thread t takes bin 255 - t, so its inclusive scan is the weight of the
+    // digits >= 255 - t; the first thread whose total reaches thr owns d*
+    const uint64_t h = hist[255 - tid];
+    const uint64_t incl = block_incl_scan_u64(h, sh);
+    const uint32_t tstar = block_sum_u32(acc + incl >= thr ? 0u : 1u, sh);
+    if ((uint32_t)tid == tstar) sh.u64[0] = incl - h;  // weight of the digits > d*
+    __syncthreads();
+    acc += sh.u64[0];
+    __syncthreads();
+    prefix |= (255u - tstar) << shift;
+  }
+  *above = acc;
+  return prefix;
+}
+
 struct SelArgs {
   const float* scores;            // [rows, N]
   int64_t rows, N;
@@ -166,10 +223,12 @@ struct SelArgs {
   int32_t* nsel;                  // [rows] or null
 };
 
-// One workgroup per row; element j lives in thread j % 256, slot j / 256.
+// One workgroup per row; element j lives in thread j / EPT, slot j % EPT.
 template <int EPT>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
+  static_assert(kSelThreads == 256, "one radix bin per thread");
   __shared__ SelShared sh;
+  __shared__ unsigned long long hist[256];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const float* s = a.scores + row * a.N;
@@ -185,7 +244,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   if (a.mode == 0) {
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const int64_t j = (int64_t)e * kSelThreads + tid;
+      const int64_t j = (int64_t)tid * EPT + e;
       key[e] = 0;
       W[e] = 0;
       if (j < N) {
@@ -200,7 +259,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     float m = -__uint_as_float(0x7f800000u);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const int64_t j = (int64_t)e * kSelThreads + tid;
+      const int64_t j = (int64_t)tid * EPT + e;
       x[e] = m;
       if (j < N) {
         x[e] = s[j] * a.scale;
@@ -244,13 +303,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
       uint32_t vc = 0;
       uint64_t jt = 0;
       if (G(0) >= a.thr) {
-        uint32_t lo = 0, hi = 0x3f800001u;  // G(lo) >= thr > G(hi)
-        while (hi - lo > 1) {
-          const uint32_t mid = lo + (hi - lo) / 2;
-          if (G(mid) >= a.thr) lo = mid; else hi = mid;
-        }
-        vc = lo;
-        const uint64_t A = G(vc + 1);
+        // crossing value vc: G(vc) >= thr > G(vc + 1) = A
+        uint64_t A;
+        vc = radix_search<EPT, true>(key, W, present, a.thr, &A, sh, hist);
         const uint32_t ngt = Nge(vc + 1);
         const uint64_t Wv = fixp(__uint_as_float(vc), 60);
         jt = (a.thr - A - 1) / Wv;  // smallest j with A + (j+1) Wv >= thr
@@ -269,57 +324,59 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     }
   }
 
-  if (eff > 0) {  // count search: largest v with #(key >= v) >= eff
-    auto Nge = [&](uint64_t v) {
-      uint32_t t = 0;
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) t += (((present >> e) & 1) && (uint64_t)key[e] >= v) ? 1u : 0u;
-      return block_sum_u32(t, sh);
-    };
-    uint64_t lo = 0, hi = 0x100000000ull;
-    while (hi - lo > 1) {
-      const uint64_t mid = lo + (hi - lo) / 2;
-      if ((int64_t)Nge(mid) >= eff) lo = mid; else hi = mid;
-    }
-    v_e = (uint32_t)lo;
-    need = (uint64_t)eff - Nge(lo + 1);
+  if (eff > 0) {  // count search: largest v with #(key >= v) >= eff (eff <= #present)
+    uint64_t above;
+    v_e = radix_search<EPT, false>(key, W, present, (uint64_t)eff, &above, sh, hist);
+    need = (uint64_t)eff - above;
   } else {
     eff = -eff;
   }
 
-  // emit selected blocks in ascending index order, expanded to tiles
-  uint32_t tie_carry = 0, out_carry = 0;
+  // emit selected blocks in ascending index order, expanded to tiles.  Thread
+  // t owns blocks [t EPT, t EPT + EPT), so one scan of per-thread tie counts
+  // ranks the ties and one scan of per-thread output counts places the lists.
   int32_t* trow = a.tiles + row * a.tcap;
   int32_t* brow = a.sel_blocks ? a.sel_blocks + row * a.bcap : nullptr;
+  const int64_t j0 = (int64_t)tid * EPT;
+  uint32_t nties = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) nties += (eff > 0 && ((present >> e) & 1) && key[e] == v_e) ? 1u : 0u;
+  uint32_t tot;
+  uint32_t rank = block_excl_scan_u32(nties, sh, &tot);
+  uint64_t selm = 0;  // bit e: block j0 + e is selected
+  uint32_t packed = 0;  // tiles | blocks << 16 of this thread
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
-    const int64_t j = (int64_t)e * kSelThreads + tid;
     const bool pres = (present >> e) & 1;
     const bool tie = eff > 0 && pres && key[e] == v_e;
-    uint32_t tot;
-    const uint32_t rank = tie_carry + block_excl_scan_u32(tie ? 1u : 0u, sh, &tot);
-    tie_carry += tot;
     const bool sel = eff > 0 && pres && (key[e] > v_e || (tie && rank < need));
-    uint32_t nt = 0;
-    int32_t t0 = 0, t1 = 0;
+    rank += tie ? 1u : 0u;
     if (sel) {
-      t0 = a.block_first_tile[j];
-      t1 = a.block_first_tile[j + 1];
+      const int32_t t0 = a.block_first_tile[j0 + e], t1 = a.block_first_tile[j0 + e + 1];
+      uint32_t nt = 0;
       for (int32_t t = t0; t < t1; ++t) nt += (a.tile_count == nullptr || a.tile_count[t] > 0) ? 1u : 0u;
+      packed += nt | (1u << 16);
+      selm |= 1ull << e;
     }
-    const uint32_t packed = nt | ((sel ? 1u : 0u) << 16);
-    const uint32_t pos = out_carry + block_excl_scan_u32(packed, sh, &tot);
-    out_carry += tot;
-    if (sel) {
-      uint32_t p = pos & 0xffffu;
-      for (int32_t t = t0; t < t1 && p < a.tcap; ++t)
-        if (a.tile_count == nullptr || a.tile_count[t] > 0) trow[p++] = t;
-      if (brow) brow[pos >> 16] = (int32_t)j;
+  }
+  const uint32_t pos = block_excl_scan_u32(packed, sh, &tot);
+  uint32_t p = pos & 0xffffu, q = pos >> 16;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    if ((selm >> e) & 1) {
+      const int32_t t0 = a.block_first_tile[j0 + e], t1 = a.block_first_tile[j0 + e + 1];
+      for (int32_t t = t0; t < t1; ++t)
+        if (a.tile_count == nullptr || a.tile_count[t] > 0) {
+          if (p < a.tcap) trow[p] = t;
+          ++p;
+        }
+      if (brow) brow[q] = (int32_t)(j0 + e);
+      ++q;
     }
   }
   if (tid == 0) {
-    a.ntiles[row] = (int32_t)(out_carry & 0xffffu);
-    if (a.nsel) a.nsel[row] = (int32_t)(out_carry >> 16);
+    a.ntiles[row] = (int32_t)(tot & 0xffffu);
+    if (a.nsel) a.nsel[row] = (int32_t)(tot >> 16);
   }
 }
 
