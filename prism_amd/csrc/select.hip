@@ -477,6 +477,7 @@ int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, i
   const int64_t need = (N + kSelThreads - 1) / kSelThreads;
   if (need <= 8) select_kernel<8><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   else if (need <= 16) select_kernel<16><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
+  else if (need <= 24) select_kernel<24><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   else if (need <= 32) select_kernel<32><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   else select_kernel<64><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_select_tiles");
