@@ -254,27 +254,49 @@ __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs 
 }
 
 // grid (units, B*H): tile-order bf16 rows (S_out per head) -> THW rows of
-// dtype TO (S_in per head); padding rows are dropped.
+// dtype TO (S_in per head); padding rows are dropped.  Each lane moves 16
+// bytes (8 channels): a wave instruction covers 64 / (D / 8) rows, and NB
+// instructions are in flight per wave.
 template <int D, typename TO, typename Map>
 __global__ __launch_bounds__(kGatherThreads) void scatter_rows_kernel(const uint16_t* __restrict__ in, int64_t S_in,
                                                                       int64_t S_out, Map m, TO* __restrict__ out) {
-  constexpr int CPL = D / 64;
+  constexpr int LPR = D / 8;     // lanes per row
+  constexpr int RPI = 64 / LPR;  // rows per wave instruction
+  constexpr int NB = 4;          // wave instructions in flight
+  constexpr int RB = RPI * NB;   // rows per batch
+  static_assert(128 % RB == 0, "a wave's 128 rows split into whole batches");
   const int bh = blockIdx.y;
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane / LPR, c8 = (lane % LPR) * 8;
   m.init(blockIdx.x);
   if (!m.live(wid * 128)) return;
-  for (int o = 0; o < 128; ++o) {
-    const int r = wid * 128 + o;
-    const int64_t tok = m.token(r);
-    if (tok < 0) continue;
-    const uint16_t* src = in + ((int64_t)bh * S_out + m.row(r)) * D + lane * CPL;
-    TO* dst = out + ((int64_t)bh * S_in + tok) * D + lane * CPL;
-    if (sizeof(TO) == 2) {
-      if (CPL == 2) *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
-      else *reinterpret_cast<uint16_t*>(dst) = src[0];
-    } else {
+  const uint16_t* inh = in + (int64_t)bh * S_out * D + c8;
+  TO* outh = out + (int64_t)bh * S_in * D + c8;
+  for (int o0 = 0; o0 < 128; o0 += RB) {
+    uint4 v[NB];
+    int64_t tok[NB];
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) reinterpret_cast<float*>(dst)[j] = bf2f(src[j]);
+    for (int b = 0; b < NB; ++b) {
+      const int r = wid * 128 + o0 + b * RPI + sub;
+      tok[b] = m.token(r);
+      if (tok[b] >= 0) v[b] = *reinterpret_cast<const uint4*>(inh + m.row(r) * D);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (tok[b] < 0) continue;
+      TO* dst = outh + tok[b] * D;
+      if (sizeof(TO) == 2) {
+        *reinterpret_cast<uint4*>(dst) = v[b];
+      } else {
+        const uint32_t w[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+        float4 lo, hi;
+        lo.x = __uint_as_float(w[0] << 16); lo.y = __uint_as_float(w[0] & 0xffff0000u);
+        lo.z = __uint_as_float(w[1] << 16); lo.w = __uint_as_float(w[1] & 0xffff0000u);
+        hi.x = __uint_as_float(w[2] << 16); hi.y = __uint_as_float(w[2] & 0xffff0000u);
+        hi.z = __uint_as_float(w[3] << 16); hi.w = __uint_as_float(w[3] & 0xffff0000u);
+        reinterpret_cast<float4*>(dst)[0] = lo;
+        reinterpret_cast<float4*>(dst)[1] = hi;
+      }
     }
   }
 }
