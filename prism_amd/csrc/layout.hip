@@ -76,27 +76,6 @@ __global__ void rearrange_kernel(const int64_t* __restrict__ shape_ids, int64_t 
   inv_idx[tok] = p;
 }
 
-template <typename T, int CPL>
-__device__ __forceinline__ void load_row(const T* p, float* x) {
-  if (sizeof(T) == 2) {
-    if (CPL == 2) {
-      const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
-      x[0] = __uint_as_float(u << 16);
-      x[CPL - 1] = __uint_as_float(u & 0xffff0000u);
-    } else {
-      x[0] = bf2f(*reinterpret_cast<const uint16_t*>(p));
-    }
-  } else {
-    if (CPL == 2) {
-      const float2 f = *reinterpret_cast<const float2*>(p);
-      x[0] = f.x;
-      x[CPL - 1] = f.y;
-    } else {
-      x[0] = *reinterpret_cast<const float*>(p);
-    }
-  }
-}
-
 struct GatherArgs {
   const void* x;             // [B,H,S_in,D] THW order, dtype T
   const uint8_t* valid;      // [S_in] THW or null
@@ -171,82 +150,128 @@ struct ChunkMap {
 };
 
 constexpr int kGatherThreads = 256;  // 4 waves, 128 rearranged rows each
-constexpr int kGatherBatch = 8;      // rows loaded per step (loads in flight)
+
+// 8 channels of one row as floats (16 bytes of bf16 or 32 bytes of fp32)
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* x) {
+  if (sizeof(T) == 2) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+    const float4 lo = reinterpret_cast<const float4*>(p)[0], hi = reinterpret_cast<const float4*>(p)[1];
+    x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
+    x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+  }
+}
 
 // grid (units, B*H).  Wave w covers rearranged rows [128 w, 128 w + 128) of
-// unit u (blocks of 64 or 128 rows: one or two whole blocks, two tiles); lane
-// l owns channels [l*CPL, l*CPL + CPL).  Padding rows are written as zeros,
-// are invalid, and belong to no block when they lie past the last block.
+// unit u (blocks of 64 or 128 rows: one or two whole blocks, two tiles).  A
+// lane moves 8 channels (16 bytes of bf16): D / 8 lanes per row, 64 / (D / 8)
+// rows per wave instruction, NB instructions in flight.  Block means are
+// fp32 sums in row order (lanes of the first row group add the rows of each
+// instruction in turn, fetched by lane shuffles); padding rows are written as
+// zeros, are invalid, and belong to no block when they lie past the last
+// block.
 template <int D, typename T, typename Map>
 __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs a, Map m) {
-  constexpr int CPL = D / 64;
+  constexpr int LPR = D / 8;     // lanes per row
+  constexpr int RPI = 64 / LPR;  // rows per wave instruction
+  constexpr int NB = 4;          // wave instructions in flight
+  constexpr int RB = RPI * NB;   // rows per batch (inside one block and one tile)
+  static_assert(64 % RB == 0, "batches must not straddle tiles");
   const int bh = blockIdx.y;
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane / LPR, cl = lane % LPR, c8 = cl * 8;
   m.init(blockIdx.x);
   if (!m.live(wid * 128)) return;  // rows per head are a multiple of 128
   const bool first_bh = bh == 0;
-  const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)bh * a.S_in * D;
+  const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)bh * a.S_in * D + c8;
   const int64_t rowbase = (int64_t)bh * a.S_out;
+  const bool pooling = a.block_mean != nullptr || a.block_count != nullptr || a.tile_count != nullptr;
 
-  float acc[CPL];
-  int cnt = 0, tcnt = 0;
+  float acc[8];
+  int cnt = 0, tcnt = 0;  // (meaningful in the first row group)
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
 
-  for (int o0 = 0; o0 < 128; o0 += kGatherBatch) {
-    float xv[kGatherBatch][CPL];
-    bool ok[kGatherBatch];
+  for (int o0 = 0; o0 < 128; o0 += RB) {
+    float xv[NB][8];
+    bool ok[NB];
+    int64_t grow[NB];
 #pragma unroll
-    for (int u = 0; u < kGatherBatch; ++u) {
-      const int r = wid * 128 + o0 + u;
+    for (int b = 0; b < NB; ++b) {
+      const int r = wid * 128 + o0 + b * RPI + sub;
       const int64_t tok = m.token(r);
-      ok[u] = tok >= 0 && (a.valid ? (a.valid[tok] != 0) : true);
+      grow[b] = m.row(r);
+      ok[b] = tok >= 0 && (a.valid ? (a.valid[tok] != 0) : true);
       if (tok >= 0) {
-        load_row<T, CPL>(x + tok * D + lane * CPL, xv[u]);
+        load8<T>(x + tok * D, xv[b]);
       } else {
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) xv[u][j] = 0.0f;
+        for (int j = 0; j < 8; ++j) xv[b][j] = 0.0f;
       }
     }
 #pragma unroll
-    for (int u = 0; u < kGatherBatch; ++u) {
-      const int r = wid * 128 + o0 + u;
-      const int64_t grow = m.row(r);
+    for (int b = 0; b < NB; ++b) {
       if (a.out_rows) {
-        uint16_t* dst = a.out_rows + (rowbase + grow) * D + lane * CPL;
-        if (CPL == 2) *reinterpret_cast<uint32_t*>(dst) = (uint32_t)f2bf(xv[u][0]) | ((uint32_t)f2bf(xv[u][CPL - 1]) << 16);
-        else dst[0] = f2bf(xv[u][0]);
+        uint4 u;
+        u.x = (uint32_t)f2bf(xv[b][0]) | ((uint32_t)f2bf(xv[b][1]) << 16);
+        u.y = (uint32_t)f2bf(xv[b][2]) | ((uint32_t)f2bf(xv[b][3]) << 16);
+        u.z = (uint32_t)f2bf(xv[b][4]) | ((uint32_t)f2bf(xv[b][5]) << 16);
+        u.w = (uint32_t)f2bf(xv[b][6]) | ((uint32_t)f2bf(xv[b][7]) << 16);
+        *reinterpret_cast<uint4*>(a.out_rows + (rowbase + grow[b]) * D + c8) = u;
       }
       if (a.rowdot) {
-        const uint16_t* y = a.dot_with + (rowbase + grow) * D + lane * CPL;
+        float y[8];
+        load8<uint16_t>(a.dot_with + (rowbase + grow[b]) * D + c8, y);
         float part = 0.0f;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) part = __builtin_fmaf(xv[u][j], bf2f(y[j]), part);
-        part = wave_sum_xor(part);
-        if (lane == 0) a.rowdot[rowbase + grow] = part;
+        for (int j = 0; j < 8; ++j) part = __builtin_fmaf(xv[b][j], y[j], part);
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+        if (cl == 0) a.rowdot[rowbase + grow[b]] = part;
       }
+      if (first_bh && cl == 0 && a.valid_re) a.valid_re[grow[b]] = ok[b] ? 1 : 0;
+    }
+    if (pooling) {
+      // rows of the batch in order: instruction b, row group g
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) acc[j] = ok[u] ? acc[j] + xv[u][j] : acc[j];
-      cnt += ok[u] ? 1 : 0;
-      tcnt += ok[u] ? 1 : 0;
-      if (first_bh && lane == 0 && a.valid_re) a.valid_re[grow] = ok[u] ? 1 : 0;
-      if ((r + 1) % m.bsz == 0) {  // block complete
-        const int64_t blk = m.block(r);
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int g = 0; g < RPI; ++g) {
+          const int src = g * LPR + cl;
+          const bool okg = __shfl((int)ok[b], src, 64) != 0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float xg = g == 0 ? xv[b][j] : __shfl(xv[b][j], src, 64);
+            acc[j] = okg ? acc[j] + xg : acc[j];
+          }
+          cnt += okg ? 1 : 0;
+          tcnt += okg ? 1 : 0;
+        }
+      const int rlast = wid * 128 + o0 + RB - 1;
+      if ((rlast + 1) % m.bsz == 0) {  // block complete
+        const int64_t blk = m.block(rlast);
         if (blk < a.N_b) {
-          if (a.block_mean) {
+          if (a.block_mean && sub == 0) {
             const float den = (float)(cnt > 0 ? cnt : 1);
-            float* dst = a.block_mean + ((int64_t)bh * a.N_b + blk) * D + lane * CPL;
+            float* dst = a.block_mean + ((int64_t)bh * a.N_b + blk) * D + c8;
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) dst[j] = acc[j] / den;
+            for (int j = 0; j < 8; ++j) dst[j] = acc[j] / den;
           }
           if (first_bh && lane == 0 && a.block_count) a.block_count[blk] = cnt;
         }
         cnt = 0;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
+        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
       }
-      if ((r & 63) == 63) {  // tile complete
-        if (first_bh && lane == 0 && a.tile_count) a.tile_count[grow >> 6] = tcnt;
+      if ((rlast + 1) % 64 == 0) {  // tile complete
+        if (first_bh && lane == 0 && a.tile_count) a.tile_count[m.row(rlast) >> 6] = tcnt;
         tcnt = 0;
       }
     }
