@@ -219,6 +219,16 @@ int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* co
 int prism_pair_tiles(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
                      int64_t col_tiles, int32_t* pairmap, hipStream_t stream);
 
+/* Launch order of an attention kernel: order[id] = the pair (index into the
+ * prism_pair_union arrays, n = BH * pairs per head) that workgroup id
+ * processes.  Ids [0, n - tail) keep the XCD group mapping the kernel uses
+ * without an order (G = 64 for prism_bsa_fwd and prism_bsa_bwd_dq, 32 for
+ * prism_bsa_bwd_dkdv); the last tail ids (tail <= 16384) take the pairs that
+ * mapping gives them, longest union list (ulen) first, so the launch does not
+ * end waiting for long workgroups started last.  Changes no result.  No
+ * counterpart in the reference (its launch order is the hardware's). */
+int prism_pair_order(const int32_t* ulen, int64_t n, int G, int64_t tail, int32_t* order, hipStream_t stream);
+
 /* Key validity per 64-token tile (the reference's kv_valid_mask,
  * bsa_interface.py:328-385, flash_attn_bsa_varlen_mask.py:263-295) packed as
  * masks[t] bit j = valid[64 t + j] != 0.  valid: [Nt*64] uint8 tile order. */
@@ -237,11 +247,13 @@ int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
  * order; ustart/ulen/ucols: prism_pair_union of the per-query-tile key lists
  * with the same tile_masks (prism_tile_masks of the key validity, or NULL when
  * no key is padded) and the same pairmap (prism_pair_tiles of those lists, or
- * NULL for tiles 2p, 2p+1).  o: [BH,Sq,D] bf16; lse: [BH,Sq] fp32 natural log (-inf
- * for rows without a valid key; their o is 0). */
+ * NULL for tiles 2p, 2p+1).  order: prism_pair_order of ulen with G = 64, or
+ * NULL.  o: [BH,Sq,D] bf16; lse: [BH,Sq] fp32 natural log (-inf for rows
+ * without a valid key; their o is 0). */
 int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
                   const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen, const int32_t* ucols,
-                  const int32_t* pairmap, float sm_scale, void* o, float* lse, hipStream_t stream);
+                  const int32_t* pairmap, const int32_t* order, float sm_scale, void* o, float* lse,
+                  hipStream_t stream);
 
 /* _attn_bwd_preprocess (common.py:110-127): delta[r] = sum_d o[r][d] * do[r][d]
  * over rows of bf16 [rows, D] tensors; fp32 out. */
@@ -254,21 +266,22 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
  * prism_bwd_preprocess; kv_valid: [Sk] uint8 tile order or NULL;
  * ustart/ulen/ucols: prism_pair_union of the per-key-tile query lists of
  * prism_transpose_lists (tile_masks NULL), built with the key-tile pairing
- * pairmap (prism_pair_tiles of those lists, or NULL for tiles 2p, 2p+1).
+ * pairmap (prism_pair_tiles of those lists, or NULL for tiles 2p, 2p+1);
+ * order: prism_pair_order of ulen with G = 32, or NULL.
  * dk, dv: [BH,Sk,D] bf16. */
 int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
                        const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint8_t* kv_valid,
                        const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap,
-                       float sm_scale, void* dk, void* dv, hipStream_t stream);
+                       const int32_t* order, float sm_scale, void* dk, void* dv, hipStream_t stream);
 
 /* dQ of attn_bwd_bsa_varlen_triton (bsa_interface.py:489-523;
  * _attn_bwd_dq_bsa_varlen_align_wrapper, flash_attn_bsa_varlen_mask.py:879-1014).
- * Shapes as for prism_bsa_bwd_dkdv; lists and tile_masks as for
+ * Shapes as for prism_bsa_bwd_dkdv; lists, tile_masks and order as for
  * prism_bsa_fwd; dq: [BH,Sq,D] bf16. */
 int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
                      int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart,
-                     const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap, float sm_scale, void* dq,
-                     hipStream_t stream);
+                     const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap, const int32_t* order,
+                     float sm_scale, void* dq, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,7 @@ struct BwdArgs {
   const int32_t* ulen;
   const int32_t* ucols;
   const int32_t* pairmap;   // tiles of pair p (of the side the grid walks), or null for 2p, 2p + 1
+  const int32_t* order;     // pair of each workgroup id (prism_pair_order), or null: xcd_group_remap
   int64_t Sq, Sk;
   int npairs;               // tile pairs per head of the side the grid walks
   float sm_scale, scale_log2;
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
   const int kh = w & 1, tk = (w >> 1) & 1, qh = w >> 2;
-  const int logical = xcd_group_remap<32>((int)blockIdx.x, (int)gridDim.x);
+  const int logical = a.order ? a.order[blockIdx.x] : xcd_group_remap<32>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
@@ -251,7 +252,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
   const int qh = w & 1, tq = w >> 1;
-  const int logical = xcd_group_remap<64>((int)blockIdx.x, (int)gridDim.x);
+  const int logical = a.order ? a.order[blockIdx.x] : xcd_group_remap<64>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
@@ -409,8 +410,8 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 
 int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
                        const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint8_t* kv_valid,
-                       const int64_t* ustart,
-                       const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap, float sm_scale, void* dk,
+                       const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap,
+                       const int32_t* order, float sm_scale, void* dk,
                        void* dv,
                        hipStream_t stream) {
   int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dkdv");
@@ -419,7 +420,7 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
   a.m2 = m2; a.delta = delta; a.kv_valid = kv_valid;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.Sq = Sq; a.Sk = Sk;
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.order = order; a.Sq = Sq; a.Sk = Sk;
   a.npairs = (int)(Sk / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
@@ -431,14 +432,15 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
 
 int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
                      int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen,
-                     const int32_t* ucols, const int32_t* pairmap, float sm_scale, void* dq, hipStream_t stream) {
+                     const int32_t* ucols, const int32_t* pairmap, const int32_t* order, float sm_scale, void* dq,
+                     hipStream_t stream) {
   int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dq");
   if (rc) return rc;
   PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq: null pointer");
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
   a.m2 = m2; a.delta = delta; a.tmask = tile_masks;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.Sq = Sq; a.Sk = Sk;
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.order = order; a.Sq = Sq; a.Sk = Sk;
   a.npairs = (int)(Sq / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
   const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);

@@ -48,6 +48,7 @@ struct FwdArgs {
   const int32_t* ulen;     // [BH * Sq/128]
   const int32_t* ucols;    // entries tile << 3 | partial << 2 | in_b << 1 | in_a
   const int32_t* pairmap;  // [BH * Sq/64]: tiles of pair p are pairmap[2p], pairmap[2p + 1] (or 2p, 2p + 1)
+  const int32_t* order;    // [BH * Sq/128] pair of each workgroup id (prism_pair_order), or null: xcd_group_remap
   int64_t Sq, Sk;
   int npairs;              // query-tile pairs per head
   float scale_log2;        // sm_scale * log2(e)
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
-  const int logical = xcd_group_remap<64>((int)blockIdx.x, (int)gridDim.x);
+  const int logical = a.order ? a.order[blockIdx.x] : xcd_group_remap<64>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
@@ -243,7 +244,7 @@ extern "C" {
 int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
                   const uint64_t* tile_masks,
                   const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap,
-                  float sm_scale, void* o, float* lse,
+                  const int32_t* order, float sm_scale, void* o, float* lse,
                   hipStream_t stream) {
   PRISM_REQUIRE(q && k && v && ustart && ulen && ucols && o && lse, "prism_bsa_fwd: null pointer");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_bsa_fwd: head_dim %d unsupported (64, 128)", D);
@@ -253,7 +254,7 @@ int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S
   PRISM_REQUIRE((int64_t)BH * (Sq / 128) < (1ll << 31), "prism_bsa_fwd: grid too large");
   FwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.tmask = tile_masks;
-  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.Sq = Sq; a.Sk = Sk;
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.order = order; a.Sq = Sq; a.Sk = Sk;
   a.npairs = (int)(Sq / 128);
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.o = (uint16_t*)o; a.lse = lse;

@@ -196,6 +196,54 @@ __global__ __launch_bounds__(256) void lse_to_m2_kernel(const float* __restrict_
   m2[i] = x == -__builtin_inff() ? __builtin_inff() : x * 1.4426950408889634f;
 }
 
+// ------------------------------------------------------------------ launch order
+// Workgroup id -> pair of the attention launches.  Ids [0, n - T) keep the
+// XCD group mapping (xcd_group_remap<G>); the last T ids take the pairs that
+// mapping would give them, longest work list first, so the launch ends on
+// short workgroups instead of waiting for long ones started last.
+constexpr int kOrderMax = 16384;  // largest sorted tail (one workgroup, LDS bitonic sort, 128 KB)
+
+__device__ __forceinline__ int group_remap_rt(int bid, int n, int G) {
+  const int full = n / (8 * G) * (8 * G);
+  if (bid >= full) return bid;
+  const int chunk = bid / (8 * G), xcd = bid & 7, slot = (bid >> 3) % G;
+  return chunk * 8 * G + xcd * G + slot;
+}
+
+__global__ __launch_bounds__(1024) void pair_order_kernel(const int32_t* __restrict__ ulen, int n, int G, int T,
+                                                          int P2, int32_t* __restrict__ order) {
+  __shared__ uint64_t key[kOrderMax];  // (~len << 32) | pair: ascending = longest first, then lower pair
+  const int k = n - T;
+  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < k; p += gridDim.x * blockDim.x)
+    order[p] = group_remap_rt(p, n, G);
+  if (blockIdx.x != 0) return;
+  for (int i = threadIdx.x; i < P2; i += blockDim.x) {
+    uint64_t v = ~0ull;
+    if (i < T) {
+      const int pair = group_remap_rt(k + i, n, G);
+      v = ((uint64_t)(0xffffffffu - (uint32_t)ulen[pair]) << 32) | (uint32_t)pair;
+    }
+    key[i] = v;
+  }
+  __syncthreads();
+  for (int size = 2; size <= P2; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < P2; i += blockDim.x) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool up = (i & size) == 0;
+          const uint64_t x = key[i], y = key[j];
+          if ((x > y) == up) {
+            key[i] = y;
+            key[j] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  for (int i = threadIdx.x; i < T; i += blockDim.x) order[k + i] = (int32_t)(key[i] & 0xffffffffu);
+}
+
 }  // namespace
 
 extern "C" {
@@ -247,6 +295,21 @@ int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream) 
   if (n == 0) return PRISM_OK;
   lse_to_m2_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(lse, n, m2);
   PRISM_LAUNCH_CHECK("prism_lse_to_m2");
+  return PRISM_OK;
+}
+
+int prism_pair_order(const int32_t* ulen, int64_t n, int G, int64_t tail, int32_t* order, hipStream_t stream) {
+  PRISM_REQUIRE(ulen && order, "prism_pair_order: null pointer");
+  PRISM_REQUIRE(n >= 1 && n < (1ll << 31), "prism_pair_order: n out of range");
+  PRISM_REQUIRE(G == 32 || G == 64, "prism_pair_order: G must be the attention kernels' group (32 or 64)");
+  PRISM_REQUIRE(tail >= 0 && tail <= n && tail <= kOrderMax, "prism_pair_order: tail must be in [0, min(n, %d)]",
+                kOrderMax);
+  int P2 = 1;
+  while (P2 < tail) P2 <<= 1;
+  const int64_t head = n - tail;
+  const unsigned blocks = (unsigned)(head > 0 ? (head + 1023) / 1024 : 1);
+  pair_order_kernel<<<blocks < 1 ? 1 : blocks, 1024, 0, stream>>>(ulen, (int)n, G, (int)tail, P2, order);
+  PRISM_LAUNCH_CHECK("prism_pair_order");
   return PRISM_OK;
 }
 

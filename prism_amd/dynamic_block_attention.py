@@ -83,9 +83,13 @@ class _Plan:
         # pair the query tiles of each zone by list overlap (fewest idle wave slots)
         self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lay.Nt)
         self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks, pairmap=self.qpair)
+        # launch order of the forward and dQ kernels (the last workgroups ids
+        # take the longest lists first: the launch does not end on a long one)
+        self.qorder = ops.pair_order(self.qunion[1], 64)
         self.klists = None
         self.kpair = None
         self.kunion = None
+        self.korder = None
 
     def sum_lens(self) -> int:
         """Executed (query tile, key tile) pairs (host sync)."""
@@ -99,7 +103,8 @@ class _DynBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _Plan, sm_scale: float):
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair)
+        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
+                                plan.qorder)
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
@@ -117,9 +122,11 @@ class _DynBSA(torch.autograd.Function):
             plan.klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, plan.B * plan.H, lay.Nt)
             plan.kpair = ops.pair_tiles(*plan.klists, lay.Nt)
             plan.kunion = ops.pair_union(*plan.klists, lay.Nt, pairmap=plan.kpair)
+            plan.korder = ops.pair_order(plan.kunion[1], 32)
         m2 = ops.lse_to_m2(lse)
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid,
-                                          plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale, plan.qpair, plan.kpair)
+                                          plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale, plan.qpair, plan.kpair,
+                                          plan.qorder, plan.korder)
         tq, tk, tv = ctx.in_dtypes
         dq = ops.scatter_rows(dq_re, lay, tq)
         dk = ops.scatter_rows(dk_re, lay, tk)

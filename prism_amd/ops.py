@@ -455,6 +455,24 @@ def pair_tiles(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt
     return out
 
 
+# fraction of an attention launch's workgroups ordered longest-list-first
+ORDER_TAIL = 0.25
+
+
+def pair_order(ulen: torch.Tensor, group: int, tail_frac: Optional[float] = None) -> torch.Tensor:
+    """Workgroup order of an attention launch over the pairs of ulen
+    (prism_pair_order): the XCD group mapping for the first ids, the last
+    tail_frac of them (at most 16384) longest work list first.  group: 64 for
+    the forward and dQ kernels, 32 for dK/dV."""
+    _cuda(ulen)
+    n = ulen.numel()
+    frac = ORDER_TAIL if tail_frac is None else tail_frac
+    tail = min(n, 16384, int(n * frac))
+    order = torch.empty(n, device=ulen.device, dtype=torch.int32)
+    _call("prism_pair_order", _p(ulen.contiguous()), n, int(group), tail, _p(order), _stream())
+    return order
+
+
 def pair_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt: int,
                tmasks: Optional[torch.Tensor] = None, col_tiles: Optional[int] = None,
                pairmap: Optional[torch.Tensor] = None):
@@ -510,28 +528,30 @@ def _attn_shapes(q, k, v):
     return B, H, Sq, Sk, D
 
 
-def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float, qpair: Optional[torch.Tensor] = None):
+def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float, qpair: Optional[torch.Tensor] = None,
+            qorder: Optional[torch.Tensor] = None):
     """q [B,H,Sq,D], k, v [B,H,Sk,D] bf16 tile order; qunion = pair_union of
     the per-query-tile key lists (with the pairing qpair, or None for
     neighbouring tiles) -> (o bf16, lse fp32 natural)."""
-    _cuda(q, k, v, tmasks, qpair)
+    _cuda(q, k, v, tmasks, qpair, qorder)
     q, k, v = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v")
     B, H, Sq, Sk, D = _attn_shapes(q, k, v)
     ustart, ulen, ucols = qunion
     o = torch.empty_like(q)
     lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
     _call("prism_bsa_fwd", _p(q), _p(k), _p(v), B * H, Sq, Sk, D, _p(tmasks), _p(ustart), _p(ulen), _p(ucols),
-          _p(qpair), float(sm_scale), _p(o), _p(lse), _stream())
+          _p(qpair), _p(qorder), float(sm_scale), _p(o), _p(lse), _stream())
     return o, lse
 
 
 def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float,
-            qpair: Optional[torch.Tensor] = None, kpair: Optional[torch.Tensor] = None):
+            qpair: Optional[torch.Tensor] = None, kpair: Optional[torch.Tensor] = None,
+            qorder: Optional[torch.Tensor] = None, korder: Optional[torch.Tensor] = None):
     """Backward over tile-order bf16 tensors; qunion / kunion = pair unions of
     the per-query-tile key lists and of the per-key-tile query lists, built
     with the pairings qpair / kpair (None: neighbouring tiles).  Returns
     dq, dk, dv (bf16, tile order)."""
-    _cuda(q, k, v, do, m2, delta, kv_valid, tmasks, qpair, kpair)
+    _cuda(q, k, v, do, m2, delta, kv_valid, tmasks, qpair, kpair, qorder, korder)
     q, k, v, do = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"), _bf16(do, "do")
     B, H, Sq, Sk, D = _attn_shapes(q, k, v)
     if do.shape != q.shape:
@@ -541,7 +561,7 @@ def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: 
     dv = torch.empty_like(v)
     s = _stream()
     _call("prism_bsa_bwd_dkdv", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(kv_valid),
-          _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), _p(kpair), float(sm_scale), _p(dk), _p(dv), s)
+          _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), _p(kpair), _p(korder), float(sm_scale), _p(dk), _p(dv), s)
     _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(tmasks),
-          _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), _p(qpair), float(sm_scale), _p(dq), s)
+          _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), _p(qpair), _p(qorder), float(sm_scale), _p(dq), s)
     return dq, dk, dv

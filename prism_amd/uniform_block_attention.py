@@ -71,9 +71,12 @@ class _ChunkPlan:
         self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lq.Nt, lk.Nt)
         self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lq.Nt, self.tmasks, col_tiles=lk.Nt,
                                      pairmap=self.qpair)
+        # launch order of the forward and dQ kernels (longest lists last-dispatched first)
+        self.qorder = ops.pair_order(self.qunion[1], 64)
         self.klists = None
         self.kpair = None
         self.kunion = None
+        self.korder = None
 
     def key_lists(self):
         if self.kunion is None:
@@ -81,6 +84,7 @@ class _ChunkPlan:
                                               self.lk.Nt)
             self.kpair = ops.pair_tiles(*self.klists, self.lk.Nt, self.lq.Nt)
             self.kunion = ops.pair_union(*self.klists, self.lk.Nt, None, col_tiles=self.lq.Nt, pairmap=self.kpair)
+            self.korder = ops.pair_order(self.kunion[1], 32)
         return self.kunion
 
     def sum_lens(self) -> int:
@@ -95,7 +99,8 @@ class _ChunkBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _ChunkPlan, sm_scale: float):
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair)
+        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
+                                plan.qorder)
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
@@ -111,7 +116,7 @@ class _ChunkBSA(torch.autograd.Function):
         m2 = ops.lse_to_m2(lse)
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, gd["rows"], m2, gd["rowdot"],
                                           plan.kv_valid, plan.tmasks, plan.qunion, kunion, ctx.sm_scale, plan.qpair,
-                                          plan.kpair)
+                                          plan.kpair, plan.qorder, plan.korder)
         tq, tk, tv = ctx.in_dtypes
         return (ops.chunk_scatter_rows(dq_re, plan.lq, tq), ops.chunk_scatter_rows(dk_re, plan.lk, tk),
                 ops.chunk_scatter_rows(dv_re, plan.lk, tv), None, None)

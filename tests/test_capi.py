@@ -77,12 +77,16 @@ def test_invalid_arguments_raise_without_gpu():
     with pytest.raises(ValueError, match="Tin\\*Hin\\*Win != S"):
         _lib.call("prism_scatter_rows", 1, 1, 1, 500, 64, 1, 8, 8, 8, 7, 8, 8, 1, 0, None)
     with pytest.raises(ValueError, match="null pointer"):
-        _lib.call("prism_bsa_fwd", None, None, None, 1, 128, 128, 64, None, None, None, None, None, 0.1, None, None,
-                  None)
+        _lib.call("prism_bsa_fwd", None, None, None, 1, 128, 128, 64, None, None, None, None, None, None, 0.1, None,
+                  None, None)
     with pytest.raises(ValueError, match="head_dim"):
-        _lib.call("prism_bsa_fwd", 1, 1, 1, 1, 128, 128, 96, None, 1, 1, 1, None, 0.1, 1, 1, None)
+        _lib.call("prism_bsa_fwd", 1, 1, 1, 1, 128, 128, 96, None, 1, 1, 1, None, None, 0.1, 1, 1, None)
     with pytest.raises(ValueError, match="multiples of 128"):
-        _lib.call("prism_bsa_bwd_dq", 1, 1, 1, 1, 1, 1, 1, 128, 192, 64, None, 1, 1, 1, None, 0.1, 1, None)
+        _lib.call("prism_bsa_bwd_dq", 1, 1, 1, 1, 1, 1, 1, 128, 192, 64, None, 1, 1, 1, None, None, 0.1, 1, None)
+    with pytest.raises(ValueError, match="tail must be"):
+        _lib.call("prism_pair_order", 1, 100, 64, 101, 1, None)
+    with pytest.raises(ValueError, match="group"):
+        _lib.call("prism_pair_order", 1, 100, 16, 10, 1, None)
     with pytest.raises(ValueError, match="even row_tiles"):
         _lib.call("prism_pair_tiles", 1, 1, 1, 10, 5, 5, 1, None)
     with pytest.raises(ValueError, match="64 or 128"):
@@ -90,4 +94,4 @@ def test_invalid_arguments_raise_without_gpu():
                   None, None, None, None, None, None, None, None)
     with pytest.raises(ValueError, match="multiple of the chunk|multiples of the chunk"):
         _lib.call("prism_chunk_scatter_rows", 1, 1, 1, 64, 4, 4, 4, 4, 4, 6, 4, 4, 4, 128, 1, 1, None)
-    assert _lib.load().prism_abi_version() == 5
+    assert _lib.load().prism_abi_version() == 6

@@ -300,6 +300,27 @@ def test_lse_to_m2():
     assert np.array_equal(m2, ref.astype(np.float32))
 
 
+def _xcd_group_remap(bid, n, G):
+    """The attention kernels' default workgroup mapping, restated."""
+    full = n // (8 * G) * (8 * G)
+    if bid >= full:
+        return bid
+    chunk, xcd, slot = bid // (8 * G), bid & 7, (bid >> 3) % G
+    return chunk * 8 * G + xcd * G + slot
+
+
+def _check_order(order, ulen, G, tail):
+    """prism_pair_order: a permutation; ids before the tail keep the default
+    mapping; the tail holds the same pairs, longest list first (ties: lower pair)."""
+    n = len(ulen)
+    assert np.array_equal(np.sort(order), np.arange(n))
+    k = n - tail
+    base = np.array([_xcd_group_remap(b, n, G) for b in range(n)])
+    assert np.array_equal(order[:k], base[:k])
+    want = sorted(base[k:].tolist(), key=lambda p: (-int(ulen[p]), p))
+    assert order[k:].tolist() == want
+
+
 def _tol(got, ref, what):
     """max-abs 2e-2, mean-abs 2e-3 (bf16 vs float64)."""
     err = np.abs(got.astype(np.float64) - ref)
@@ -322,6 +343,13 @@ def test_attention_fwd_bwd_tolerance(case):
     q0 = ops.pair_union(plan.qstart, plan.qlen, plan.qcols, plan.lay.Nt, plan.tmasks)
     o0, lse0 = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, q0, sm)
     assert bits_equal(host(o), host(o0)) and bits_equal(host(lse), host(lse0))
+    # nor does the launch order (every tail length, up to all workgroups)
+    npairs = plan.qunion[1].numel()
+    for frac in (0.1, 1.0):
+        qo = ops.pair_order(plan.qunion[1], 64, frac)
+        _check_order(host(qo), host(plan.qunion[1]), 64, min(npairs, 16384, int(npairs * frac)))
+        o1, lse1 = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, qo)
+        assert bits_equal(host(o), host(o1)) and bits_equal(host(lse), host(lse1))
     qf = O.bf16_bits_to_f32(host(plan.q_re)).reshape(B * H, S, D)
     kf = O.bf16_bits_to_f32(host(plan.k_re)).reshape(B * H, S, D)
     vf = O.bf16_bits_to_f32(host(plan.v_re)).reshape(B * H, S, D)
@@ -350,6 +378,12 @@ def test_attention_fwd_bwd_tolerance(case):
                          ops.pair_union(*klists, plan.lay.Nt), sm)
     for g, g0 in zip((dq, dk, dv), grads0):
         assert bits_equal(host(g), host(g0))
+    korder = ops.pair_order(kunion[1], 32, 1.0)
+    _check_order(host(korder), host(kunion[1]), 32, min(kunion[1].numel(), 16384))
+    grads1 = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_t, m2, delta, plan.kv_valid, plan.tmasks, plan.qunion,
+                         kunion, sm, plan.qpair, kpair, ops.pair_order(plan.qunion[1], 64, 1.0), korder)
+    for g, g1 in zip((dq, dk, dv), grads1):
+        assert bits_equal(host(g), host(g1))
     dof = O.bf16_bits_to_f32(do).reshape(B * H, S, D)
     dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, og, dof, lse_ref, *lists, kv, sm)
     for name, g, r in (("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
