@@ -544,6 +544,23 @@ def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float, qpair: Optional[torch.Tens
     return o, lse
 
 
+# dK/dV and dQ are independent: with BWD_CONCURRENT the dK/dV kernel runs on a
+# second stream (default priority) so that the dQ kernel's workgroups fill the
+# CUs that the end of the dK/dV launch leaves idle.  Measured 0.7% faster per
+# step at config 4, but the two launches then overlap, so their individual
+# durations no longer measure either kernel; off by default.
+BWD_CONCURRENT = False
+_side_streams: Dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    st = _side_streams.get(idx)
+    if st is None:
+        st = _side_streams[idx] = torch.cuda.Stream(device=idx)
+    return st
+
+
 def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float,
             qpair: Optional[torch.Tensor] = None, kpair: Optional[torch.Tensor] = None,
             qorder: Optional[torch.Tensor] = None, korder: Optional[torch.Tensor] = None):
@@ -559,9 +576,27 @@ def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: 
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    s = _stream()
-    _call("prism_bsa_bwd_dkdv", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(kv_valid),
-          _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), _p(kpair), _p(korder), float(sm_scale), _p(dk), _p(dv), s)
+    def dkdv(stream):
+        _call("prism_bsa_bwd_dkdv", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(kv_valid),
+              _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), _p(kpair), _p(korder), float(sm_scale), _p(dk), _p(dv),
+              stream)
+
+    main = torch.cuda.current_stream()
+    if BWD_CONCURRENT:
+        side = _side_stream(q.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            dkdv(side.cuda_stream)
+        # the side stream reads and writes these: the allocator must not hand
+        # their memory out again before its work is done
+        for t in (q, k, v, do, m2, delta, kv_valid, kunion[0], kunion[1], kunion[2], kpair, korder, dk, dv):
+            if t is not None:
+                t.record_stream(side)
+    else:
+        dkdv(main.cuda_stream)
     _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(tmasks),
-          _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), _p(qpair), _p(qorder), float(sm_scale), _p(dq), s)
+          _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), _p(qpair), _p(qorder), float(sm_scale), _p(dq),
+          main.cuda_stream)
+    if BWD_CONCURRENT:
+        main.wait_stream(side)
     return dq, dk, dv
