@@ -338,8 +338,8 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int b = 8 * (r >> 2) + (r & 3);
-        sacc[0][r] = ((lo >> b) & 1u) ? sacc[0][r] : NINF;
-        sacc[1][r] = ((hi >> b) & 1u) ? sacc[1][r] : NINF;
+        sacc[0][r] = keep_or_ninf(sacc[0][r], lo, b);
+        sacc[1][r] = keep_or_ninf(sacc[1][r], hi, b);
       }
     }
 #pragma unroll

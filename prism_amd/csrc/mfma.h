@@ -59,6 +59,15 @@ __device__ __forceinline__ float xor32_add(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// x if bit b of bits is set, else -inf: the signed one-bit field extract
+// (v_bfe_i32) is the all-ones / zero select mask and one three-input bit
+// operation (v_bitop3_b32) merges, two independent VALU ops per element
+// instead of a compare, a VCC hazard and a select
+__device__ __forceinline__ float keep_or_ninf(float x, uint32_t bits, int b) {
+  const uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)bits, (uint32_t)b, 1u);
+  return __uint_as_float((__float_as_uint(x) & m) | (~m & 0xff800000u));
+}
+
 // 2^x on the transcendental unit (v_exp_f32); exp2(-inf) = 0
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
