@@ -411,6 +411,33 @@ __global__ __launch_bounds__(64) void set_bits_kernel(const int64_t* __restrict_
   }
 }
 
+// grid (words, BH): workgroup (w, bh) builds bitmap column w (q tiles
+// 32 w .. 32 w + 31) of head bh for every k tile in LDS with LDS atomics and
+// writes it once (no global atomics, the bitmap needs no clearing)
+constexpr int kColMaxTiles = 16384;  // LDS column of up to 16384 k tiles (64 KB of dynamic LDS)
+__global__ __launch_bounds__(256) void set_bits_col_kernel(const int64_t* __restrict__ qstart,
+                                                           const int32_t* __restrict__ qlen,
+                                                           const int32_t* __restrict__ qcols, int64_t Ntq, int64_t Ntk,
+                                                           int64_t words, uint32_t* __restrict__ bm) {
+  extern __shared__ uint32_t col[];  // [Ntk]
+  const int64_t w = blockIdx.x, bh = blockIdx.y;
+  for (int64_t k = threadIdx.x; k < Ntk; k += blockDim.x) col[k] = 0u;
+  __syncthreads();
+  for (int j = 0; j < 32; ++j) {
+    const int64_t t = w * 32 + j;
+    if (t >= Ntq) break;
+    const int64_t row = bh * Ntq + t;
+    const int n = qlen[row];
+    const int32_t* cols = qcols + qstart[row];
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int32_t k = cols[i];
+      if (k >= 0 && k < Ntk) atomicOr(&col[k], 1u << j);
+    }
+  }
+  __syncthreads();
+  for (int64_t k = threadIdx.x; k < Ntk; k += blockDim.x) bm[(bh * Ntk + k) * words + w] = col[k];
+}
+
 // one wave per k row: emit the set bits (ascending q tiles)
 __global__ __launch_bounds__(256) void emit_bits_kernel(const uint32_t* __restrict__ bm, int64_t rows,
                                                         int64_t words, int64_t kcap, int64_t* __restrict__ kstart,
@@ -503,8 +530,13 @@ int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int3
   PRISM_REQUIRE(kcap >= Ntq, "prism_transpose_lists: kcap must be >= Ntq");
   const int64_t qrows = (int64_t)BH * Ntq, krows = (int64_t)BH * Ntk, words = (Ntq + 31) / 32;
   if (qrows == 0) return PRISM_OK;
-  fill_u32_kernel<<<1024, 256, 0, stream>>>(bitmap, krows * words, 0u);
-  set_bits_kernel<<<(unsigned)qrows, 64, 0, stream>>>(qstart, qlen, qcols, Ntq, Ntk, words, bitmap);
+  if (Ntk <= kColMaxTiles) {
+    set_bits_col_kernel<<<dim3((unsigned)words, (unsigned)BH), 256, (size_t)Ntk * 4, stream>>>(qstart, qlen, qcols, Ntq,
+                                                                                            Ntk, words, bitmap);
+  } else {
+    fill_u32_kernel<<<1024, 256, 0, stream>>>(bitmap, krows * words, 0u);
+    set_bits_kernel<<<(unsigned)qrows, 64, 0, stream>>>(qstart, qlen, qcols, Ntq, Ntk, words, bitmap);
+  }
   emit_bits_kernel<<<(unsigned)((krows + 3) / 4), 256, 0, stream>>>(bitmap, krows, words, kcap, kstart, klen, kcols);
   PRISM_LAUNCH_CHECK("prism_transpose_lists");
   return PRISM_OK;
