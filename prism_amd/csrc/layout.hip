@@ -172,7 +172,8 @@ __device__ __forceinline__ void load8(const T* p, float* x) {
 // grid (units, B*H).  Wave w covers rearranged rows [128 w, 128 w + 128) of
 // unit u (blocks of 64 or 128 rows: one or two whole blocks, two tiles).  A
 // lane moves 8 channels (16 bytes of bf16): D / 8 lanes per row, 64 / (D / 8)
-// rows per wave instruction, NB instructions in flight.  Block means are
+// rows per wave instruction, NB instructions in flight (fewer registers, more
+// waves per SIMD beat more loads per wave here).  Block means are
 // fp32 sums in row order (lanes of the first row group add the rows of each
 // instruction in turn, fetched by lane shuffles); padding rows are written as
 // zeros, are invalid, and belong to no block when they lie past the last
@@ -181,7 +182,7 @@ template <int D, typename T, typename Map>
 __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs a, Map m) {
   constexpr int LPR = D / 8;     // lanes per row
   constexpr int RPI = 64 / LPR;  // rows per wave instruction
-  constexpr int NB = 4;          // wave instructions in flight
+  constexpr int NB = 2;          // wave instructions in flight (2: 0.256 ms, 4: 0.283, 8: 0.326 at C4)
   constexpr int RB = RPI * NB;   // rows per batch (inside one block and one tile)
   static_assert(64 % RB == 0, "batches must not straddle tiles");
   const int bh = blockIdx.y;
