@@ -271,6 +271,8 @@ def main():
     ap.add_argument("--path", default="dynamic", choices=("dynamic", "uniform"),
                     help="dynamic: _run_bsa_dynamic (the headline); uniform: the fixed 4x4x4-chunk branch of "
                          "_run_bsa (flash_attn_bsa_3d) on the same inputs and selection parameters")
+    ap.add_argument("--sweep", action="store_true",
+                    help="C5: density sweep on the config's shapes (one JSON line of its own, not the headline)")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -298,6 +300,9 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     log(f"[bench] config {args.config}: generating inputs")
     inp = make_inputs(args.config)
+    if args.sweep:
+        run_sweep(args, inp)
+        return
     if args.path == "uniform":
         run_uniform(args, inp)
         return
@@ -439,6 +444,85 @@ def main():
         "roofline": roof, "cpu_baseline": cpu, "dense": dense, "breakdown": breakdown,
     }
     print(json.dumps(rec), flush=True)
+
+
+SWEEP_DENSITIES = (0.05, 0.10, 0.25, 0.50, 1.00)
+
+
+def run_sweep(args, inp):
+    """C5: density sweep on the C4 shapes.  Shape ids uniform over the 13
+    candidates (seeded) and passed as shape_ids=; top-k only with
+    k = round(d N_b) for d in SWEEP_DENSITIES (sparsity = 1 - (k + 0.5) / N_b,
+    so that int((1 - s) N_b) = k, bsa_interface.py:289; s = 0 for k = N_b);
+    fwd + bwd of flash_attn_bsa_3d_dynamic per density against torch SDPA
+    fwd + bwd on the same unpadded shape.  Prints one JSON line with the
+    per-density step time, kept-block TFLOP/s and realised density, the dense
+    time, and the density at which the sparse step stops being faster."""
+    import torch
+    from prism_amd import flash_attn_bsa_3d_dynamic, ops, plan_dynamic
+    from prism_amd.adapter import padded_grid
+    from prism_amd.dynamic_block_shape import ALL_CANDIDATE_SHAPES
+    B, H, D, S = inp["B"], inp["H"], inp["D"], inp["S"]
+    grid = inp["grid"]
+    gp, _ = padded_grid(grid)
+    Nz = (gp[0] // 8) * (gp[1] // 8) * (gp[2] // 8)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    sid = torch.randint(0, len(ALL_CANDIDATE_SHAPES), (Nz,), generator=gen, device="cuda", dtype=torch.int64)
+    N_b = ops.ZoneLayout(sid, gp, grid).N_b
+    q = inp["q"].clone().requires_grad_(True)
+    k = inp["k"].clone().requires_grad_(True)
+    v = inp["v"].clone().requires_grad_(True)
+    do = inp["do"]
+    rows = []
+    for d in SWEEP_DENSITIES:
+        kk = max(1, min(N_b, round(d * N_b)))
+        sp = 0.0 if kk == N_b else 1.0 - (kk + 0.5) / N_b
+
+        def step():
+            q.grad = k.grad = v.grad = None
+            out = flash_attn_bsa_3d_dynamic(q, k, v, gp, method="ivpq", sparsity=sp, cdf_threshold=None,
+                                            shape_ids=sid, input_grid=grid)
+            out.backward(do)
+
+        log(f"[sweep] density {d}: k={kk} of N_b={N_b}")
+        ms, _ = time_region(step, args.steps, args.warmup)
+        with torch.no_grad():
+            plan = plan_dynamic(q.detach(), k.detach(), v.detach(), gp, method="ivpq", sparsity=sp,
+                                cdf_threshold=None, shape_ids=sid, input_grid=grid)
+        sum_lens = plan.sum_lens()
+        Nt = plan.lay.Nt
+        fl = 64 * 64 * D * sum_lens
+        rows.append({"target_density": d, "k": kk, "density": round(sum_lens / (B * H * Nt * Nt), 4),
+                     "ms_per_step": round(ms, 2), "tflops": round(14 * fl / (ms * 1e-3) / 1e12, 1)})
+        del plan
+        torch.cuda.empty_cache()
+    qd = inp["q"].clone().requires_grad_(True)
+    kd = inp["k"].clone().requires_grad_(True)
+    vd = inp["v"].clone().requires_grad_(True)
+
+    def dstep():
+        qd.grad = kd.grad = vd.grad = None
+        o = torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)
+        o.backward(do)
+
+    log("[sweep] dense SDPA")
+    dms, _ = time_region(dstep, 2, 1)
+    # the sparse step's time grows with density; first density where it is no
+    # longer faster than dense, linearly interpolated (None: faster everywhere)
+    cross = None
+    for a_, b_ in zip(rows, rows[1:]):
+        if a_["ms_per_step"] < dms <= b_["ms_per_step"]:
+            t = (dms - a_["ms_per_step"]) / (b_["ms_per_step"] - a_["ms_per_step"])
+            cross = round(a_["density"] + t * (b_["density"] - a_["density"]), 4)
+    print(json.dumps({
+        "metric": "C5 density sweep: sparse fwd+bwd ms per step vs dense SDPA fwd+bwd",
+        "config": {"workload": "c5: C4 shapes, seeded uniform shape ids, top-k only", "B": B, "H": H, "D": D,
+                   "grid": list(grid), "grid_padded": list(gp), "N_b": N_b},
+        "steps": args.steps, "warmup": args.warmup, "dtype": "bf16", "data": "synthetic",
+        "sweep": rows,
+        "dense": {"impl": "torch SDPA (ROCm) fwd+bwd, same shape, unpadded", "ms": round(dms, 2),
+                  "tflops": round(14 * S * S * D * B * H / (dms * 1e-3) / 1e12, 1)},
+        "crossover_density": cross}))
 
 
 def run_uniform(args, inp):
