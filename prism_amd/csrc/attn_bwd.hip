@@ -30,7 +30,10 @@
 // holds half-size partial accumulators; the two partials are added in a
 // fixed order through LDS at the end (deterministic).  Wave w owns keys
 // [32 kh, 32 kh + 32) of tile 2p + tk and query rows [32 qh, 32 qh + 32) of
-// every listed query tile (kh = w & 1, tk = (w >> 1) & 1, qh = w >> 2).  S = Q K^T and dP = dO V^T keep one key per lane column, so P
+// every listed query tile (kh = w & 1, qh = (w >> 1) & 1, tk = w >> 2).
+// Waves w and w + 4 share a SIMD (the hardware places wave i of a workgroup
+// on SIMD (i + c) mod 4), so each SIMD holds one wave of each key tile and an
+// entry listed by one tile only still keeps all four SIMDs busy.  S = Q K^T and dP = dO V^T keep one key per lane column, so P
 // and dS feed the B operand of dV^T = dO^T P and dK^T = Q^T dS straight from
 // the accumulators.
 // dQ: two 4-wave workgroups per CU (their phases drift apart, so one's
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
-  const int kh = w & 1, tk = (w >> 1) & 1, qh = w >> 2;
+  const int kh = w & 1, qh = (w >> 1) & 1, tk = w >> 2;
   const int logical = a.order ? a.order[blockIdx.x] : xcd_group_remap<32>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   // add the two query-half partials in a fixed order (qh = 0 + qh = 1)
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem);
-  const int slot = w & 3;
+  const int slot = kh | tk << 1;  // (kh, tk) of the wave pair
   if (qh == 1) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
