@@ -1,5 +1,8 @@
-"""Parity at the full BASELINE config-4 size (2K: B=1, H=5, D=128, input grid
-21x90x160, zone grid 24x96x160, top-48 + p = 0.9).
+"""Parity at the full sizes of the BASELINE GPU configs:
+  c4  2K:    B=1, H=5,  D=128, input grid 21x90x160, top-48 + p = 0.9
+  c3  1080p: B=1, H=24, D=128, input grid 21x68x120, top-32 + p = 0.9
+  c2  720p:  B=1, H=24, D=128, input grid 21x45x80,  sparsity 0.75
+(inputs from bench.make_inputs, the benchmark's own generator).
 
 The whole plan and the attention kernels run at full size; the float64
 oracle checks what it finishes in seconds:
@@ -47,14 +50,15 @@ def _rows(t, bh, first, count):
     return t.view(-1, t.shape[-2], t.shape[-1])[bh, first:first + count].float().cpu().numpy()
 
 
-def test_config4_full_size():
+@pytest.mark.parametrize("cfg", ["c2", "c3", "c4"])
+def test_full_size(cfg):
     import bench
     from prism_amd import a2v_token_norms, ops, plan_dynamic
     from prism_amd.adapter import padded_grid
     from prism_amd.dynamic_block_shape import _gradient_and_shapes
 
-    say("fullsize: config-4 inputs")
-    inp = bench.make_inputs("c4")
+    say("fullsize:", cfg, "inputs")
+    inp = bench.make_inputs(cfg)
     B, H, D, grid = inp["B"], inp["H"], inp["D"], inp["grid"]
     gp, _ = padded_grid(grid)
     BH, sm = B * H, 1 / math.sqrt(D)
@@ -63,7 +67,10 @@ def test_config4_full_size():
     with torch.no_grad():
         sid = _gradient_and_shapes(inp["v"], norms, gp, "ivpq", 0.5, 0.15, 1.0, None, grid)[2]
         N_b = ops.ZoneLayout(sid, gp, grid).N_b
-        sp, cdf = 1.0 - (inp["topk"] + 0.5) / N_b, inp["cdf"]
+        if inp["sp_only"] is not None:
+            sp, cdf = inp["sp_only"], None
+        else:
+            sp, cdf = 1.0 - (inp["topk"] + 0.5) / N_b, inp["cdf"]
         plan = plan_dynamic(inp["q"], inp["k"], inp["v"], gp, method="ivpq", sparsity=sp, cdf_threshold=cdf,
                             audio_token_norms=norms, input_grid=grid)
     lay, Nt = plan.lay, plan.lay.Nt
