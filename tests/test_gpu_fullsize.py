@@ -3,8 +3,9 @@
   c3  1080p: B=1, H=24, D=128, input grid 21x68x120, top-32 + p = 0.9
   c2  720p:  B=1, H=24, D=128, input grid 21x45x80,  sparsity 0.75
 (inputs from bench.make_inputs, the benchmark's own generator), through the
-dynamic-shape path (flash_attn_bsa_3d_dynamic's plan and kernels) and, for
-c3 and c4, the uniform 4x4x4-chunk path (flash_attn_bsa_3d).
+dynamic-shape path (flash_attn_bsa_3d_dynamic's plan and kernels), for c3
+and c4 the uniform 4x4x4-chunk path (flash_attn_bsa_3d), and at c4 the v2a
+bridge cross-attention (flash_attn_bsa_cross, audio queries over video keys).
 
 The whole plan and the attention kernels run at full size; the float64
 oracle checks what it finishes in seconds:
@@ -250,5 +251,51 @@ def test_full_size_uniform(cfg):
     torch.cuda.synchronize()
     _attention(rng, plan.q_re, plan.k_re, plan.v_re, plan.kv_valid, o, lse, do_re, delta, dq, dk, dv, plan.qstart,
                plan.qlen, plan.qcols, plan.klists, BH, Nt, D, sm)
+    del plan, o, lse, dq, dk, dv, do_re, gd, inp
+    torch.cuda.empty_cache()
+
+
+def test_full_size_cross_v2a():
+    """The v2a bridge cross-attention at config-4 size (hymm/config.py:249-253:
+    Q = audio, 1-D chunks of 64 tokens; K = video, 3-D 4x4x4 chunks; sparsity
+    0.875): 2,000 audio queries over the 302,400 video keys of config 4."""
+    import bench
+    from prism_amd import ops
+    from prism_amd.uniform_block_attention import plan_chunked
+
+    say("fullsize v2a: inputs")
+    inp = bench.make_inputs("c4")
+    B, H, D, grid = inp["B"], inp["H"], inp["D"], inp["grid"]
+    BH, sm, Sa, sp = B * H, 1 / math.sqrt(D), 2000, 0.875
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    qa = torch.randn((B, H, Sa, D), generator=gen, device=DEV).to(torch.bfloat16)
+    do = torch.randn((B, H, Sa, D), generator=gen, device=DEV).to(torch.bfloat16)
+    lq = ops.ChunkLayout((1, 1, Sa), (1, 1, 64), DEV)
+    lk = ops.ChunkLayout(grid, (4, 4, 4), DEV)
+    say("fullsize v2a: plan")
+    plan = plan_chunked(qa, inp["k"], inp["v"], lq, lk, sparsity=sp, cdf_threshold=None, sm_scale=sm)
+    Ntq, Ntk = lq.Nt, lk.Nt
+    k_tile_count = plan.kv_valid.view(-1, TILE).sum(1, dtype=torch.int32)
+    q_tile_count = torch.clamp(Sa - TILE * torch.arange(Ntq, device=DEV), 0, TILE).to(torch.int32)
+    tiles, ntiles, tcap = plan.sel["tiles"], plan.sel["ntiles"], plan.sel["tcap"]
+    rng = np.random.default_rng(6)
+    kbt = O.chunk_kblock_tiles(lk.N_b, lk.csz, Ntk)
+    _selection_rows(rng, plan.scores.view(BH, lq.N_b, lk.N_b), tiles, ntiles, tcap, sp, None, sm, kbt, Ntk,
+                    k_tile_count.cpu().numpy())
+    _list_structure(tiles, ntiles, tcap, Ntk, lq.N_b, BH, lq.block_id_of_tile, plan.qstart, plan.qlen,
+                    q_tile_count)
+
+    say("fullsize v2a: forward")
+    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, plan.qorder)
+    say("fullsize v2a: backward")
+    gd = ops.chunk_gather_pool(do, lq, None, rows=True, dot_with=o)
+    do_re, delta = gd["rows"], gd["rowdot"]
+    kunion = plan.key_lists()
+    m2 = ops.lse_to_m2(lse)
+    dq, dk, dv = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid, plan.tmasks,
+                             plan.qunion, kunion, sm, plan.qpair, plan.kpair, plan.qorder, plan.korder)
+    torch.cuda.synchronize()
+    _attention(rng, plan.q_re, plan.k_re, plan.v_re, plan.kv_valid, o, lse, do_re, delta, dq, dk, dv, plan.qstart,
+               plan.qlen, plan.qcols, plan.klists, BH, Ntq, D, sm)
     del plan, o, lse, dq, dk, dv, do_re, gd, inp
     torch.cuda.empty_cache()
