@@ -21,7 +21,8 @@ oracle checks what it finishes in seconds:
     them; they are checked against float64 sums over those query tiles with
     each query row's LSE and delta taken from the kernels (the LSE itself is
     checked on the sampled query rows);
-  * two forward launches give bit-identical O and LSE.
+  * two forward launches give bit-identical O and LSE, two backward
+    launches bit-identical dQ, dK and dV.
 """
 import math
 
@@ -205,6 +206,12 @@ def test_full_size(cfg):
     m2 = ops.lse_to_m2(lse)
     dq, dk, dv = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid, plan.tmasks,
                              plan.qunion, kunion, sm, plan.qpair, kpair, plan.qorder, korder)
+    # a second backward launch gives the same bits (no atomics, fixed orders)
+    again = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid, plan.tmasks,
+                        plan.qunion, kunion, sm, plan.qpair, kpair, plan.qorder, korder)
+    for g, g2 in zip((dq, dk, dv), again):
+        assert torch.equal(g.view(torch.int16), g2.view(torch.int16))
+    del again
     torch.cuda.synchronize()
     _attention(rng, plan.q_re, plan.k_re, plan.v_re, plan.kv_valid, o, lse, do_re, delta, dq, dk, dv, plan.qstart,
                plan.qlen, plan.qcols, klists, BH, Nt, D, sm)
