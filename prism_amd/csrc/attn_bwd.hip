@@ -33,7 +33,8 @@
 // every listed query tile (kh = w & 1, qh = (w >> 1) & 1, tk = w >> 2).
 // Waves w and w + 4 share a SIMD (the hardware places wave i of a workgroup
 // on SIMD (i + c) mod 4), so each SIMD holds one wave of each key tile and an
-// entry listed by one tile only still keeps all four SIMDs busy.  S = Q K^T and dP = dO V^T keep one key per lane column, so P
+// entry listed by one tile only still keeps all four SIMDs busy.
+// S = Q K^T and dP = dO V^T keep one key per lane column, so P
 // and dS feed the B operand of dV^T = dO^T P and dK^T = Q^T dS straight from
 // the accumulators.
 // dQ: two 4-wave workgroups per CU (their phases drift apart, so one's
