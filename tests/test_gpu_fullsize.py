@@ -159,15 +159,22 @@ def _sparsity(inp, N_b):
     return 1.0 - (inp["topk"] + 0.5) / N_b, inp["cdf"]
 
 
-@pytest.mark.parametrize("cfg", ["c2", "c3", "c4"])
+@pytest.mark.parametrize("cfg", ["c2", "c3", "c4", "c4_d64"])
 def test_full_size(cfg):
+    """c4_d64: config 4's tokens and lists with head_dim 64 (config 1's head
+    size; the first 64 channels of config 4's inputs), for the D = 64
+    kernels at full size."""
     import bench
     from prism_amd import a2v_token_norms, ops, plan_dynamic
     from prism_amd.adapter import padded_grid
     from prism_amd.dynamic_block_shape import _gradient_and_shapes
 
     say("fullsize:", cfg, "inputs")
-    inp = bench.make_inputs(cfg)
+    inp = bench.make_inputs(cfg.split("_")[0])
+    if cfg.endswith("_d64"):
+        for name in ("q", "k", "v", "do"):
+            inp[name] = inp[name][..., :64].contiguous()
+        inp["D"] = 64
     B, H, D, grid = inp["B"], inp["H"], inp["D"], inp["grid"]
     gp, _ = padded_grid(grid)
     BH, sm = B * H, 1 / math.sqrt(D)
