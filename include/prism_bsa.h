@@ -92,7 +92,11 @@ int prism_a2v_norms(const void* res, int dtype, int64_t S, int C, void* out, int
 /* _build_block_tile_maps (dynamic_block_attention.py:138-170) in CSR form.
  * block_offset: [Nz+1] (block_offset[Nz] = N_b), block_id_of_tile: [Nz*8],
  * block_first_tile: [Nz*8+1] (block b owns tiles [first[b], first[b+1]);
- * entry N_b is the sentinel N_tiles, as kblock_tiles row N_b). */
+ * entry N_b is the sentinel N_tiles, as kblock_tiles row N_b).
+ * A shape id outside 0..12 sets block_offset[Nz] = -1 (the other outputs are
+ * then meaningless): the caller checks it before passing the ids to any other
+ * entry point, which all take valid ids (the reference raises an IndexError
+ * from local_orders[shape_ids] in the same case, dynamic_block_attention.py:130). */
 int prism_zone_layout(const int64_t* shape_ids, int Nz, int32_t* block_offset, int32_t* block_id_of_tile,
                       int32_t* block_first_tile, hipStream_t stream);
 

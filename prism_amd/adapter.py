@@ -102,7 +102,7 @@ class DynamicBlockSparseAttention:
             audio_token_norms=None if audio_token_norms is None else audio_token_norms.reshape(-1),
             lambda_a=p.get("dynamic_block_lambda_a", 0.5), tau_128=p.get("dynamic_block_tau_128", 0.15),
             lambda_128=p.get("dynamic_block_lambda_128", 1.0), shape_ids=cached, return_shape_ids=True,
-            input_grid=(T, H, W))
+            input_grid=(T, H, W), compute_padded_queries=False)  # padded rows are sliced away (:429-431)
         if self.training:
             self._dyn_shape_cache = (self.pass_id, grid_padded, used)
         return out

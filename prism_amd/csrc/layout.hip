@@ -33,15 +33,19 @@ __global__ __launch_bounds__(kLayoutThreads) void zone_layout_kernel(
     const int64_t* __restrict__ shape_ids, int Nz, int32_t* __restrict__ block_offset,
     int32_t* __restrict__ block_id_of_tile, int32_t* __restrict__ block_first_tile) {
   __shared__ int32_t sWave[kLayoutThreads / 64];
-  __shared__ int32_t sCarry;
+  __shared__ int32_t sCarry, sBad;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  if (tid == 0) sCarry = 0;
+  if (tid == 0) sCarry = sBad = 0;
   __syncthreads();
   for (int base = 0; base < Nz; base += kLayoutThreads) {
     const int z = base + tid;
     int tpb = 1, nbz = 0;
     if (z < Nz) {
-      const int c = (int)shape_ids[z];
+      const int64_t id = shape_ids[z];
+      // an id outside the candidate table is reported through block_offset[Nz]
+      // (the caller raises); shape 0 stands in so that no access leaves bounds
+      const int c = (id >= 0 && id < PRISM_NCAND) ? (int)id : 0;
+      if (c != id) sBad = 1;
       tpb = (kCand[c][0] * kCand[c][1] * kCand[c][2]) / 64;
       nbz = 8 / tpb;
     }
@@ -60,8 +64,9 @@ __global__ __launch_bounds__(kLayoutThreads) void zone_layout_kernel(
     if (tid == kLayoutThreads - 1) sCarry = excl + nbz;
     __syncthreads();
   }
+  __syncthreads();
   if (tid == 0) {
-    block_offset[Nz] = sCarry;
+    block_offset[Nz] = sBad ? -1 : sCarry;
     block_first_tile[sCarry] = Nz * 8;
   }
 }

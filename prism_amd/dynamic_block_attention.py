@@ -52,7 +52,7 @@ class _Plan:
     """Everything the attention kernels need for one call, built under no_grad."""
 
     def __init__(self, q, k, v, grid, shape_ids, valid_mask, sparsity, cdf_threshold, sm_scale,
-                 compute_padded_queries=False, box=None):
+                 compute_padded_queries=False, box=None, keep_scores=False):
         B, H, _, D = q.shape
         self.lay = ops.ZoneLayout(shape_ids, grid, box)
         lay = self.lay
@@ -69,9 +69,12 @@ class _Plan:
         self.tile_count = gq["tile_count"]
         scores = ops.block_scores(gq["block_mean"].view(B * H, lay.N_b, D), gk["block_mean"].view(B * H, lay.N_b, D),
                                   self.block_count if masked else None)
-        self.scores = scores
         sel = ops.select_tiles(scores, sparsity, cdf_threshold, sm_scale, lay.block_first_tile,
                                self.tile_count if masked else None)
+        # the [B*H, N_b, N_b] scores (564 MB at 2K) are freed once the lists
+        # exist, as the reference frees them per head; kept only on request
+        self.scores = scores if keep_scores else None
+        del scores
         self.sel = sel
         skip = masked and not compute_padded_queries
         self.qstart, self.qlen = ops.tile_rows(sel["ntiles"], lay.block_id_of_tile, B * H, lay.Nt, lay.N_b,
@@ -136,14 +139,17 @@ class _DynBSA(torch.autograd.Function):
 
 def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold=None, audio_token_norms=None,
                  valid_mask=None, lambda_a=0.5, tau_128=0.15, lambda_128=1.0, shape_ids=None,
-                 compute_padded_queries=False, input_grid=None) -> _Plan:
+                 compute_padded_queries=False, input_grid=None, keep_scores=False) -> _Plan:
     """Steps (1)-(5) of flash_attn_bsa_3d_dynamic: shape ids, layout, pooled
     scores, selection and tile lists (no attention).
 
     With input_grid (Ti, Hi, Wi) inside grid_padded, q, k, v, the audio norms
     and valid_mask cover the input grid only (S = Ti Hi Wi): the zero padding
     and padding mask of wan_video_dit.py:342-400 are applied inside the
-    kernels, with results identical to padding first."""
+    kernels, with results identical to padding first.  compute_padded_queries
+    defaults to False here, the adapters' setting (flash_attn_bsa_3d_dynamic
+    passes True unless told otherwise).  keep_scores keeps the fp32 block
+    scores on the plan (plan.scores) for inspection."""
     B, Hn, S, D = q.shape
     T, H, W = grid_padded
     box = tuple(input_grid) if input_grid is not None else (T, H, W)
@@ -156,11 +162,13 @@ def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold
         raise ValueError(f"unknown dynamic-block method: {method!r}")
     sm_scale = 1.0 / (D ** 0.5)
     with torch.no_grad():
-        if shape_ids is None:
+        if shape_ids is not None:
+            shape_ids = torch.as_tensor(shape_ids, device=q.device)
+        else:
             shape_ids = _gradient_and_shapes(v.detach(), audio_token_norms, (T, H, W), method, lambda_a, tau_128,
                                              lambda_128, valid_mask, box)[2]
         return _Plan(q.detach(), k.detach(), v.detach(), (T, H, W), shape_ids, valid_mask, sparsity, cdf_threshold,
-                     sm_scale, compute_padded_queries, box)
+                     sm_scale, compute_padded_queries, box, keep_scores)
 
 
 def flash_attn_bsa_3d_dynamic(
@@ -179,7 +187,7 @@ def flash_attn_bsa_3d_dynamic(
     lambda_128: float = 1.0,
     shape_ids: Optional[torch.Tensor] = None,
     return_shape_ids: bool = False,
-    compute_padded_queries: bool = False,
+    compute_padded_queries: bool = True,
     input_grid: Optional[Tuple[int, int, int]] = None,
 ):
     """Dynamic-block-shape BSA for video self-attention; returns [B,H,S,D] in
@@ -188,12 +196,13 @@ def flash_attn_bsa_3d_dynamic(
     (attention itself runs in bf16 MFMA with fp32 accumulation).
 
     With a valid_mask, query tiles that hold no valid token are padding the
-    caller slices away (wan_video_dit.py:429-431).  The reference still
-    attends for them (their pooled query is 0, so the threshold keeps ~p of
-    all blocks); here their output is 0 unless compute_padded_queries=True.
-    Outputs at valid positions and all gradients of valid tokens are the same
-    either way when the incoming gradient is 0 at padded positions (as the
-    caller's unpadding makes it).
+    caller slices away (wan_video_dit.py:429-431).  Like the reference, this
+    function attends for them by default (their pooled query is 0, so the
+    threshold keeps ~p of all blocks).  compute_padded_queries=False (not in
+    the reference's signature; the adapters use it) gives them empty lists
+    instead: their output rows are 0, and outputs at valid positions and all
+    gradients of valid tokens are the same either way when the incoming
+    gradient is 0 at padded positions (as the caller's unpadding makes it).
 
     input_grid (not in the reference's signature) takes the caller's unpadded
     grid: q, k, v [B,H,Ti*Hi*Wi,D], audio norms and valid_mask then cover it,

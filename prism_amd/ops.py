@@ -14,6 +14,7 @@ import torch
 from . import _lib
 
 F32, BF16 = 0, 1
+_CANDIDATES = 13  # entries of the candidate shape table (dynamic_block_shape.py:6-27)
 
 
 def _stream() -> int:
@@ -172,6 +173,10 @@ class ZoneLayout:
         self.Nt = self.Nz * 8
         self.S = T * Hg * Wg
         self.S_in = self.box[0] * self.box[1] * self.box[2]
+        if shape_ids.dtype.is_floating_point or shape_ids.dtype == torch.bool or shape_ids.dim() != 1 \
+                or shape_ids.numel() != self.Nz:
+            raise ValueError(f"shape_ids must be a 1-D integer tensor of {self.Nz} zone ids for grid {self.grid}, "
+                             f"got {shape_ids.dtype} {tuple(shape_ids.shape)}")
         self.shape_ids = shape_ids.contiguous().to(torch.int64)
         dev = shape_ids.device
         self.block_offset = torch.empty(self.Nz + 1, device=dev, dtype=torch.int32)
@@ -180,13 +185,18 @@ class ZoneLayout:
         _call("prism_zone_layout", _p(self.shape_ids), self.Nz, _p(self.block_offset), _p(self.block_id_of_tile),
                   _p(self.block_first_tile), _stream())
         # the one host synchronisation of the path (the reference syncs here too,
-        # dynamic_block_attention.py:153): N_b sizes the block tensors
+        # dynamic_block_attention.py:153): N_b sizes the block tensors; the
+        # kernel reports ids outside the candidate table as N_b = -1, before
+        # any other kernel reads them
         self.N_b = int(self.block_offset[self.Nz].item())
+        if self.N_b < 0:
+            raise ValueError(f"shape_ids must index the {_CANDIDATES}-entry candidate table (0..{_CANDIDATES - 1})")
 
 
 def rearrange_index(shape_ids: torch.Tensor, grid):
     _cuda(shape_ids)
     T, Hg, Wg = _grid(grid)
+    ZoneLayout(shape_ids, grid)  # validates the ids (count and range) before the kernel reads them
     S = T * Hg * Wg
     src = torch.empty(S, device=shape_ids.device, dtype=torch.int64)
     inv = torch.empty(S, device=shape_ids.device, dtype=torch.int64)

@@ -21,9 +21,11 @@ undoes the rearrangement and drops the padding.
 
 Deliberate differences from the reference, as in the dynamic path: chunk means
 and scores are fp32 with one fixed summation order (the reference pools and
-scores in q's dtype); query tiles with no valid token get empty lists (their
-output rows are 0 instead of attention over the selected keys) unless
-compute_padded_queries=True; queries are pooled with their own validity in
+scores in q's dtype); with compute_padded_queries=False (the adapters and
+flash_attn_bsa_cross, which slice padded rows away) query tiles with no valid
+token get empty lists (their output rows are 0 instead of attention over the
+selected keys), while flash_attn_bsa and flash_attn_bsa_3d attend for them by
+default, as the reference does; queries are pooled with their own validity in
 their own chunk order (the reference pools them with the key-order mask, which
 is the same thing whenever the two chunk shapes agree).
 """
@@ -40,7 +42,7 @@ class _ChunkPlan:
     """Rearranged rows, selection and work lists of one call (built under no_grad)."""
 
     def __init__(self, q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, q_valid, k_valid, sparsity,
-                 cdf_threshold, sm_scale, compute_padded_queries=False):
+                 cdf_threshold, sm_scale, compute_padded_queries=False, keep_scores=False):
         B, H, _, D = q.shape
         BH = B * H
         self.lq, self.lk = lq, lk
@@ -53,10 +55,12 @@ class _ChunkPlan:
         k_masked = k_valid is not None or lk.padded
         self.kv_valid = gk["valid_re"] if k_masked else None
         # uniform path: no invalid-key fill of the scores (bsa_interface.py:611-631)
-        self.scores = ops.block_scores(gq["block_mean"].view(BH, lq.N_b, D), gk["block_mean"].view(BH, lk.N_b, D),
-                                       None)
-        sel = ops.select_tiles(self.scores, sparsity, cdf_threshold, sm_scale, lk.block_first_tile,
+        scores = ops.block_scores(gq["block_mean"].view(BH, lq.N_b, D), gk["block_mean"].view(BH, lk.N_b, D), None)
+        sel = ops.select_tiles(scores, sparsity, cdf_threshold, sm_scale, lk.block_first_tile,
                                gk["tile_count"] if k_masked else None, tiles_per_block=lk.tiles_per_block)
+        # scores are freed once the lists exist (kept only on request)
+        self.scores = scores if keep_scores else None
+        del scores
         self.sel = sel
         if q_masked and not compute_padded_queries:
             qcount = gq["tile_count"]  # tiles without a valid query token (and row padding) get no list
@@ -134,13 +138,14 @@ def _check_qkv(q, k, v):
 
 
 def plan_chunked(q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, *, sparsity, cdf_threshold, sm_scale,
-                 q_valid=None, k_valid=None, compute_padded_queries=False) -> _ChunkPlan:
-    """Selection half of the uniform path (no attention)."""
+                 q_valid=None, k_valid=None, compute_padded_queries=False, keep_scores=False) -> _ChunkPlan:
+    """Selection half of the uniform path (no attention).  keep_scores keeps
+    the fp32 chunk scores on the plan (plan.scores) for inspection."""
     if sparsity is None and cdf_threshold is None:
         raise ValueError("Either sparsity or cdf_threshold must be provided")
     with torch.no_grad():
         return _ChunkPlan(q.detach(), k.detach(), v.detach(), lq, lk, q_valid, k_valid, sparsity, cdf_threshold,
-                          sm_scale, compute_padded_queries)
+                          sm_scale, compute_padded_queries, keep_scores)
 
 
 def bsa_chunked(q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, *, sparsity, cdf_threshold, sm_scale,
@@ -153,7 +158,7 @@ def bsa_chunked(q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, *, sparsity, 
 
 
 def flash_attn_bsa(q, k, v, chunk_size_q, chunk_size_k, sparsity, cdf_threshold, sm_scale, kv_valid_mask=None,
-                   q_valid_mask=None, score_modifier=None, compute_padded_queries=False):
+                   q_valid_mask=None, score_modifier=None, compute_padded_queries=True):
     """_attention_bsa.apply (bsa_interface.py:597-683): q, k, v [B,H,S,D]
     already in chunk order; chunk sizes in tokens (64 or 128).  The query
     chunks are pooled with q_valid_mask, else with kv_valid_mask when
@@ -174,7 +179,7 @@ def flash_attn_bsa(q, k, v, chunk_size_q, chunk_size_k, sparsity, cdf_threshold,
 def flash_attn_bsa_3d(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, latent_shape_q, latent_shape_k,
                       sparsity=0.875, cdf_threshold=None, chunk_3d_shape_q: Sequence[int] = (4, 4, 8),
                       chunk_3d_shape_k: Sequence[int] = (4, 4, 8), valid_mask: Optional[torch.Tensor] = None,
-                      compute_padded_queries: bool = False) -> torch.Tensor:
+                      compute_padded_queries: bool = True) -> torch.Tensor:
     """Uniform 3-D-chunk BSA over THW tokens (bsa_interface.py:1123-1176).
     q: [B,H,Sq,D], k, v: [B,H,Sk,D] in THW order of latent_shape_q / _k, each a
     multiple of its chunk shape; valid_mask [Sq] (True = valid, Sq == Sk)

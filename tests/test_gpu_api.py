@@ -288,6 +288,25 @@ def test_errors_match_reference():
         flash_attn_bsa_3d_dynamic(x.cpu(), x.cpu(), x.cpu(), (8, 8, 8), method="ivpq")
 
 
+def test_bad_shape_ids_raise():
+    """Caller-supplied shape ids outside the 13-entry table, or of the wrong
+    count or type, raise ValueError before any kernel but the (bounds-safe)
+    zone layout reads them; good ids still work after a rejected call."""
+    from prism_amd import flash_attn_bsa_3d_dynamic, ops
+    x = torch.zeros((1, 1, 1024, 64), device="cuda", dtype=torch.bfloat16)
+    grid = (8, 8, 16)  # two zones
+    for bad in ([0, 13], [-1, 0], [0, 1, 2], [[0, 1]]):
+        with pytest.raises(ValueError, match="shape_ids"):
+            flash_attn_bsa_3d_dynamic(x, x, x, grid, method="ivpq", shape_ids=torch.tensor(bad, device="cuda"))
+    with pytest.raises(ValueError, match="shape_ids"):
+        flash_attn_bsa_3d_dynamic(x, x, x, grid, method="ivpq", shape_ids=torch.tensor([0.0, 1.0], device="cuda"))
+    with pytest.raises(ValueError, match="shape_ids"):
+        ops.rearrange_index(torch.tensor([3, 99], device="cuda"), grid)
+    out, sid = flash_attn_bsa_3d_dynamic(x, x, x, grid, method="ivpq", shape_ids=torch.tensor([12, 0]),
+                                         return_shape_ids=True)
+    assert sid.tolist() == [12, 0] and out.shape == x.shape and bool(torch.isfinite(out).all())
+
+
 def test_a2v_norms_adapter_batch0_dtype():
     from prism_amd import a2v_token_norms
     rng = np.random.default_rng(1)

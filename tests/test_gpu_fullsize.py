@@ -41,12 +41,19 @@ def say(*a):
     print(*a, flush=True)
 
 
-def _tol(got, ref, what):
-    """max-abs 2e-2, mean-abs 2e-3 (bf16 vs float64)."""
-    err = np.abs(got.astype(np.float64) - ref)
+def _tol(got, ref, what, rel_bound=1e-2):
+    """max-abs 2e-2, mean-abs 2e-3 (bf16 vs float64); plus
+    a relative bound ||got - ref|| / ||ref|| <= 1e-2 (Frobenius), which
+    catches a scaled result where the values are small (at long lists |O| and
+    |dQ| average ~6e-3, below the absolute bounds)."""
+    diff = got.astype(np.float64) - ref
+    err = np.abs(diff)
     mx, mean = float(err.max()), float(err.mean())
-    say(what, "max-abs", mx, "mean-abs", mean)
+    ref_norm = float(np.linalg.norm(ref))
+    rel = float(np.linalg.norm(diff)) / ref_norm if ref_norm > 0 else float(np.linalg.norm(diff))
+    say(what, "max-abs", mx, "mean-abs", mean, "rel", rel, "||ref||", ref_norm)
     assert mx <= 2e-2 and mean <= 2e-3, (what, mx, mean)
+    assert rel <= rel_bound, (what, "relative error", rel, "||ref||", ref_norm)
 
 
 def _rows(t, bh, first, count):
@@ -87,16 +94,17 @@ def _list_structure(tiles, ntiles, tcap, Ntk, N_b, BH, block_id_of_tile, qstart,
 
 
 def _attention(rng, q_re, k_re, v_re, kv_valid, o, lse, do_re, delta, dq, dk, dv, qstart, qlen, qcols, klists,
-               BH, Nt, D, sm):
-    """O, LSE, dQ of sampled query tiles vs the float64 oracle; dK, dV of
-    sampled key tiles vs float64 sums over the query tiles that list them."""
+               BH, Nt, D, sm, nq=6, nk=3):
+    """O, LSE, dQ of nq sampled query tiles vs the float64 oracle; dK, dV of
+    nk sampled key tiles vs float64 sums over the query tiles that list them
+    (the last of each is the tile with the longest list)."""
     kv = kv_valid.cpu().numpy().astype(bool)
     lse_h = lse.view(BH, -1)
     delta_h = delta.view(BH, -1)
     qlen_h = qlen.cpu().numpy()
     qstart_h = qstart.cpu().numpy()
     cand = np.nonzero(qlen_h > 0)[0]
-    pick = list(rng.choice(cand, 5, replace=False)) + [int(cand[np.argmax(qlen_h[cand])])]
+    pick = list(rng.choice(cand, nq - 1, replace=False)) + [int(cand[np.argmax(qlen_h[cand])])]
     for r in pick:
         bh, t = divmod(int(r), Nt)
         n = int(qlen_h[r])
@@ -128,7 +136,7 @@ def _attention(rng, q_re, k_re, v_re, kv_valid, o, lse, do_re, delta, dq, dk, dv
         _tol(_rows(dq, bh, t * TILE, TILE), dq_ref[0, :TILE], "dQ")
     kstart, klen, kcols = (x.cpu().numpy() for x in klists)
     kcand = np.nonzero(klen > 0)[0]
-    kpick = list(rng.choice(kcand, 2, replace=False)) + [int(kcand[np.argmax(klen[kcand])])]
+    kpick = list(rng.choice(kcand, nk - 1, replace=False)) + [int(kcand[np.argmax(klen[kcand])])]
     for r in kpick:
         bh, j = divmod(int(r), klen.size // BH)
         n = int(klen[r])
@@ -185,7 +193,7 @@ def test_full_size(cfg):
         N_b = ops.ZoneLayout(sid, gp, grid).N_b
         sp, cdf = _sparsity(inp, N_b)
         plan = plan_dynamic(inp["q"], inp["k"], inp["v"], gp, method="ivpq", sparsity=sp, cdf_threshold=cdf,
-                            audio_token_norms=norms, input_grid=grid)
+                            audio_token_norms=norms, input_grid=grid, keep_scores=True)
     lay, Nt = plan.lay, plan.lay.Nt
     assert lay.N_b == N_b and plan.S == gp[0] * gp[1] * gp[2]
     tiles, ntiles, tcap = plan.sel["tiles"], plan.sel["ntiles"], plan.sel["tcap"]
@@ -242,7 +250,8 @@ def test_full_size_uniform(cfg):
     lay = ops.ChunkLayout(grid, (4, 4, 4), DEV)
     sp, cdf = _sparsity(inp, lay.N_b)
     say("fullsize uniform: plan")
-    plan = plan_chunked(inp["q"], inp["k"], inp["v"], lay, lay, sparsity=sp, cdf_threshold=cdf, sm_scale=sm)
+    plan = plan_chunked(inp["q"], inp["k"], inp["v"], lay, lay, sparsity=sp, cdf_threshold=cdf, sm_scale=sm,
+                        keep_scores=True)
     Nt, N_b = lay.Nt, lay.N_b
     assert plan.kv_valid is not None  # the padded grid has padding rows
     tile_count = plan.kv_valid.view(-1, TILE).sum(1, dtype=torch.int32)
@@ -287,7 +296,8 @@ def test_full_size_cross_v2a():
     lq = ops.ChunkLayout((1, 1, Sa), (1, 1, 64), DEV)
     lk = ops.ChunkLayout(grid, (4, 4, 4), DEV)
     say("fullsize v2a: plan")
-    plan = plan_chunked(qa, inp["k"], inp["v"], lq, lk, sparsity=sp, cdf_threshold=None, sm_scale=sm)
+    plan = plan_chunked(qa, inp["k"], inp["v"], lq, lk, sparsity=sp, cdf_threshold=None, sm_scale=sm,
+                        keep_scores=True)
     Ntq, Ntk = lq.Nt, lk.Nt
     k_tile_count = plan.kv_valid.view(-1, TILE).sum(1, dtype=torch.int32)
     q_tile_count = torch.clamp(Sa - TILE * torch.arange(Ntq, device=DEV), 0, TILE).to(torch.int32)

@@ -233,7 +233,7 @@ def test_full_selection_pipeline_bitexact(case):
         plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method=method,
                             sparsity=sp, cdf_threshold=p,
                             audio_token_norms=None if case["nh"] is None else dev(case["nh"]),
-                            valid_mask=None if valid is None else dev(valid).bool())
+                            valid_mask=None if valid is None else dev(valid).bool(), keep_scores=True)
         assert np.array_equal(host(plan.lay.shape_ids), ref["shape_ids"])
         assert bits_equal(host(plan.scores).reshape(ref["scores"].shape), ref["scores"])
         qlen = host(plan.qlen)
@@ -321,12 +321,19 @@ def _check_order(order, ulen, G, tail):
     assert order[k:].tolist() == want
 
 
-def _tol(got, ref, what):
-    """max-abs 2e-2, mean-abs 2e-3 (bf16 vs float64)."""
-    err = np.abs(got.astype(np.float64) - ref)
+def _tol(got, ref, what, rel_bound=1e-2):
+    """max-abs 2e-2, mean-abs 2e-3 (bf16 vs float64); plus
+    a relative bound ||got - ref|| / ||ref|| <= 1e-2 (Frobenius), which
+    catches a scaled result where the values are small (at long lists |O| and
+    |dQ| average ~6e-3, below the absolute bounds)."""
+    diff = got.astype(np.float64) - ref
+    err = np.abs(diff)
     mx, mean = float(err.max()), float(err.mean())
-    say(what, "max-abs", mx, "mean-abs", mean)
+    ref_norm = float(np.linalg.norm(ref))
+    rel = float(np.linalg.norm(diff)) / ref_norm if ref_norm > 0 else float(np.linalg.norm(diff))
+    say(what, "max-abs", mx, "mean-abs", mean, "rel", rel, "||ref||", ref_norm)
     assert mx <= 2e-2 and mean <= 2e-3, (what, mx, mean)
+    assert rel <= rel_bound, (what, "relative error", rel, "||ref||", ref_norm)
 
 
 def test_attention_fwd_bwd_tolerance(case):
@@ -390,18 +397,19 @@ def test_attention_fwd_bwd_tolerance(case):
         _tol(O.bf16_bits_to_f32(host(g)).reshape(B * H, S, D), r, name)
 
 
-@pytest.mark.parametrize("compute_padded", [False, True])
+@pytest.mark.parametrize("compute_padded", [False, True, None])
 def test_end_to_end_autograd(case, compute_padded):
     """flash_attn_bsa_3d_dynamic forward + backward through autograd in THW
     order vs the oracle attention on the oracle's own selection (with and
-    without attention for fully padded query tiles)."""
+    without attention for fully padded query tiles; None = the default call,
+    which attends for them as the reference does)."""
     from prism_amd import flash_attn_bsa_3d_dynamic
     valid = case["valid"] if case["pad"] else None
     B, H, S, D = case["q"].shape
     sm = 1 / math.sqrt(D)
     ref = O.select_pipeline(case["qh"], case["kh"], case["vh"], case["grid"], method="ivpq", sparsity=0.7,
                             cdf_threshold_p=0.9, audio_norms=case["nh"], valid=valid,
-                            skip_padded_queries=not compute_padded)
+                            skip_padded_queries=compute_padded is False)
     src, inv = O.rearrange_index(ref["shape_ids"], case["grid"])
     tof = (lambda a: O.bf16_bits_to_f32(a)) if case["qh"].dtype == np.uint16 else (lambda a: O.bf16_bits_to_f32(bf16(a)))
     qf, kf, vf = (tof(case[n])[:, :, src].reshape(B * H, S, D) for n in ("qh", "kh", "vh"))
@@ -409,10 +417,11 @@ def test_end_to_end_autograd(case, compute_padded):
     o_ref, lse_ref = O.attn_fwd(qf, kf, vf, ref["qstart"], ref["qlen"], ref["qcols"], kv, sm)
     tdt = torch.bfloat16 if case["qh"].dtype == np.uint16 else torch.float32
     q, k, v = (dev(case[n]).requires_grad_(True) for n in ("qh", "kh", "vh"))
+    kw = {} if compute_padded is None else {"compute_padded_queries": compute_padded}
     out, sid = flash_attn_bsa_3d_dynamic(q, k, v, case["grid"], method="ivpq", sparsity=0.7, cdf_threshold=0.9,
                                          audio_token_norms=None if case["nh"] is None else dev(case["nh"]),
                                          valid_mask=None if valid is None else dev(valid).bool(),
-                                         return_shape_ids=True, compute_padded_queries=compute_padded)
+                                         return_shape_ids=True, **kw)
     assert out.dtype == tdt
     assert np.array_equal(host(sid), ref["shape_ids"])
     og = out.detach().float().cpu().numpy().reshape(B * H, S, D)

@@ -177,12 +177,13 @@ def test_flash_attn_bsa_3d_vs_oracle(ucase):
             x *= valid[None, None, :, None]
         qkv.append(bf16(x) if dt == "bf16" else x)
     qh, kh, vh = qkv
+    # flash_attn_bsa_3d attends for fully padded query tiles by default, as the reference does
     ref = O.uniform_pipeline(_f(qh), _f(kh), grid, grid, cq, ck, sparsity=sp, cdf_threshold_p=cdf, q_valid=valid,
-                             k_valid=valid, skip_padded_queries=True)
+                             k_valid=valid, skip_padded_queries=False)
     vm = None if valid is None else dev(valid).bool()
     lq, lk = ops.ChunkLayout(grid, cq, DEV), ops.ChunkLayout(grid, ck, DEV)
     plan = plan_chunked(dev(qh), dev(kh), dev(vh), lq, lk, sparsity=sp, cdf_threshold=cdf, sm_scale=1 / math.sqrt(D),
-                        q_valid=vm, k_valid=vm)
+                        q_valid=vm, k_valid=vm, compute_padded_queries=True, keep_scores=True)
     assert bits_equal(host(plan.scores), ref["scores"])
     _check_lists(plan, ref, B * H)
     _run_and_compare(qh, kh, vh, lambda q, k, v: flash_attn_bsa_3d(q, k, v, grid, grid, sparsity=sp, cdf_threshold=cdf,
@@ -217,7 +218,7 @@ def test_flash_attn_bsa_cross_vs_oracle(ccase):
     ref = O.uniform_pipeline(_f(qh), _f(kh), qgrid, kgrid, chq, chk, sparsity=sp, q_pad_rows=lq.rows,
                              k_pad_rows=lk.rows, skip_padded_queries=True)
     plan = plan_chunked(dev(qh), dev(kh), dev(vh), lq, lk, sparsity=sp, cdf_threshold=None,
-                        sm_scale=1 / math.sqrt(D))
+                        sm_scale=1 / math.sqrt(D), keep_scores=True)
     assert bits_equal(host(plan.scores), ref["scores"])
     _check_lists(plan, ref, B * H)
     kw = dict(q_grid_size=qshape if qs == "3d" else None, k_grid_size=kshape if ks == "3d" else None, sparsity=sp)
@@ -243,7 +244,7 @@ def test_flash_attn_bsa_block_order_chunk128_kvmask():
     kv = (rng.random(S) > 0.1).astype(np.uint8)
     kv[256:384] = 0  # one fully padded chunk
     ref = O.uniform_pipeline(_f(qh), _f(kh), (1, 1, S), (1, 1, S), (1, 1, 128), (1, 1, 128), sparsity=0.5,
-                             cdf_threshold_p=0.85, q_valid=kv, k_valid=kv, skip_padded_queries=True)
+                             cdf_threshold_p=0.85, q_valid=kv, k_valid=kv, skip_padded_queries=False)
     sm = 1 / math.sqrt(D)
     _run_and_compare(qh, kh, vh, lambda q, k, v: flash_attn_bsa(q, k, v, 128, 128, 0.5, 0.85, sm,
                                                                 kv_valid_mask=dev(kv).bool()),
