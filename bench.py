@@ -124,69 +124,189 @@ def make_inputs(cfg_name, seed=0, device="cuda"):
 
 # ------------------------------------------------------------------ timing helpers
 def time_region(fn, steps, warmup):
+    """warmup untimed calls, then steps timed calls each bracketed by HIP
+    events on the current stream.  Returns (mean ms, median ms, wall ms per
+    call)."""
+    import statistics
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    st = torch.cuda.Event(enable_timing=True)
-    en = torch.cuda.Event(enable_timing=True)
-    st.record()
-    for _ in range(steps):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in ev:
+        a.record()
         fn()
-    en.record()
+        b.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return st.elapsed_time(en) / steps, wall / steps * 1e3
+    per = [a.elapsed_time(b) for a, b in ev]
+    return sum(per) / steps, statistics.median(per), wall / steps * 1e3
 
 
-# ------------------------------------------------------------------ CPU baseline (oracle)
-def cpu_baseline(plan, inp, budget_s=12.0):
-    """float64 numpy oracle attention fwd+bwd on a seeded sample of query
-    tiles of the same plan, reported as kept-block TFLOP/s."""
-    import numpy as np
-    from oracle import oracle as O
-    B, H, S, D = plan.B, plan.H, plan.S, plan.D
-    Nt = plan.lay.Nt
-    qlen = plan.qlen.cpu().numpy()
-    qstart = plan.qstart.cpu().numpy()
-    qcols = plan.qcols.cpu().numpy()
-    rng = np.random.default_rng(0)
-    rows = rng.permutation(np.nonzero(qlen > 0)[0])
-    tof = lambda t: t.float().cpu().numpy().reshape(B * H, S, D)
-    q, k, v = tof(plan.q_re), tof(plan.k_re), tof(plan.v_re)
-    sm = 1 / math.sqrt(D)
-    done_pairs, t_used, n_rows = 0, 0.0, 0
-    for r in rows:
-        bh, t = divmod(int(r), Nt)
-        n = int(qlen[r])
+DENSE_STEPS, DENSE_WARMUP = 10, 3  # torch SDPA comparison: median of 10 after 3 warm-ups
+
+
+# ------------------------------------------------------------------ CPU baseline
+def _host_threads() -> int:
+    """Host threads for the CPU baseline: every core this process may use
+    (the CPU share OMP_NUM_THREADS states on a GPU box, else os.cpu_count)."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        pass
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _pad_host(x, grid, gp):
+    """[B,H,S,D] (or [S]) THW of grid on the GPU -> float32 host tensor over
+    the zero-padded zone grid gp (the padding of wan_video_dit.py:342-400)."""
+    import torch
+    T, Hg, Wg = grid
+    if x.dim() == 1:
+        out = torch.zeros(gp, device=x.device, dtype=torch.float32)
+        out[:T, :Hg, :Wg] = x.view(T, Hg, Wg).float()
+        return out.reshape(-1).cpu()
+    B, H, S, D = x.shape
+    out = torch.zeros((B, H, *gp, D), device=x.device, dtype=torch.float32)
+    out[:, :, :T, :Hg, :Wg] = x.view(B, H, T, Hg, Wg, D).float()
+    return out.view(B, H, -1, D).cpu()
+
+
+def cpu_c1_end_to_end(seed=0):
+    """Config 1 through the whole CPU path (oracle/torch_path.py), forward and
+    backward: B=1, H=4, D=64, fp32, grid 4x16x16 padded to 8x16x16, 64 audio
+    tokens, top-8 blocks + p = 0.9.  Returns (ms, kept tile pairs)."""
+    import torch
+    from oracle import torch_path as TP
+    g = torch.Generator().manual_seed(seed)
+    grid, gp, H, D = (4, 16, 16), (8, 16, 16), 4, 64
+    S, Sp = 4 * 16 * 16, 8 * 16 * 16
+    valid = torch.zeros(gp, dtype=torch.bool)
+    valid[:4] = True
+    valid = valid.reshape(-1)
+    pad = lambda x: torch.cat([x, torch.zeros(*x.shape[:-2], Sp - S, x.shape[-1])], dim=-2)
+    q, k, v, do = (pad(torch.randn(1, H, S, D, generator=g)) for _ in range(4))
+    # A2V residual of 64 audio tokens: cross-attention of the video queries
+    # (heads concatenated, C = 256) over audio keys/values; its per-token norms
+    qv = q[0, :, :S].transpose(0, 1).reshape(S, H * D)
+    ka, va = torch.randn(64, H * D, generator=g), torch.randn(64, H * D, generator=g)
+    res = torch.softmax(qv @ ka.T / math.sqrt(H * D), dim=-1) @ va
+    norms = torch.cat([res.norm(dim=-1), torch.zeros(Sp - S)])
+    sid = TP.zone_shapes(v, norms, gp, valid)
+    N_b = TP.block_maps(sid)[2]
+    sp = 1.0 - (8 + 0.5) / N_b
+    t0 = time.perf_counter()
+    out = TP.forward_backward(q, k, v, do, gp, sparsity=sp, cdf_threshold=0.9, norms=norms, valid=valid)
+    ms = (time.perf_counter() - t0) * 1e3
+    return ms, int(out[4]["lens"].sum())
+
+
+def cpu_baseline(inp, sparsity, cdf, budget_s=12.0):
+    """The reference's pure-PyTorch path (block-mask selection + masked SDPA)
+    restated in torch float32 (oracle/torch_path.py), timed on the host cores
+    on the same inputs: zone statistics and shapes, rearrangement + pooling,
+    and scores + selection + tile lists at full size; the masked SDPA forward
+    + backward (dense over every key of the head, as masked SDPA computes it)
+    on seeded query tiles for about budget_s seconds, extrapolated to every
+    query tile; config 1 end to end.  value = the step's kept-block FLOPs
+    ((4 + 10) 64 64 D sum_lens, the GPU line's convention) / the
+    extrapolated CPU step time."""
+    import torch
+    from oracle import torch_path as TP
+    from prism_amd import a2v_token_norms
+    from prism_amd.adapter import padded_grid, valid_mask_for
+    threads = _host_threads()
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        grid = inp["grid"]
+        gp, _ = padded_grid(grid)
+        B, H, D = inp["B"], inp["H"], inp["D"]
+        with torch.no_grad():
+            q, k, v, do = (_pad_host(inp[n], grid, gp) for n in ("q", "k", "v", "do"))
+            norms = _pad_host(a2v_token_norms(inp["res"]), grid, gp)
+        valid = valid_mask_for(grid, "cpu")
+        sm = 1.0 / math.sqrt(D)
+        st = {}
         t0 = time.perf_counter()
-        # one query tile against its listed key tiles: tile 0 holds the
-        # queries, tiles 1..n the keys/values, and only tile 0 has a list
-        keys = O._row_keys(qcols, int(qstart[r]), n)
-        Sx = 64 * (n + 1)
-        qx = np.zeros((1, Sx, D), np.float32)
-        kx = np.zeros((1, Sx, D), np.float32)
-        vx = np.zeros((1, Sx, D), np.float32)
-        qx[0, :64] = q[bh, t * 64:(t + 1) * 64]
-        kx[0, 64:] = k[bh, keys]
-        vx[0, 64:] = v[bh, keys]
-        st = np.zeros(n + 1, np.int64)
-        ln = np.zeros(n + 1, np.int32)
-        ln[0] = n
-        cols = np.arange(1, n + 1, dtype=np.int32)
-        o, lse = O.attn_fwd(qx, kx, vx, st, ln, cols, None, sm)
-        O.attn_bwd(qx, kx, vx, o, np.ones_like(o), lse, st, ln, cols, None, sm)
-        t_used += time.perf_counter() - t0
-        done_pairs += n
-        n_rows += 1
-        if t_used > budget_s:
-            break
-    flops = 14 * 64 * 64 * D * done_pairs
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": flops / t_used / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"float64 numpy oracle attention fwd+bwd on {n_rows} random query tiles "
-                      f"({done_pairs} kept tile pairs) of the same plan, {t_used:.1f} s"}
+        sid = TP.zone_shapes(v, norms, gp, valid)
+        st["zone_stats_shapes"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        src, _ = TP.rearrange_index(sid, gp)
+        bid, kbt, N_b = TP.block_maps(sid)
+        q_re, k_re, v_re = (x.index_select(2, src) for x in (q, k, v))
+        do_re = do.index_select(2, src)
+        valid_re = None if valid is None else valid[src]
+        qm, _, tcount = TP.block_means(q_re, valid_re, bid, N_b)
+        km, bcount, _ = TP.block_means(k_re, valid_re, bid, N_b)
+        st["rearrange_pool"] = time.perf_counter() - t0
+        Nt = q.shape[2] // 64
+        t0 = time.perf_counter()
+        tiles, lens = [], []
+        for h in range(H):
+            s = qm[:, h] @ km[:, h].transpose(-1, -2)
+            if valid is not None:
+                s = s.masked_fill((bcount == 0)[None, None, :], float("-inf"))
+            sel = TP.select_blocks(s.reshape(-1, N_b), sparsity, cdf, sm).clamp(max=N_b)
+            t, n = TP.tile_lists(sel, kbt, tcount if valid is not None else None, Nt)
+            tiles.append(t.view(B, N_b, -1)[:, bid])
+            lens.append(n.view(B, N_b)[:, bid])
+            del s, sel
+        tiles, lens = torch.stack(tiles, 1), torch.stack(lens, 1)
+        st["scores_select_lists"] = time.perf_counter() - t0
+        sum_lens = int(lens.sum())
+        # masked SDPA on seeded query tiles of the same plan
+        gen = torch.Generator().manual_seed(0)
+        order = torch.randperm(B * H * Nt, generator=gen)
+        used, n_tiles, pairs = 0.0, 0, 0
+        for r in order.tolist():
+            b, rem = divmod(r, H * Nt)
+            h, t = divmod(rem, Nt)
+            rows = slice(t * 64, (t + 1) * 64)
+            t0 = time.perf_counter()
+            mask = TP.token_mask(tiles[b, h, t], lens[b, h, t], Nt, valid_re)
+            TP.masked_attention(q_re[b, h, rows][None], k_re[b, h][None], v_re[b, h][None], mask[None],
+                                do_re[b, h, rows][None])
+            used += time.perf_counter() - t0
+            n_tiles += 1
+            pairs += int(lens[b, h, t])
+            if used > budget_s:
+                break
+        attn_s = used / n_tiles * (B * H * Nt)
+        total_s = sum(st.values()) + attn_s
+        c1_ms, c1_pairs = cpu_c1_end_to_end()
+    finally:
+        torch.set_num_threads(prev_threads)
+    flops = 14 * 64 * 64 * D * sum_lens
+    return {"value": flops / total_s / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "ms_per_step_extrapolated": round(total_s * 1e3, 1),
+            "stages_ms": {k_: round(v_ * 1e3, 1) for k_, v_ in st.items()},
+            "attention_ms_extrapolated": round(attn_s * 1e3, 1),
+            "sum_lens": sum_lens,
+            "c1_end_to_end_ms": round(c1_ms, 1), "c1_kept_tile_pairs": c1_pairs,
+            "sample": (f"torch float32 restatement of the reference's CPU path on {threads} host threads: zone "
+                       f"statistics + shapes, rearrangement + pooling, scores + selection + tile lists at full "
+                       f"size (measured); masked SDPA fwd+bwd dense over all {q.shape[2]} keys of the head for "
+                       f"{n_tiles} random query tiles ({pairs} kept tile pairs, {used:.1f} s), extrapolated to all "
+                       f"{B * H * Nt} query tiles (extrapolated); config 1 end to end {c1_ms:.0f} ms")}
 
 
 # ------------------------------------------------------------------ HBM traffic
@@ -275,7 +395,8 @@ def main():
                     help="C5: density sweep on the config's shapes (one JSON line of its own, not the headline)")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--cpu-budget", type=float, default=8.0,
+                    help="seconds of sampled masked-SDPA work in the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run one plain device copy of 2 GiB (reference dispatch for the HBM counters)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CALIB_FETCH_CSV", "CALIB_WRITE_CSV"),
@@ -345,14 +466,19 @@ def main():
     with ops.kernel_timing() as tm:
         st = torch.cuda.Event(enable_timing=True)
         en = torch.cuda.Event(enable_timing=True)
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
         t0 = time.perf_counter()
         st.record()
-        for _ in range(args.steps):
+        marks[0].record()
+        for i in range(args.steps):
             step()
+            marks[i + 1].record()
         en.record()
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - t0) / args.steps * 1e3
     ms = st.elapsed_time(en) / args.steps
+    import statistics
+    ms_median = statistics.median(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
     kt = ops.summarize(tm)  # name -> (launches, average ms per launch)
 
     # the plan of these inputs (deterministic: identical to the one inside each step)
@@ -415,18 +541,19 @@ def main():
             o.backward(do)
 
         try:
-            dms, _ = time_region(dstep, 2, 1)
+            dmean, dms, _ = time_region(dstep, DENSE_STEPS, DENSE_WARMUP)
             dense = {"impl": "torch SDPA (ROCm) fwd+bwd, same shape, unpadded", "ms": round(dms, 2),
+                     "ms_mean": round(dmean, 2), "timing": f"median of {DENSE_STEPS} after {DENSE_WARMUP} warm-ups",
                      "tflops": round(14 * S * S * D * B * H / (dms * 1e-3) / 1e12, 1),
-                     "speedup_sparse_vs_dense": round(dms / ms, 2)}
+                     "speedup_sparse_vs_dense": round(dms / ms_median, 2)}
         except Exception as e:  # report, do not fail the bench
             dense = {"error": repr(e)[:200]}
         del qd, kd, vd
 
     cpu = None
     if not args.no_cpu:
-        log("[bench] CPU oracle baseline")
-        cpu = cpu_baseline(plan, inp, args.cpu_budget)
+        log("[bench] CPU baseline (the reference's torch path, float32, host cores)")
+        cpu = cpu_baseline(inp, sparsity, cdf, args.cpu_budget)
 
     value = kept_flops / (ms * 1e-3) / 1e12
     rec = {
@@ -439,6 +566,7 @@ def main():
                    "sparsity": sparsity, "N_b": Nb, "sum_lens": sum_lens, "density": round(density, 4),
                    "density_valid_q": round(density_valid, 4), "pair_union_efficiency": round(union_eff, 4),
                    "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3),
+                   "ms_per_step_median": round(ms_median, 3),
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "dense": dense, "breakdown": breakdown,
@@ -485,7 +613,7 @@ def run_sweep(args, inp):
             out.backward(do)
 
         log(f"[sweep] density {d}: k={kk} of N_b={N_b}")
-        ms, _ = time_region(step, args.steps, args.warmup)
+        ms, _, _ = time_region(step, args.steps, args.warmup)
         with torch.no_grad():
             plan = plan_dynamic(q.detach(), k.detach(), v.detach(), gp, method="ivpq", sparsity=sp,
                                 cdf_threshold=None, shape_ids=sid, input_grid=grid)
@@ -506,7 +634,7 @@ def run_sweep(args, inp):
         o.backward(do)
 
     log("[sweep] dense SDPA")
-    dms, _ = time_region(dstep, 2, 1)
+    _, dms, _ = time_region(dstep, DENSE_STEPS, DENSE_WARMUP)
     # the sparse step's time grows with density; first density where it is no
     # longer faster than dense, linearly interpolated (None: faster everywhere)
     cross = None
