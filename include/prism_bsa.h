@@ -192,6 +192,20 @@ int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int3
                           int64_t Ntk, uint32_t* bitmap, int64_t kcap, int64_t* kstart, int32_t* klen,
                           int32_t* kcols, hipStream_t stream);
 
+/* prism_transpose_lists without the bitmap argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * bitmap lives in a library-owned device workspace of 2^21 uint32 words (8 MiB
+ * per GPU, held until the process ends); heads are processed in batches that
+ * fit it, and one head's bitmap (Ntk * ceil(Ntq / 32) words) must fit
+ * (else PRISM_EINVAL).  The call allocates nothing.  Every call on a GPU uses
+ * that GPU's one workspace: calls that overlap on one GPU (different streams
+ * or threads) race and must be serialised by the caller.  Outputs as
+ * prism_transpose_lists. */
+int prism_transpose_lists_noalloc(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH,
+                                  int64_t Ntq, int64_t Ntk, int64_t kcap, int64_t* kstart, int32_t* klen,
+                                  int32_t* kcols, hipStream_t stream);
+
 /* ------------------------------------------------------------------ attention */
 
 /* Work lists of the paired-tile attention kernels.  Every attention kernel runs

@@ -37,6 +37,7 @@ SIGNATURES = {
     "prism_select_tiles": [P, I64, I64, I32, I64, I64, F32, U64, P, P, I64, P, P, P, I64, P, P],
     "prism_tile_rows": [P, P, P, I32, I64, I64, I64, P, P, P],
     "prism_transpose_lists": [P, P, P, I32, I64, I64, P, I64, P, P, P, P],
+    "prism_transpose_lists_noalloc": [P, P, P, I32, I64, I64, I64, P, P, P, P],
     "prism_pair_union": [P, P, P, I64, I64, I64, P, P, I64, P, P, P, P],
     "prism_pair_tiles": [P, P, P, I64, I64, I64, P, P],
     "prism_pair_order": [P, I64, I32, I64, P, P],

@@ -12,6 +12,8 @@
 //   tile_rows_kernel     q-tile rows share their q-block's list (:315-318)
 //   transpose kernels    create_indices_k_from_indices_q_varlen (bsa_interface.py:147-161)
 //                        as a bitmap transpose instead of a dense N_tiles^2 mask + sort
+//                        (prism_transpose_lists_noalloc: the same kernels with the
+//                        bitmap in a file-scope device workspace)
 //
 // Canonical arithmetic (compiled with -ffp-contract=off):
 //   score   = fmaf chain over d ascending, from +0;
@@ -23,6 +25,8 @@
 // (four 8-bit digits, LDS histograms) on the fp32 bit pattern of w
 // (order-preserving for w >= 0) with exact integer sums, so the result does
 // not depend on thread order.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -438,14 +442,17 @@ __global__ __launch_bounds__(256) void set_bits_col_kernel(const int64_t* __rest
   for (int64_t k = threadIdx.x; k < Ntk; k += blockDim.x) bm[(bh * Ntk + k) * words + w] = col[k];
 }
 
-// one wave per k row: emit the set bits (ascending q tiles)
+// one wave per k row: emit the set bits (ascending q tiles); bitmap row r is
+// output row row0 + r
 __global__ __launch_bounds__(256) void emit_bits_kernel(const uint32_t* __restrict__ bm, int64_t rows,
-                                                        int64_t words, int64_t kcap, int64_t* __restrict__ kstart,
-                                                        int32_t* __restrict__ klen, int32_t* __restrict__ kcols) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+                                                        int64_t words, int64_t kcap, int64_t row0,
+                                                        int64_t* __restrict__ kstart, int32_t* __restrict__ klen,
+                                                        int32_t* __restrict__ kcols) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const uint32_t* w = bm + row * words;
+  if (r >= rows) return;
+  const uint32_t* w = bm + r * words;
+  const int64_t row = row0 + r;
   int32_t* out = kcols + row * kcap;
   uint32_t carry = 0;
   for (int64_t base = 0; base < words; base += 64) {
@@ -465,6 +472,61 @@ __global__ __launch_bounds__(256) void emit_bits_kernel(const uint32_t* __restri
     kstart[row] = row * kcap;
     klen[row] = (int32_t)carry;
   }
+}
+
+// The list transpose of heads [bh0, bh0 + nbh) through the bitmap bm (rows
+// of those heads only): bits set per bitmap column in LDS when the key tiles
+// fit (nothing to clear), else zero-filled and set with global atomics.
+void launch_transpose(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int bh0, int nbh,
+                      int64_t Ntq, int64_t Ntk, uint32_t* bm, int64_t kcap, int64_t* kstart, int32_t* klen,
+                      int32_t* kcols, hipStream_t stream) {
+  const int64_t words = (Ntq + 31) / 32, krows = (int64_t)nbh * Ntk;
+  const int64_t* qs = qstart + (int64_t)bh0 * Ntq;  // entries of qstart are absolute offsets into qcols
+  const int32_t* ql = qlen + (int64_t)bh0 * Ntq;
+  if (Ntk <= kColMaxTiles) {
+    set_bits_col_kernel<<<dim3((unsigned)words, (unsigned)nbh), 256, (size_t)Ntk * 4, stream>>>(qs, ql, qcols, Ntq,
+                                                                                              Ntk, words, bm);
+  } else {
+    fill_u32_kernel<<<1024, 256, 0, stream>>>(bm, krows * words, 0u);
+    set_bits_kernel<<<(unsigned)((int64_t)nbh * Ntq), 64, 0, stream>>>(qs, ql, qcols, Ntq, Ntk, words, bm);
+  }
+  emit_bits_kernel<<<(unsigned)((krows + 3) / 4), 256, 0, stream>>>(bm, krows, words, kcap, (int64_t)bh0 * Ntk, kstart,
+                                                                    klen, kcols);
+}
+
+// Workspace of prism_transpose_lists_noalloc: the bitmap of as many heads as
+// fit, in a file-scope device array instead of caller memory.  Each GPU the
+// library runs on holds its own copy (8 MiB) until the process ends; host
+// code reaches it only through the address hipGetSymbolAddress returns for
+// the current device (scratch_device_ptr), never through the name.
+constexpr int64_t kScratchWords = (int64_t)1 << 21;
+static __device__ __align__(256) uint32_t scratch[kScratchWords];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint32_t* g_scratch_ptr[kMaxDevices] = {};
+
+// device address of `scratch` on the current device (looked up once per device)
+int scratch_device_ptr(uint32_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    prism_set_error("prism_transpose_lists_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return PRISM_EHIP;
+  }
+  PRISM_REQUIRE(dev >= 0 && dev < kMaxDevices, "prism_transpose_lists_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      prism_set_error("prism_transpose_lists_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+      return PRISM_EHIP;
+    }
+    g_scratch_ptr[dev] = (uint32_t*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PRISM_OK;
 }
 
 }  // namespace
@@ -528,17 +590,34 @@ int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int3
   PRISM_REQUIRE(qstart && qlen && qcols && bitmap && kstart && klen && kcols, "prism_transpose_lists: null pointer");
   PRISM_REQUIRE(Ntq >= 1 && Ntk >= 1, "prism_transpose_lists: empty tile range");
   PRISM_REQUIRE(kcap >= Ntq, "prism_transpose_lists: kcap must be >= Ntq");
-  const int64_t qrows = (int64_t)BH * Ntq, krows = (int64_t)BH * Ntk, words = (Ntq + 31) / 32;
-  if (qrows == 0) return PRISM_OK;
-  if (Ntk <= kColMaxTiles) {
-    set_bits_col_kernel<<<dim3((unsigned)words, (unsigned)BH), 256, (size_t)Ntk * 4, stream>>>(qstart, qlen, qcols, Ntq,
-                                                                                            Ntk, words, bitmap);
-  } else {
-    fill_u32_kernel<<<1024, 256, 0, stream>>>(bitmap, krows * words, 0u);
-    set_bits_kernel<<<(unsigned)qrows, 64, 0, stream>>>(qstart, qlen, qcols, Ntq, Ntk, words, bitmap);
-  }
-  emit_bits_kernel<<<(unsigned)((krows + 3) / 4), 256, 0, stream>>>(bitmap, krows, words, kcap, kstart, klen, kcols);
+  if (BH <= 0) return PRISM_OK;
+  launch_transpose(qstart, qlen, qcols, 0, BH, Ntq, Ntk, bitmap, kcap, kstart, klen, kcols, stream);
   PRISM_LAUNCH_CHECK("prism_transpose_lists");
+  return PRISM_OK;
+}
+
+int prism_transpose_lists_noalloc(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH,
+                                  int64_t Ntq, int64_t Ntk, int64_t kcap, int64_t* kstart, int32_t* klen,
+                                  int32_t* kcols, hipStream_t stream) {
+  PRISM_REQUIRE(qstart && qlen && qcols && kstart && klen && kcols, "prism_transpose_lists_noalloc: null pointer");
+  PRISM_REQUIRE(Ntq >= 1 && Ntk >= 1, "prism_transpose_lists_noalloc: empty tile range");
+  PRISM_REQUIRE(kcap >= Ntq, "prism_transpose_lists_noalloc: kcap must be >= Ntq");
+  const int64_t per_head = Ntk * ((Ntq + 31) / 32);  // bitmap words of one head
+  PRISM_REQUIRE(per_head <= kScratchWords,
+                "prism_transpose_lists_noalloc: one head's bitmap (%lld key tiles x %lld words) exceeds the "
+                "%lld-word workspace; use prism_transpose_lists with a caller workspace",
+                (long long)Ntk, (long long)((Ntq + 31) / 32), (long long)kScratchWords);
+  if (BH <= 0) return PRISM_OK;
+  uint32_t* ws = nullptr;
+  const int rc = scratch_device_ptr(&ws);
+  if (rc != PRISM_OK) return rc;
+  // heads in batches that fit the workspace, one after the other on `stream`
+  const int per_batch = (int)(kScratchWords / per_head < BH ? kScratchWords / per_head : BH);
+  for (int bh0 = 0; bh0 < BH; bh0 += per_batch) {
+    const int nbh = BH - bh0 < per_batch ? BH - bh0 : per_batch;
+    launch_transpose(qstart, qlen, qcols, bh0, nbh, Ntq, Ntk, ws, kcap, kstart, klen, kcols, stream);
+  }
+  PRISM_LAUNCH_CHECK("prism_transpose_lists_noalloc");
   return PRISM_OK;
 }
 
