@@ -218,16 +218,17 @@ def cpu_c1_end_to_end(seed=0):
     return ms, int(out[4]["lens"].sum())
 
 
-def cpu_baseline(inp, sparsity, cdf, budget_s=12.0):
+def cpu_baseline(inp, sparsity, cdf, budget_s=12.0, step_pairs=None):
     """The reference's pure-PyTorch path (block-mask selection + masked SDPA)
     restated in torch float32 (oracle/torch_path.py), timed on the host cores
     on the same inputs: zone statistics and shapes, rearrangement + pooling,
     and scores + selection + tile lists at full size; the masked SDPA forward
     + backward (dense over every key of the head, as masked SDPA computes it)
     on seeded query tiles for about budget_s seconds, extrapolated to every
-    query tile; config 1 end to end.  value = the step's kept-block FLOPs
-    ((4 + 10) 64 64 D sum_lens, the GPU line's convention) / the
-    extrapolated CPU step time."""
+    query tile; config 1 end to end.  value = the kept-block FLOPs of the
+    GPU step ((4 + 10) 64 64 D step_pairs, the GPU line's convention; the CPU
+    path's own count when step_pairs is None) / the extrapolated CPU step
+    time, i.e. the rate at which the host completes the same step."""
     import torch
     from oracle import torch_path as TP
     from prism_amd import a2v_token_norms
@@ -294,13 +295,13 @@ def cpu_baseline(inp, sparsity, cdf, budget_s=12.0):
         c1_ms, c1_pairs = cpu_c1_end_to_end()
     finally:
         torch.set_num_threads(prev_threads)
-    flops = 14 * 64 * 64 * D * sum_lens
+    flops = 14 * 64 * 64 * D * (sum_lens if step_pairs is None else step_pairs)
     return {"value": flops / total_s / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "cpu_model": _cpu_model(),
             "ms_per_step_extrapolated": round(total_s * 1e3, 1),
             "stages_ms": {k_: round(v_ * 1e3, 1) for k_, v_ in st.items()},
             "attention_ms_extrapolated": round(attn_s * 1e3, 1),
-            "sum_lens": sum_lens,
+            "cpu_path_kept_tile_pairs": sum_lens,  # includes the padded query tiles the reference attends for
             "c1_end_to_end_ms": round(c1_ms, 1), "c1_kept_tile_pairs": c1_pairs,
             "sample": (f"torch float32 restatement of the reference's CPU path on {threads} host threads: zone "
                        f"statistics + shapes, rearrangement + pooling, scores + selection + tile lists at full "
@@ -553,7 +554,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline (the reference's torch path, float32, host cores)")
-        cpu = cpu_baseline(inp, sparsity, cdf, args.cpu_budget)
+        cpu = cpu_baseline(inp, sparsity, cdf, args.cpu_budget, step_pairs=sum_lens)
 
     value = kept_flops / (ms * 1e-3) / 1e12
     rec = {
@@ -736,7 +737,7 @@ def run_uniform(args, inp):
         "config": {"workload": f"{args.config}-uniform: flash_attn_bsa_3d, 4x4x4 chunks (_run_bsa uniform branch)",
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(lq.pgrid), "chunk": list(chunk),
                    "topk": inp["topk"], "cdf_threshold": cdf, "sparsity": sparsity, "N_b": N_b,
-                   "sum_lens": sum_lens, "density": round(sum_lens / (B * H * lq.Nt * lq.Nt), 4),
+                   "cpu_path_kept_tile_pairs": sum_lens,  # includes the padded query tiles the reference attends for "density": round(sum_lens / (B * H * lq.Nt * lq.Nt), 4),
                    "pair_union_efficiency": round(union_eff, 4), "wall_ms_per_step": round(wall_ms, 3),
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},

@@ -113,8 +113,7 @@ def attn_bwd_bsa_varlen(do, q, k, v, o, dq, dk, dv, sm_scale, lse, block_indices
     qstart, qlen, qcols = _lists_from_dense(block_indices, block_indices_lens)
     do = do.to(torch.bfloat16).contiguous()
     o = o.to(torch.bfloat16).contiguous()
-    delta = torch.empty((B, H, S), device=q.device, dtype=torch.float32)
-    ops._call("prism_bwd_preprocess", o.data_ptr(), do.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
+    delta = ops.bwd_preprocess(o, do)
     klists = ops.transpose_lists(qstart, qlen, qcols, B * H, Ntq, Ntk)
     kv = ops._u8(kv_valid_mask)
     tm = ops.tile_masks(kv)

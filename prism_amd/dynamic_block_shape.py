@@ -119,14 +119,7 @@ def compute_effective_gradient(v_headavg_thw_d: torch.Tensor, audio_norms_thw: O
 
 
 def _assign(g: torch.Tensor, rho: torch.Tensor, method: int, tau_128: float, lambda_128: float) -> torch.Tensor:
-    ops._cuda(g, rho)
-    g = g.contiguous().float()
-    rho = rho.contiguous().float()
-    Nz = rho.shape[0]
-    sid = torch.empty(Nz, device=g.device, dtype=torch.int64)
-    ops._call("prism_assign_shapes", g.data_ptr(), rho.data_ptr(), Nz, method, float(tau_128),
-                  float(lambda_128), sid.data_ptr(), ops._stream())
-    return sid
+    return ops.assign_shapes(g, rho, method, tau_128, lambda_128)
 
 
 def select_shapes_ivpq(g: torch.Tensor, rho: torch.Tensor, tau_128: float = 0.15) -> torch.Tensor:

@@ -1,8 +1,10 @@
-"""Tensor-level wrappers over the prism_bsa C-ABI.
+"""Tensor-level wrappers over the prism_bsa kernels.
 
-PyTorch supplies device memory (the caching allocator) and the current HIP
-stream; every computation runs in libprism_bsa.so.  Inputs must be CUDA (HIP)
-tensors; they are made contiguous where the kernels need it.
+Every computation runs in libprism_bsa.so, reached through its PyTorch
+operator registration (torch.ops.prism.*, libprism_torch.so): each operator
+allocates its outputs through the caching allocator and launches on the
+current HIP stream.  Inputs must be GPU tensors; they are made contiguous
+where the kernels need it.
 """
 from __future__ import annotations
 
@@ -11,9 +13,11 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
-from . import _lib
+from . import _lib  # noqa: F401  (the ctypes binding of the same C-ABI, for C-ABI-level callers and tests)
+from . import _torch_ops
 
 F32, BF16 = 0, 1
+_ops = _torch_ops.load()
 _CANDIDATES = 13  # entries of the candidate shape table (dynamic_block_shape.py:6-27)
 
 
@@ -43,20 +47,24 @@ def summarize(timings) -> Dict[str, Tuple[int, float]]:
     return {name: (len(ev), sum(a.elapsed_time(b) for a, b in ev) / len(ev)) for name, ev in timings.items() if ev}
 
 
-def _call(name: str, *args) -> None:
+def _op(name: str, *args):
+    """torch.ops.prism.<name>(*args), timed under kernel_timing() (key
+    "prism_<name>", the C-ABI entry point the operator wraps)."""
+    fn = getattr(_ops, name)
     if _timings is None:
-        _lib.call(name, *args)
-        return
+        return fn(*args)
     st = torch.cuda.Event(enable_timing=True)
     en = torch.cuda.Event(enable_timing=True)
     st.record()
-    _lib.call(name, *args)
+    out = fn(*args)
     en.record()
-    _timings.setdefault(name, []).append((st, en))
+    _timings.setdefault("prism_" + name, []).append((st, en))
+    return out
 
 
-def _p(t: Optional[torch.Tensor]):
-    return None if t is None else t.data_ptr()
+def _opt(t: torch.Tensor) -> Optional[torch.Tensor]:
+    """Empty placeholder outputs of the operators -> None."""
+    return None if t.numel() == 0 and t.dim() == 1 and t.dtype == torch.float32 else t
 
 
 def _code(t: torch.Tensor) -> int:
@@ -94,13 +102,8 @@ def zone_stats(v: torch.Tensor, grid, valid: Optional[torch.Tensor] = None, box=
     B, H, S, D = v.shape
     T, Hg, Wg = _grid(grid)
     Ti, Hi, Wi = _grid(box if box is not None else grid)
-    Nz = (T // 8) * (Hg // 8) * (Wg // 8)
-    packed = torch.empty((Nz, 25 * D), device=v.device, dtype=torch.float32)
-    av = torch.empty((Nz, 24), device=v.device, dtype=torch.uint8)
-    vm = _u8(valid)
-    _call("prism_zone_stats", _p(v), _code(v), H, S, D, _p(vm), T, Hg, Wg, Ti, Hi, Wi, _p(packed), _p(av),
-          _stream())
-    return packed, av
+    _code(v)
+    return _op("zone_stats", v, _u8(valid), [T, Hg, Wg], [Ti, Hi, Wi])
 
 
 def audio_zone_stats(norms: torch.Tensor, grid, valid: Optional[torch.Tensor] = None, box=None):
@@ -108,48 +111,36 @@ def audio_zone_stats(norms: torch.Tensor, grid, valid: Optional[torch.Tensor] = 
     norms = norms.contiguous()
     T, Hg, Wg = _grid(grid)
     Ti, Hi, Wi = _grid(box if box is not None else grid)
-    Nz = (T // 8) * (Hg // 8) * (Wg // 8)
-    abar = torch.empty(Nz, device=norms.device, dtype=torch.float32)
-    vhat = torch.empty((Nz, 3), device=norms.device, dtype=torch.float32)
-    vm = _u8(valid)
-    _call("prism_audio_zone_stats", _p(norms), _code(norms), _p(vm), T, Hg, Wg, Ti, Hi, Wi, _p(abar), _p(vhat),
-          _stream())
-    return abar, vhat
+    _code(norms)
+    return _op("audio_zone_stats", norms, _u8(valid), [T, Hg, Wg], [Ti, Hi, Wi])
 
 
 def zone_gradient(packed: torch.Tensor, axis_valid: torch.Tensor, D: int):
     _cuda(packed, axis_valid)
-    Nz = packed.shape[0]
-    rho_raw = torch.empty(Nz, device=packed.device, dtype=torch.float32)
-    aniso = torch.empty((Nz, 3), device=packed.device, dtype=torch.float32)
-    _call("prism_zone_gradient", _p(packed.contiguous()), _p(axis_valid.contiguous()), Nz, D, _p(rho_raw),
-              _p(aniso), _stream())
-    return rho_raw, aniso
+    return _op("zone_gradient", packed, axis_valid, int(D))
 
 
 def zone_shapes(rho_raw, aniso, abar, vhat, method: str, lambda_a: float, tau_128: float, lambda_128: float):
     if method not in ("ivpq", "penalty"):
         raise ValueError(f"unknown dynamic-block method: {method!r}")
     _cuda(rho_raw, aniso, abar, vhat)
-    Nz = rho_raw.shape[0]
-    dev = rho_raw.device
-    g = torch.empty((Nz, 3), device=dev, dtype=torch.float32)
-    rho = torch.empty(Nz, device=dev, dtype=torch.float32)
-    sid = torch.empty(Nz, device=dev, dtype=torch.int64)
-    _call("prism_zone_shapes", _p(rho_raw), _p(aniso), _p(abar), _p(vhat), Nz, 0 if method == "ivpq" else 1,
-              float(lambda_a), float(tau_128), float(lambda_128), _p(g), _p(rho), _p(sid), _stream())
-    return g, rho, sid
+    return _op("zone_shapes", rho_raw, aniso, abar, vhat, 0 if method == "ivpq" else 1, float(lambda_a),
+               float(tau_128), float(lambda_128))
+
+
+def assign_shapes(g: torch.Tensor, rho: torch.Tensor, method: int, tau_128: float, lambda_128: float) -> torch.Tensor:
+    """select_shapes_ivpq (method 0) / select_shapes_penalty (method 1) on given g, rho."""
+    _cuda(g, rho)
+    return _op("assign_shapes", g.contiguous().float(), rho.contiguous().float(), int(method), float(tau_128),
+               float(lambda_128))
 
 
 def a2v_norms(residual: torch.Tensor) -> torch.Tensor:
     """Per-token L2 norm of batch 0: [B,S,C] (or [S,C]) -> [S] in the input dtype."""
     _cuda(residual)
     r = residual[0] if residual.dim() == 3 else residual
-    r = r.contiguous()
-    S, C = r.shape
-    out = torch.empty(S, device=r.device, dtype=r.dtype)
-    _call("prism_a2v_norms", _p(r), _code(r), S, C, _p(out), _code(out), _stream())
-    return out
+    _code(r)
+    return _op("a2v_norms", r.contiguous())
 
 
 # ------------------------------------------------------------------ geometry
@@ -178,12 +169,7 @@ class ZoneLayout:
             raise ValueError(f"shape_ids must be a 1-D integer tensor of {self.Nz} zone ids for grid {self.grid}, "
                              f"got {shape_ids.dtype} {tuple(shape_ids.shape)}")
         self.shape_ids = shape_ids.contiguous().to(torch.int64)
-        dev = shape_ids.device
-        self.block_offset = torch.empty(self.Nz + 1, device=dev, dtype=torch.int32)
-        self.block_id_of_tile = torch.empty(self.Nt, device=dev, dtype=torch.int32)
-        self.block_first_tile = torch.empty(self.Nt + 1, device=dev, dtype=torch.int32)
-        _call("prism_zone_layout", _p(self.shape_ids), self.Nz, _p(self.block_offset), _p(self.block_id_of_tile),
-                  _p(self.block_first_tile), _stream())
+        self.block_offset, self.block_id_of_tile, self.block_first_tile = _op("zone_layout", self.shape_ids)
         # the one host synchronisation of the path (the reference syncs here too,
         # dynamic_block_attention.py:153): N_b sizes the block tensors; the
         # kernel reports ids outside the candidate table as N_b = -1, before
@@ -196,12 +182,8 @@ class ZoneLayout:
 def rearrange_index(shape_ids: torch.Tensor, grid):
     _cuda(shape_ids)
     T, Hg, Wg = _grid(grid)
-    ZoneLayout(shape_ids, grid)  # validates the ids (count and range) before the kernel reads them
-    S = T * Hg * Wg
-    src = torch.empty(S, device=shape_ids.device, dtype=torch.int64)
-    inv = torch.empty(S, device=shape_ids.device, dtype=torch.int64)
-    _call("prism_rearrange_index", _p(shape_ids.contiguous()), T, Hg, Wg, _p(src), _p(inv), _stream())
-    return src, inv
+    lay = ZoneLayout(shape_ids, grid)  # validates the ids (count and range) before the kernel reads them
+    return _op("rearrange_index", lay.shape_ids, [T, Hg, Wg])
 
 
 def gather_pool(x: torch.Tensor, lay: ZoneLayout, valid: Optional[torch.Tensor] = None, *, rows: bool = True,
@@ -215,30 +197,20 @@ def gather_pool(x: torch.Tensor, lay: ZoneLayout, valid: Optional[torch.Tensor] 
     if S_in != lay.S_in:
         raise ValueError(f"gather_pool: x has {S_in} tokens, the layout's input grid {lay.box} holds {lay.S_in}")
     S = lay.S
-    T, Hg, Wg = lay.grid
-    Ti, Hi, Wi = lay.box
-    dev = x.device
-    out = {}
-    out["rows"] = torch.empty((B, H, S, D), device=dev, dtype=torch.bfloat16) if rows else None
-    out["block_mean"] = torch.empty((B, H, lay.N_b, D), device=dev, dtype=torch.float32) if pool else None
-    if counts:
-        out["block_count"] = torch.empty(lay.N_b, device=dev, dtype=torch.int32)
-        out["tile_count"] = torch.empty(lay.Nt, device=dev, dtype=torch.int32)
-        out["valid_re"] = torch.empty(S, device=dev, dtype=torch.uint8)
-    else:
-        out["block_count"] = out["tile_count"] = out["valid_re"] = None
-    rowdot = None
+    _code(x)
     if dot_with is not None:
         dot_with = dot_with.contiguous()
         if dot_with.dtype != torch.bfloat16 or dot_with.shape != (B, H, S, D):
             raise ValueError("gather_pool: dot_with must be bf16 [B,H,S,D] in tile order")
-        rowdot = torch.empty((B, H, S), device=dev, dtype=torch.float32)
-    out["rowdot"] = rowdot
-    vm = _u8(valid)
-    _call("prism_gather_pool", _p(x), _code(x), B, H, S_in, D, _p(vm), _p(lay.shape_ids), _p(lay.block_offset),
-              T, Hg, Wg, Ti, Hi, Wi, lay.N_b, _p(out["rows"]), _p(out["block_mean"]), _p(out["block_count"]),
-              _p(out["tile_count"]), _p(out["valid_re"]), _p(dot_with), _p(rowdot), _stream())
-    return out
+    res = _op("gather_pool", x, _u8(valid), lay.shape_ids, lay.block_offset, list(lay.grid), list(lay.box), lay.N_b,
+              rows, pool, counts, dot_with)
+    return _gathered(res, rows, pool, counts, dot_with is not None)
+
+
+def _gathered(res, rows, pool, counts, rowdot):
+    keys = ("rows", "block_mean", "block_count", "tile_count", "valid_re", "rowdot")
+    want = (rows, pool, counts, counts, counts, rowdot)
+    return {k: (t if w else None) for k, t, w in zip(keys, res, want)}
 
 
 def scatter_rows(rows: torch.Tensor, lay: ZoneLayout, out_dtype: torch.dtype) -> torch.Tensor:
@@ -248,12 +220,10 @@ def scatter_rows(rows: torch.Tensor, lay: ZoneLayout, out_dtype: torch.dtype) ->
     B, H, S, D = rows.shape
     if S != lay.S:
         raise ValueError(f"scatter_rows: {S} rows, the layout holds {lay.S}")
-    T, Hg, Wg = lay.grid
-    Ti, Hi, Wi = lay.box
-    out = torch.empty((B, H, lay.S_in, D), device=rows.device, dtype=out_dtype)
-    _call("prism_scatter_rows", _p(rows), B, H, lay.S_in, D, _p(lay.shape_ids), T, Hg, Wg, Ti, Hi, Wi, _p(out),
-          _code(out), _stream())
-    return out
+    code = F32 if out_dtype == torch.float32 else BF16 if out_dtype == torch.bfloat16 else None
+    if code is None:
+        raise TypeError(f"prism_amd: unsupported dtype {out_dtype} (float32 or bfloat16)")
+    return _op("scatter_rows", rows, lay.shape_ids, list(lay.grid), list(lay.box), code)
 
 
 class ChunkLayout:
@@ -312,30 +282,17 @@ def chunk_gather_pool(x: torch.Tensor, lay: ChunkLayout, valid: Optional[torch.T
     B, H, S, D = x.shape
     if S != lay.S_in:
         raise ValueError(f"sequence length {S} != grid {lay.grid} ({lay.S_in} tokens)")
-    dev = x.device
-    out = {}
-    out["rows"] = torch.empty((B, H, lay.rows, D), device=dev, dtype=torch.bfloat16) if rows else None
-    out["block_mean"] = torch.empty((B, H, lay.N_b, D), device=dev, dtype=torch.float32) if pool else None
-    if counts:
-        out["block_count"] = torch.empty(lay.N_b, device=dev, dtype=torch.int32)
-        out["tile_count"] = torch.empty(lay.Nt, device=dev, dtype=torch.int32)
-        out["valid_re"] = torch.empty(lay.rows, device=dev, dtype=torch.uint8)
-    else:
-        out["block_count"] = out["tile_count"] = out["valid_re"] = None
-    rowdot = None
+    _code(x)
     if dot_with is not None:
         dot_with = dot_with.contiguous()
         if dot_with.dtype != torch.bfloat16 or dot_with.shape != (B, H, lay.rows, D):
             raise ValueError("chunk_gather_pool: dot_with must be bf16 [B,H,rows,D] in chunk order")
-        rowdot = torch.empty((B, H, lay.rows), device=dev, dtype=torch.float32)
-    out["rowdot"] = rowdot
     vm = _u8(valid)
     if vm is not None and vm.numel() != lay.S_in:
         raise ValueError(f"valid mask has {vm.numel()} entries, grid {lay.grid} has {lay.S_in} tokens")
-    _call("prism_chunk_gather_pool", _p(x), _code(x), B, H, D, _p(vm), *lay.args(), _p(out["rows"]),
-          _p(out["block_mean"]), _p(out["block_count"]), _p(out["tile_count"]), _p(out["valid_re"]), _p(dot_with),
-          _p(rowdot), _stream())
-    return out
+    res = _op("chunk_gather_pool", x, vm, list(lay.grid), list(lay.pgrid), list(lay.chunk), lay.rows, rows, pool,
+              counts, dot_with)
+    return _gathered(res, rows, pool, counts, dot_with is not None)
 
 
 def chunk_scatter_rows(rows: torch.Tensor, lay: ChunkLayout, out_dtype: torch.dtype) -> torch.Tensor:
@@ -346,9 +303,10 @@ def chunk_scatter_rows(rows: torch.Tensor, lay: ChunkLayout, out_dtype: torch.dt
     B, H, R, D = rows.shape
     if R != lay.rows:
         raise ValueError(f"rows per head {R} != layout rows {lay.rows}")
-    out = torch.empty((B, H, lay.S_in, D), device=rows.device, dtype=out_dtype)
-    _call("prism_chunk_scatter_rows", _p(rows), B, H, D, *lay.args(), _p(out), _code(out), _stream())
-    return out
+    code = F32 if out_dtype == torch.float32 else BF16 if out_dtype == torch.bfloat16 else None
+    if code is None:
+        raise TypeError(f"prism_amd: unsupported dtype {out_dtype} (float32 or bfloat16)")
+    return _op("chunk_scatter_rows", rows, list(lay.grid), list(lay.pgrid), list(lay.chunk), code)
 
 
 # ------------------------------------------------------------------ selection
@@ -361,11 +319,7 @@ def block_scores(qc: torch.Tensor, kc: torch.Tensor, block_count: Optional[torch
     BH = qc.numel() // (Nq * D)
     if kc.shape[-1] != D or kc.numel() != BH * Nk * D:
         raise ValueError("block_scores: q and k means must share batch dims and D")
-    qc = qc.contiguous().float()
-    kc = kc.contiguous().float()
-    out = torch.empty((*qc.shape[:-1], Nk), device=qc.device, dtype=torch.float32)
-    _call("prism_block_scores", _p(qc), _p(kc), _p(block_count), BH, Nq, Nk, D, _p(out), _stream())
-    return out
+    return _op("block_scores", qc.contiguous().float(), kc.contiguous().float(), block_count)
 
 
 def cdf_threshold_fixed(p: float) -> int:
@@ -410,15 +364,11 @@ def select_tiles(scores: torch.Tensor, sparsity, cdf_threshold, sm_scale: float,
     mode, k_lo, ub = selection_params(N, sparsity, cdf_threshold)
     width = min(k_lo, N) if mode == 0 else ub
     tcap = max(tiles_per_block * width, 1)
-    dev = scores.device
-    tiles = torch.empty((rows, tcap), device=dev, dtype=torch.int32)
-    ntiles = torch.empty(rows, device=dev, dtype=torch.int32)
-    sel = torch.full((rows, max(width, 1)), N, device=dev, dtype=torch.int32) if want_blocks else None
-    nsel = torch.empty(rows, device=dev, dtype=torch.int32) if want_blocks else None
     thr = cdf_threshold_fixed(cdf_threshold) if mode != 0 else 0
-    _call("prism_select_tiles", _p(scores.contiguous()), rows, N, mode, k_lo, ub, float(sm_scale), thr,
-              _p(block_first_tile), _p(tile_count), tcap, _p(tiles), _p(ntiles), _p(sel), max(width, 1), _p(nsel),
-              _stream())
+    tiles, ntiles, sel, nsel = _op("select_tiles", scores.contiguous(), mode, k_lo, ub, float(sm_scale), thr,
+                                   block_first_tile, tile_count, tcap, max(width, 1), bool(want_blocks))
+    if not want_blocks:
+        sel = nsel = None
     return dict(tiles=tiles, ntiles=ntiles, sel_blocks=sel, nsel=nsel, tcap=tcap, width=width)
 
 
@@ -427,11 +377,7 @@ def tile_rows(ntiles: torch.Tensor, block_id_of_tile: torch.Tensor, BH: int, Nt:
     """Per-query-tile list starts and lengths; tiles whose q_tile_count is 0
     (no valid query token) get empty lists."""
     _cuda(ntiles, block_id_of_tile, q_tile_count)
-    qstart = torch.empty(BH * Nt, device=ntiles.device, dtype=torch.int64)
-    qlen = torch.empty(BH * Nt, device=ntiles.device, dtype=torch.int32)
-    _call("prism_tile_rows", _p(ntiles), _p(block_id_of_tile), _p(q_tile_count), BH, Nt, N_b, tcap, _p(qstart), _p(qlen),
-          _stream())
-    return qstart, qlen
+    return _op("tile_rows", ntiles, block_id_of_tile, q_tile_count, int(BH), int(Nt), int(N_b), int(tcap))
 
 
 def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tensor, BH: int, Nt: int,
@@ -440,15 +386,7 @@ def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tenso
     default Nt) -> per-key-tile ascending query lists."""
     _cuda(qstart, qlen, qcols)
     Ntq, Ntk = int(Nt), int(Nt if Ntk is None else Ntk)
-    dev = qstart.device
-    words = (Ntq + 31) // 32
-    bitmap = torch.empty(BH * Ntk * words, device=dev, dtype=torch.int32)
-    kstart = torch.empty(BH * Ntk, device=dev, dtype=torch.int64)
-    klen = torch.empty(BH * Ntk, device=dev, dtype=torch.int32)
-    kcols = torch.empty(BH * Ntk * Ntq, device=dev, dtype=torch.int32)
-    _call("prism_transpose_lists", _p(qstart), _p(qlen), _p(qcols), BH, Ntq, Ntk, _p(bitmap), Ntq, _p(kstart),
-          _p(klen), _p(kcols), _stream())
-    return kstart, klen, kcols
+    return _op("transpose_lists", qstart, qlen, qcols, int(BH), Ntq, Ntk)
 
 
 # ------------------------------------------------------------------ attention
@@ -458,11 +396,7 @@ def pair_tiles(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt
     maximises the summed list overlap of the pairs.  Returns pairmap [rows]
     int32: pair p of a head is tiles (pairmap[2p], pairmap[2p+1])."""
     _cuda(start, length, cols)
-    rows = start.numel()
-    out = torch.empty(rows, device=start.device, dtype=torch.int32)
-    _call("prism_pair_tiles", _p(start), _p(length), _p(cols), rows, int(Nt), int(Nt if col_tiles is None else col_tiles),
-          _p(out), _stream())
-    return out
+    return _op("pair_tiles", start, length, cols, int(Nt), int(Nt if col_tiles is None else col_tiles))
 
 
 # fraction of an attention launch's workgroups ordered longest-list-first
@@ -478,9 +412,7 @@ def pair_order(ulen: torch.Tensor, group: int, tail_frac: Optional[float] = None
     n = ulen.numel()
     frac = ORDER_TAIL if tail_frac is None else tail_frac
     tail = min(n, 16384, int(n * frac))
-    order = torch.empty(n, device=ulen.device, dtype=torch.int32)
-    _call("prism_pair_order", _p(ulen.contiguous()), n, int(group), tail, _p(order), _stream())
-    return order
+    return _op("pair_order", ulen, int(group), tail)
 
 
 def pair_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt: int,
@@ -492,16 +424,8 @@ def pair_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt
     the listed tiles (default Nt).  Returns (ustart [rows/2] int64,
     ulen [rows/2] int32, ucols int32)."""
     _cuda(start, length, cols, tmasks, pairmap)
-    rows = start.numel()
-    pairs = rows // 2
-    dev = start.device
     ucap = int(Nt if col_tiles is None else col_tiles)
-    ustart = torch.empty(pairs, device=dev, dtype=torch.int64)
-    ulen = torch.empty(pairs, device=dev, dtype=torch.int32)
-    ucols = torch.empty(max(pairs * ucap, 1), device=dev, dtype=torch.int32)
-    _call("prism_pair_union", _p(start), _p(length), _p(cols), rows, int(Nt), ucap, _p(pairmap), _p(tmasks), ucap,
-          _p(ustart), _p(ulen), _p(ucols), _stream())
-    return ustart, ulen, ucols
+    return _op("pair_union", start, length, cols, int(Nt), ucap, pairmap, tmasks)
 
 
 def tile_masks(valid: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
@@ -509,19 +433,12 @@ def tile_masks(valid: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     if valid is None:
         return None
     _cuda(valid)
-    v = _u8(valid)
-    Nt = v.numel() // 64
-    out = torch.empty(Nt, device=v.device, dtype=torch.int64)
-    _call("prism_tile_masks", _p(v), Nt, _p(out), _stream())
-    return out
+    return _op("tile_masks", _u8(valid))
 
 
 def lse_to_m2(lse: torch.Tensor) -> torch.Tensor:
     _cuda(lse)
-    lse = lse.contiguous().float()
-    out = torch.empty_like(lse)
-    _call("prism_lse_to_m2", _p(lse), lse.numel(), _p(out), _stream())
-    return out
+    return _op("lse_to_m2", lse.contiguous().float())
 
 
 def _bf16(t: torch.Tensor, name: str) -> torch.Tensor:
@@ -547,11 +464,7 @@ def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float, qpair: Optional[torch.Tens
     q, k, v = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v")
     B, H, Sq, Sk, D = _attn_shapes(q, k, v)
     ustart, ulen, ucols = qunion
-    o = torch.empty_like(q)
-    lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
-    _call("prism_bsa_fwd", _p(q), _p(k), _p(v), B * H, Sq, Sk, D, _p(tmasks), _p(ustart), _p(ulen), _p(ucols),
-          _p(qpair), _p(qorder), float(sm_scale), _p(o), _p(lse), _stream())
-    return o, lse
+    return _op("bsa_fwd", q, k, v, tmasks, ustart, ulen, ucols, qpair, qorder, float(sm_scale))
 
 
 # dK/dV and dQ are independent: with BWD_CONCURRENT the dK/dV kernel runs on a
@@ -583,30 +496,31 @@ def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: 
     B, H, Sq, Sk, D = _attn_shapes(q, k, v)
     if do.shape != q.shape:
         raise ValueError("do must have q's shape")
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    def dkdv(stream):
-        _call("prism_bsa_bwd_dkdv", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(kv_valid),
-              _p(kunion[0]), _p(kunion[1]), _p(kunion[2]), _p(kpair), _p(korder), float(sm_scale), _p(dk), _p(dv),
-              stream)
+    def dkdv():
+        return _op("bsa_bwd_dkdv", q, k, v, do, m2, delta, kv_valid, kunion[0], kunion[1], kunion[2], kpair, korder,
+                   float(sm_scale))
 
     main = torch.cuda.current_stream()
     if BWD_CONCURRENT:
         side = _side_stream(q.device)
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            dkdv(side.cuda_stream)
+            dk, dv = dkdv()
         # the side stream reads and writes these: the allocator must not hand
         # their memory out again before its work is done
         for t in (q, k, v, do, m2, delta, kv_valid, kunion[0], kunion[1], kunion[2], kpair, korder, dk, dv):
             if t is not None:
                 t.record_stream(side)
     else:
-        dkdv(main.cuda_stream)
-    _call("prism_bsa_bwd_dq", _p(q), _p(k), _p(v), _p(do), _p(m2), _p(delta), B * H, Sq, Sk, D, _p(tmasks),
-          _p(qunion[0]), _p(qunion[1]), _p(qunion[2]), _p(qpair), _p(qorder), float(sm_scale), _p(dq),
-          main.cuda_stream)
+        dk, dv = dkdv()
+    dq = _op("bsa_bwd_dq", q, k, v, do, m2, delta, tmasks, qunion[0], qunion[1], qunion[2], qpair, qorder,
+             float(sm_scale))
     if BWD_CONCURRENT:
         main.wait_stream(side)
     return dq, dk, dv
+
+
+def bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
+    """delta = rowsum(o * do) over the last dim (bf16 inputs, fp32 out)."""
+    _cuda(o, do)
+    return _op("bwd_preprocess", _bf16(o, "o"), _bf16(do, "do"))

@@ -373,8 +373,7 @@ def test_attention_fwd_bwd_tolerance(case):
     rng = np.random.default_rng(99)
     do = bf16(rng.standard_normal((B, H, S, D)).astype(np.float32))
     do_t = dev(do)
-    delta = torch.empty((B, H, S), device=DEV, dtype=torch.float32)
-    ops._lib.call("prism_bwd_preprocess", o.data_ptr(), do_t.data_ptr(), B * H * S, D, delta.data_ptr(), ops._stream())
+    delta = ops.bwd_preprocess(o, do_t)
     klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, plan.lay.Nt)
     kpair = ops.pair_tiles(*klists, plan.lay.Nt)
     kunion = ops.pair_union(*klists, plan.lay.Nt, pairmap=kpair)
