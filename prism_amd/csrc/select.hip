@@ -190,10 +190,26 @@ __device__ __forceinline__ uint32_t radix_search(const uint32_t* key, const uint
     const uint32_t hmask = level == 0 ? 0u : (0xffffffffu << (shift + 8));
     hist[tid] = 0ull;  // kSelThreads == 256 bins
     __syncthreads();
+    // A thread's elements are neighbouring blocks, whose weights mostly share
+    // a digit (at the first level, all of a row's weights share one or two
+    // exponent bytes): runs of one digit are summed in registers and added
+    // with one LDS atomic, instead of one atomic per element on the same
+    // few bins.  Integer sums, so the histogram is the same.
+    uint32_t run_bin = 0xffffffffu;
+    uint64_t run_w = 0;
 #pragma unroll
     for (int e = 0; e < EPT; ++e)
-      if (((present >> e) & 1) && (key[e] & hmask) == prefix)
-        atomicAdd(&hist[(key[e] >> shift) & 255u], WEIGHTED ? (unsigned long long)W[e] : 1ull);
+      if (((present >> e) & 1) && (key[e] & hmask) == prefix) {
+        const uint32_t b = (key[e] >> shift) & 255u;
+        const uint64_t w = WEIGHTED ? W[e] : 1ull;
+        if (b != run_bin) {
+          if (run_bin != 0xffffffffu) atomicAdd(&hist[run_bin], (unsigned long long)run_w);
+          run_bin = b;
+          run_w = 0;
+        }
+        run_w += w;
+      }
+    if (run_bin != 0xffffffffu) atomicAdd(&hist[run_bin], (unsigned long long)run_w);
     __syncthreads();
     // thread t takes bin 255 - t, so its inclusive scan is the weight of the
     // digits >= 255 - t; the first thread whose total reaches thr owns d*

@@ -65,17 +65,27 @@ __global__ __launch_bounds__(kZoneThreads) void zone_stats_kernel(
   const int tid = threadIdx.x;
   const int lt = tid >> 6, lane = tid & 63;
 
+  __shared__ int sPart[8][17];    // per frame t: valid tokens, per h, per w
   {
     const int64_t tok = token_in(z, tid, ZH, ZW, box);
-    sValid[tid] = tok < 0 ? (uint8_t)0 : valid ? valid[tok] : (uint8_t)1;
+    const uint8_t ok = tok < 0 ? (uint8_t)0 : valid ? valid[tok] : (uint8_t)1;
+    sValid[tid] = ok;
+    // wave lt holds frame lt: lane 8 h + w is token (lt, h, w)
+    const uint64_t m = __ballot(ok != 0);
+    if (lane < 17) {
+      const uint64_t sel = lane == 0 ? ~0ull : lane <= 8 ? (0xffull << (8 * (lane - 1)))
+                                                         : (0x0101010101010101ull << (lane - 9));
+      sPart[lt][lane] = __popcll(m & sel);
+    }
   }
   __syncthreads();
   if (tid < 25) {
     int cnt = 0;
-    for (int i = 0; i < 512; ++i) {
-      const int t = i >> 6, h = (i >> 3) & 7, w = i & 7;
-      const int sel = tid < 8 ? (t == tid) : tid < 16 ? (h == tid - 8) : tid < 24 ? (w == tid - 16) : 1;
-      cnt += (sel && sValid[i]) ? 1 : 0;
+    if (tid < 8) {
+      cnt = sPart[tid][0];
+    } else {
+      const int col = tid < 24 ? tid - 7 : 0;  // h = tid - 8 -> column 1 + h; w = tid - 16 -> column 9 + w
+      for (int t = 0; t < 8; ++t) cnt += sPart[t][col];
     }
     sCnt[tid] = cnt;
   }
@@ -92,23 +102,43 @@ __global__ __launch_bounds__(kZoneThreads) void zone_stats_kernel(
     float r[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) r[j] = 0.0f;
+    // the eight tokens of row (lt, lh), two heads per step: sixteen row loads
+    // in flight per wave (positions outside the input grid read as zero); each
+    // token's head sum still runs over h in order from +0
+    int64_t tok[8];
+    float acc[8][CPL];
 #pragma unroll
     for (int lw = 0; lw < 8; ++lw) {
-      const int lf = (lt * 8 + lh) * 8 + lw;
-      const int64_t tok = token_in(z, lf, ZH, ZW, box);
-      const bool ok = sValid[lf] != 0;
-      float acc[CPL];
+      tok[lw] = token_in(z, (lt * 8 + lh) * 8 + lw, ZH, ZW, box);
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
-      for (int h = 0; h < (tok < 0 ? 0 : H); ++h) {
-        float x[CPL];
-        load_chan<T, CPL>(v + ((int64_t)h * S + tok) * D + lane * CPL, x);
+      for (int j = 0; j < CPL; ++j) acc[lw][j] = 0.0f;
+    }
+    for (int h = 0; h < H; h += 2) {
+      const bool two = h + 1 < H;
+      float x0[8][CPL], x1[8][CPL];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[j] = acc[j] + x[j];
+      for (int lw = 0; lw < 8; ++lw) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x0[lw][j] = x1[lw][j] = 0.0f;
+        if (tok[lw] >= 0) {
+          load_chan<T, CPL>(v + ((int64_t)h * S + tok[lw]) * D + lane * CPL, x0[lw]);
+          if (two) load_chan<T, CPL>(v + ((int64_t)(h + 1) * S + tok[lw]) * D + lane * CPL, x1[lw]);
+        }
       }
 #pragma unroll
+      for (int lw = 0; lw < 8; ++lw)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          acc[lw][j] = acc[lw][j] + x0[lw][j];
+          if (two) acc[lw][j] = acc[lw][j] + x1[lw][j];
+        }
+    }
+#pragma unroll
+    for (int lw = 0; lw < 8; ++lw) {
+      const bool ok = sValid[(lt * 8 + lh) * 8 + lw] != 0;
+#pragma unroll
       for (int j = 0; j < CPL; ++j) {
-        float a = acc[j] * invH;
+        float a = acc[lw][j] * invH;
         if (sizeof(T) == 2) a = round_bf(a);
         r[j] = ok ? r[j] + a : r[j];
         cacc[lw][j] = ok ? cacc[lw][j] + a : cacc[lw][j];
