@@ -394,6 +394,9 @@ def main():
                          "_run_bsa (flash_attn_bsa_3d) on the same inputs and selection parameters")
     ap.add_argument("--sweep", action="store_true",
                     help="C5: density sweep on the config's shapes (one JSON line of its own, not the headline)")
+    ap.add_argument("--bridge", action="store_true",
+                    help="the a2v bridge o-projection with fused residual norms (prism_linear_rownorm) at the "
+                         "config's tokens and C, against torch F.linear + the norm kernel (one JSON line)")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=8.0,
@@ -424,6 +427,9 @@ def main():
     inp = make_inputs(args.config)
     if args.sweep:
         run_sweep(args, inp)
+        return
+    if args.bridge:
+        run_bridge(args, inp)
         return
     if args.path == "uniform":
         run_uniform(args, inp)
@@ -652,6 +658,40 @@ def run_sweep(args, inp):
         "dense": {"impl": "torch SDPA (ROCm) fwd+bwd, same shape, unpadded", "ms": round(dms, 2),
                   "tflops": round(14 * S * S * D * B * H / (dms * 1e-3) / 1e12, 1)},
         "crossover_density": cross}))
+
+
+def run_bridge(args, inp):
+    """The a2v bridge output projection of the config (residual = x W^T + b,
+    interactionv2.py:348; M = video tokens, N = K = C) with the per-token
+    residual norms (wan_video_dit.py:742-752) fused into its epilogue
+    (prism_linear_rownorm), against torch's F.linear (hipBLASLt) followed by
+    prism_a2v_norms: median ms of each, and the fused kernel's bf16 MFMA
+    rate (2 M N K flop)."""
+    import torch
+    from prism_amd import ops
+    S, C = inp["S"], CONFIGS[args.config][5]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(S, C, generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn(C, C, generator=g, device="cuda") / C ** 0.5).to(torch.bfloat16)
+    b = (0.1 * torch.randn(C, generator=g, device="cuda")).to(torch.bfloat16)
+    del inp
+    torch.cuda.empty_cache()
+    steps, warm = max(args.steps, 10), max(args.warmup, 3)
+    with ops.kernel_timing() as tm:
+        fmean, fmed, _ = time_region(lambda: ops.linear_rownorm(x, w, b), steps, warm)
+    kt = ops.summarize(tm)
+    umean, umed, _ = time_region(lambda: ops.a2v_norms(torch.nn.functional.linear(x, w, b)), steps, warm)
+    flop = 2.0 * S * C * C
+    print(json.dumps({
+        "metric": "a2v bridge o-projection + residual norms (fused epilogue) ms",
+        "config": {"workload": f"{args.config}: M={S} video tokens, N=K=C={C}, bf16, bias"},
+        "steps": steps, "warmup": warm, "dtype": "bf16", "data": "synthetic",
+        "fused_ms": round(fmed, 3), "fused_ms_mean": round(fmean, 3),
+        "fused_tflops": round(flop / (fmed * 1e-3) / 1e12, 1),
+        "fused_mfma_frac": round(flop / (fmed * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "unfused_torch_linear_plus_norms_ms": round(umed, 3),
+        "speedup_fused_vs_unfused": round(umed / fmed, 3),
+        "breakdown": {k: {"launches": n // steps, "ms": round(t, 4)} for k, (n, t) in kt.items()}}), flush=True)
 
 
 def run_uniform(args, inp):

@@ -87,6 +87,18 @@ int prism_assign_shapes(const float* g, const float* rho, int Nz, int method, fl
 int prism_a2v_norms(const void* res, int dtype, int64_t S, int C, void* out, int out_dtype,
                     hipStream_t stream);
 
+/* The a2v bridge's output projection with the residual norms of
+ * wan_video_dit.py:742-752 fused into its epilogue: y = x W^T + b
+ * (nn.Linear, ConditionalCrossAttention.o, interactionv2.py:225, :348; the
+ * a2v_bridge_residual of mova.py:127-137) and norms[m] = ||y[m, :]||_2 of the
+ * stored bf16 values.  x: [M, K] bf16, w: [N, K] bf16, bias: [N] bf16 or NULL;
+ * y: [M, N] bf16; norms: [M] of norms_dtype; partial: workspace of
+ * M * (N / 256) floats (per-row sums of squares of each 256-column tile,
+ * added in tile order).  N must be a multiple of 256, K of 64; x and w each
+ * below 4 GiB. */
+int prism_linear_rownorm(const void* x, const void* w, const void* bias, int64_t M, int N, int K, void* y,
+                         void* norms, int norms_dtype, float* partial, hipStream_t stream);
+
 /* ------------------------------------------------------------------ geometry */
 
 /* _build_block_tile_maps (dynamic_block_attention.py:138-170) in CSR form.

@@ -26,6 +26,7 @@ SIGNATURES = {
     "prism_zone_shapes": [P, P, P, P, I32, I32, F32, F32, F32, P, P, P, P],
     "prism_assign_shapes": [P, P, I32, I32, F32, F32, P, P],
     "prism_a2v_norms": [P, I32, I64, I32, P, I32, P],
+    "prism_linear_rownorm": [P, P, P, I64, I32, I32, P, P, I32, P, P],
     "prism_zone_layout": [P, I32, P, P, P, P],
     "prism_rearrange_index": [P, I32, I32, I32, P, P, P],
     "prism_gather_pool": [P, I32, I32, I32, I64, I32, P, P, P, I32, I32, I32, I32, I32, I32, I64, P, P, P, P, P, P, P, P],

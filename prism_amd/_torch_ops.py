@@ -49,7 +49,12 @@ def _zones(grid):
 
 
 def _register_fakes():
-    reg = torch.library.register_fake
+    def reg(qualname):
+        # a library built before an operator was added lacks it: calling it
+        # then fails loudly; its fake is simply not registered
+        if not hasattr(torch.ops.prism, qualname.split("::")[1]):
+            return lambda fn: fn
+        return torch.library.register_fake(qualname)
     f32, bf16, u8, i32, i64 = torch.float32, torch.bfloat16, torch.uint8, torch.int32, torch.int64
 
     @reg("prism::zone_stats")
@@ -79,6 +84,10 @@ def _register_fakes():
     @reg("prism::a2v_norms")
     def _(residual):
         return _empty(residual, (residual.shape[0],), residual.dtype)
+
+    @reg("prism::linear_rownorm")
+    def _(x, weight, bias, norms_dtype):
+        return _empty(x, (x.shape[0], weight.shape[0]), x.dtype), _empty(x, (x.shape[0],), f32 if norms_dtype == 0 else bf16)
 
     @reg("prism::zone_layout")
     def _(shape_ids):

@@ -39,6 +39,21 @@ def a2v_token_norms(a2v_bridge_residual: torch.Tensor) -> torch.Tensor:
         return ops.a2v_norms(a2v_bridge_residual)
 
 
+def a2v_bridge_projection(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
+    """The a2v bridge's output projection with the residual norms fused:
+    residual = x weight^T + bias (ConditionalCrossAttention.o,
+    hymm/models/modules/interactionv2.py:225, :348; the a2v_bridge_residual of
+    mova.py:127-137) and ||residual[0, m, :]||_2 (wan_video_dit.py:742-752)
+    formed in the projection's epilogue instead of a second read of the
+    residual.  x: [B, S, K] or [S, K] bf16; weight: [C, K] bf16; bias: [C]
+    bf16 or None (C a multiple of 256, K of 64).  Returns (residual in x's
+    layout with C channels, norms [S] bf16 of batch 0)."""
+    lead = x.shape[:-1]
+    y, norms = ops.linear_rownorm(x.reshape(-1, x.shape[-1]), weight, bias)
+    S = x.shape[-2] if x.dim() == 3 else x.shape[0]
+    return y.view(*lead, weight.shape[0]), norms[:S]
+
+
 def padded_grid(grid_size):
     T, H, W = grid_size
     pt = (ZONE_SIZE - T % ZONE_SIZE) % ZONE_SIZE

@@ -25,7 +25,8 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 TORCH_OPS_SRC = "torch_ops.cpp"
 TORCH_OPS_PATH = os.path.join(HERE, "libprism_torch.so")
 
-SOURCES = ["errors.hip", "stats.hip", "layout.hip", "select.hip", "lists.hip", "attn_fwd.hip", "attn_bwd.hip"]
+SOURCES = ["errors.hip", "stats.hip", "layout.hip", "select.hip", "lists.hip", "attn_fwd.hip", "attn_bwd.hip",
+           "oproj.hip"]
 CANONICAL = {"stats.hip", "layout.hip", "select.hip"}
 
 COMMON_FLAGS = [

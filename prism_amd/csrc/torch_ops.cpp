@@ -166,6 +166,28 @@ Tensor a2v_norms(const Tensor& res_) {
   return out;
 }
 
+std::tuple<Tensor, Tensor> linear_rownorm(const Tensor& x_, const Tensor& w_, const OptT& bias_, int64_t norms_dtype) {
+  on_gpu(x_, "x");
+  on_gpu(w_, "weight");
+  on_gpu(bias_, "bias");
+  check_dtype(x_, at::kBFloat16, "x");
+  check_dtype(w_, at::kBFloat16, "weight");
+  check_dtype(bias_, at::kBFloat16, "bias");
+  const c10::DeviceGuard guard(x_.device());
+  const Tensor x = x_.contiguous(), w = w_.contiguous();
+  const OptT bias = cont(bias_);
+  TORCH_CHECK_VALUE(x.dim() == 2 && w.dim() == 2 && w.size(1) == x.size(1),
+                    "linear_rownorm: x must be [M, K] and weight [N, K]");
+  if (bias) TORCH_CHECK_VALUE(bias->numel() == w.size(0), "linear_rownorm: bias must have N entries");
+  const int64_t M = x.size(0), N = w.size(0), K = x.size(1);
+  Tensor y = at::empty({M, N}, x.options());
+  Tensor norms = at::empty({M}, opts(x, dtype_of_code(norms_dtype)));
+  Tensor partial = at::empty({M * std::max<int64_t>(N / 256, 1)}, opts(x, at::kFloat));
+  PRISM_TORCH_CALL(prism_linear_rownorm, x.data_ptr(), w.data_ptr(), p(bias), M, (int)N, (int)K, y.data_ptr(),
+                   norms.data_ptr(), (int)norms_dtype, partial.data_ptr<float>(), stream_of(x));
+  return {y, norms};
+}
+
 // ------------------------------------------------------------------ geometry
 std::tuple<Tensor, Tensor, Tensor> zone_layout(const Tensor& sid_) {
   on_gpu(sid_, "shape_ids");
@@ -573,6 +595,7 @@ TORCH_LIBRARY(prism, m) {
         "float tau_128, float lambda_128) -> (Tensor, Tensor, Tensor)");
   m.def("assign_shapes(Tensor g, Tensor rho, int method, float tau_128, float lambda_128) -> Tensor");
   m.def("a2v_norms(Tensor residual) -> Tensor");
+  m.def("linear_rownorm(Tensor x, Tensor weight, Tensor? bias, int norms_dtype) -> (Tensor, Tensor)");
   m.def("zone_layout(Tensor shape_ids) -> (Tensor, Tensor, Tensor)");
   m.def("rearrange_index(Tensor shape_ids, int[] grid) -> (Tensor, Tensor)");
   m.def("gather_pool(Tensor x, Tensor? valid, Tensor shape_ids, Tensor block_offset, int[] grid, int[] box, int N_b, "
@@ -610,6 +633,7 @@ TORCH_LIBRARY_IMPL(prism, CUDA, m) {
   m.impl("zone_shapes", &zone_shapes);
   m.impl("assign_shapes", &assign_shapes);
   m.impl("a2v_norms", &a2v_norms);
+  m.impl("linear_rownorm", &linear_rownorm);
   m.impl("zone_layout", &zone_layout);
   m.impl("rearrange_index", &rearrange_index);
   m.impl("gather_pool", &gather_pool);

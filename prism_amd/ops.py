@@ -143,6 +143,20 @@ def a2v_norms(residual: torch.Tensor) -> torch.Tensor:
     return _op("a2v_norms", r.contiguous())
 
 
+def linear_rownorm(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                   norms_dtype: Optional[torch.dtype] = None):
+    """y = x weight^T + bias (bf16, fp32 accumulate) and the L2 norm of every
+    row of the stored y, fused: [M, K] x [N, K] -> ([M, N], [M]).  N must be a
+    multiple of 256 and K of 64."""
+    _cuda(x, weight, bias)
+    nd = x.dtype if norms_dtype is None else norms_dtype
+    code = F32 if nd == torch.float32 else BF16 if nd == torch.bfloat16 else None
+    if code is None:
+        raise TypeError(f"prism_amd: unsupported dtype {nd} (float32 or bfloat16)")
+    return _op("linear_rownorm", _bf16(x, "x"), _bf16(weight, "weight"), None if bias is None else _bf16(bias, "bias"),
+               code)
+
+
 # ------------------------------------------------------------------ geometry
 class ZoneLayout:
     """Per-call block/tile bookkeeping for one set of shape ids.
