@@ -189,7 +189,8 @@ def _random_scores(rng, rows, N, kind):
 def test_select_bitexact(kind):
     from prism_amd import ops
     rng = np.random.default_rng(11)
-    for N in (37, 300, 1440, 2900):
+    # 8, 16 and 32 elements per thread of the workgroup that takes a row
+    for N in (37, 300, 1440, 2900, 6500):
         rows = 24
         s = _random_scores(rng, rows, N, kind)
         first = np.arange(N + 1, dtype=np.int32)
@@ -202,6 +203,30 @@ def test_select_bitexact(kind):
             got = host(res["sel_blocks"])
             for r in range(rows):
                 assert np.array_equal(got[r, : n[r]], ref_sel[r, : n[r]]), (kind, N, sp, p, r)
+
+
+@pytest.mark.parametrize("N", [300, 5000, 6500])
+def test_select_tile_expansion_any_tile_count(N):
+    """Blocks of 0..4 tiles (the C-ABI takes any block_first_tile) with padded
+    tiles dropped: each row's list is the tiles of its selected blocks, in
+    ascending block order, whose tile_count is non-zero."""
+    from prism_amd import ops
+    rng = np.random.default_rng(5)
+    rows = 16
+    s = _random_scores(rng, rows, N, "plain")
+    per = rng.integers(0, 5, N)
+    first = np.concatenate([[0], np.cumsum(per)]).astype(np.int32)
+    tc = (rng.random(int(first[-1])) > 0.2).astype(np.int32)
+    for sp, p in ((0.9, None), (None, 0.9), (0.5, 0.3)):
+        say("expansion", N, sp, p)
+        ref_sel, ref_n = O.select(s, sp, p, 0.125)
+        res = ops.select_tiles(dev(s), sp, p, 0.125, dev(first), dev(tc), want_blocks=True, tiles_per_block=4)
+        nt, tiles = host(res["ntiles"]), host(res["tiles"])
+        assert np.array_equal(host(res["nsel"]), ref_n)
+        for r in range(rows):
+            want = [t for b in ref_sel[r, : ref_n[r]] for t in range(first[b], first[b + 1]) if tc[t] > 0]
+            assert nt[r] == len(want), (N, sp, p, r)
+            assert np.array_equal(tiles[r, : nt[r]], want), (N, sp, p, r)
 
 
 def test_select_tile_expansion_bitexact(case):

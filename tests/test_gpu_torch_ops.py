@@ -44,6 +44,10 @@ def test_opcheck_statistics_and_geometry(plan):
     g, rho, _ = torch.ops.prism.zone_shapes(rho_raw, aniso, None, None, 0, 0.5, 0.15, 1.0)
     _check("assign_shapes", g, rho, 1, 0.15, 1.0)
     _check("a2v_norms", torch.randn(300, 256, device="cuda", dtype=torch.bfloat16))
+    xb = torch.randn(300, 128, device="cuda", dtype=torch.bfloat16)
+    wt = torch.randn(256, 128, device="cuda", dtype=torch.bfloat16)
+    _check("linear_rownorm", xb, wt, torch.randn(256, device="cuda", dtype=torch.bfloat16), 0)
+    _check("linear_rownorm", xb, wt, None, 1)
     _check("zone_layout", lay.shape_ids)
     _check("rearrange_index", lay.shape_ids, grid)
     _check("gather_pool", v, valid, lay.shape_ids, lay.block_offset, grid, grid, lay.N_b, True, True, True, None)

@@ -10,7 +10,7 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 OPS = ["zone_stats", "audio_zone_stats", "zone_gradient", "zone_shapes", "assign_shapes", "a2v_norms", "zone_layout",
        "rearrange_index", "gather_pool", "scatter_rows", "chunk_gather_pool", "chunk_scatter_rows", "block_scores",
        "select_tiles", "tile_rows", "transpose_lists", "pair_tiles", "pair_union", "pair_order", "tile_masks",
-       "lse_to_m2", "bsa_fwd", "bwd_preprocess", "bsa_bwd_dkdv", "bsa_bwd_dq"]
+       "lse_to_m2", "bsa_fwd", "bwd_preprocess", "bsa_bwd_dkdv", "bsa_bwd_dq", "linear_rownorm"]
 
 
 @pytest.fixture(scope="module")
@@ -42,6 +42,8 @@ def test_fake_shapes(prism):
         g, rho, sid = prism.zone_shapes(_t((Nz,), f32), _t((Nz, 3), f32), None, None, 0, 0.5, 0.15, 1.0)
         assert g.shape == (Nz, 3) and sid.dtype == i64
         assert prism.a2v_norms(_t((Sin, 256), bf)).dtype == bf
+        yb, nb = prism.linear_rownorm(_t((Sin, 128), bf), _t((256, 128), bf), None, 0)
+        assert yb.shape == (Sin, 256) and yb.dtype == bf and nb.shape == (Sin,) and nb.dtype == f32
         boff, bot, bft = prism.zone_layout(_t((Nz,), i64))
         assert boff.shape == (Nz + 1,) and bot.shape == (Nt,) and bft.shape == (Nt + 1,)
         out = prism.gather_pool(v, None, _t((Nz,), i64), boff, grid, box, N_b, True, True, True, None)
