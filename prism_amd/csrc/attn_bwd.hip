@@ -88,7 +88,7 @@ template <int D>
 __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   using T = BwdTiles<D>;
   using RT = typename T::RT;
-  constexpr int P = RT::P, NS = D / 16, NDT = D / 32;
+  constexpr int NS = D / 16, NDT = D / 32;
   constexpr int SB = T::DKDV_STAGE;
   __shared__ __align__(16) uint8_t smem[T::DKDV_LDS];
 
@@ -133,9 +133,9 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
     }
   };
   RowOperand rop;                // Q / dO rows 32 qh + l32
-  rop.init<P>(32 * qh, l32, g);
+  rop.init<RT>(32 * qh, l32, g);
   TrOperand top;                 // Q^T / dO^T over query rows 32 qh .. 32 qh + 31
-  top.init<P>(32 * qh, lane);
+  top.init<RT>(32 * qh, lane);
 
   EntryRing<kStagesDkdv> ring;
   ring.init(U, n);
@@ -208,8 +208,8 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
       const bf16x8 sb = b_from_acc(&pacc, t2);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sDO, t2, dt), pb, dv[dt], 0, 0, 0);
-        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sQ, t2, dt), sb, dk[dt], 0, 0, 0);
+        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<RT>(sDO, t2, dt), pb, dv[dt], 0, 0, 0);
+        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<RT>(sQ, t2, dt), sb, dk[dt], 0, 0, 0);
       }
     }
   }
@@ -256,7 +256,7 @@ template <int D>
 __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   using T = BwdTiles<D>;
   using RT = typename T::RT;
-  constexpr int P = RT::P, NS = D / 16, NDT = D / 32;
+  constexpr int NS = D / 16, NDT = D / 32;
   constexpr int SB = T::DQ_STAGE;
   constexpr int SLOTS = 2 * RT::KB / 4;  // KB-instructions per wave and stage (4 waves)
   __shared__ __align__(16) uint8_t smem[kStagesDq * SB];
@@ -289,9 +289,9 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
     }
   };
   RowOperand rop;  // K / V rows l32 (+ 32 kh as an immediate)
-  rop.init<P>(0, l32, g);
+  rop.init<RT>(0, l32, g);
   TrOperand top;   // K^T over key rows 0 .. 63
-  top.init<P>(0, lane);
+  top.init<RT>(0, lane);
 
   EntryRing<kStagesDq> ring;
   ring.init(U, n);
@@ -337,8 +337,8 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
-        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sK + 32 * kh * P, s), qf[s], sacc[kh], 0, 0, 0);
-        pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sV + 32 * kh * P, s), df[s], pacc[kh], 0, 0, 0);
+        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sK + RT::rows(32 * kh), s), qf[s], sacc[kh], 0, 0, 0);
+        pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sV + RT::rows(32 * kh), s), df[s], pacc[kh], 0, 0, 0);
       }
     // exponentials, dS and dQ at raised wave priority (as in the forward
     // kernel; measured 1% faster; the same in dK/dV was 4% slower)
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
       const bf16x8 sb = b_from_acc(pacc, tt);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
-        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<P>(sK, tt, dt), sb, dq[dt], 0, 0, 0);
+        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<RT>(sK, tt, dt), sb, dq[dt], 0, 0, 0);
     }
     __builtin_amdgcn_s_setprio(0);
   }

@@ -70,7 +70,6 @@ template <int D>
 __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   using T = FwdTiles<D>;
   using RT = typename T::RT;
-  constexpr int P = RT::P;
   constexpr int NS = D / 16;   // MFMA k-steps over d
   constexpr int NDT = D / 32;  // 32-row d blocks of O^T
   __shared__ __align__(16) uint8_t smem[kStages * T::STAGE];
@@ -112,9 +111,9 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     }
   };
   RowOperand kop;
-  kop.init<P>(0, l32, g);
+  kop.init<RT>(0, l32, g);
   TrOperand vop;
-  vop.init<P>(0, lane);
+  vop.init<RT>(0, lane);
 
   EntryRing<kStages> ring;
   ring.init(U, n);
@@ -153,7 +152,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) kfr[kh][s] = kop.load(sK + 32 * kh * P, s);
+      for (int kh = 0; kh < 2; ++kh) kfr[kh][s] = kop.load(sK + RT::rows(32 * kh), s);
     f32x16 sacc[2] = {f32x16_zero(), f32x16_zero()};
 #pragma unroll
     for (int s = 0; s < NS; ++s)
@@ -164,7 +163,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) vfr[tt][dt] = vop.load<P>(sV, tt, dt);
+      for (int dt = 0; dt < NDT; ++dt) vfr[tt][dt] = vop.load<RT>(sV, tt, dt);
     if (e & 4) {
       // this lane's keys are 32kh + 8j + 4g + i: bit (32kh + 8j + i) of vmask >> 4g
       const uint64_t mm = sload_u64(a.tmask + (e >> 3)) >> (4 * g);

@@ -21,7 +21,7 @@
 // (consume_regs), or the compiler's first-use wait inside the loop would
 // drain the tile copy on every iteration.
 //
-// The LDS layout of the tiles (padded, swizzled rows) is described with
+// The LDS layout of the tiles (quads of rows, chunks swizzled) is described with
 // RowTile below; each tile is a whole number of KB, so a stage is filled by a
 // fixed number of KB-instructions spread over the waves.
 #pragma once
@@ -150,48 +150,59 @@ __device__ __forceinline__ int stage_ahead(int st) {
 }
 
 // ------------------------------------------------------------ row tiles
-// A bf16 tile [64][D] is kept row-major in LDS with a pitch of 2D + 64 bytes,
-// 16-byte chunk c of row r stored at chunk (c & ~3) | ((c & 3) ^ ((r >> 2) & 3)).
-// Two read patterns use the same tile without bank conflicts (64 banks):
+// A bf16 tile [64][D] (rows of W = 2D bytes) is kept in LDS without padding,
+// one quad of rows (4 rows, Q = 4W bytes) after the other, each quad being a
+// permutation of the quad's Q contiguous bytes in memory, so one 1 KB
+// DMA instruction copies whole contiguous rows.  Inside the quad of rows
+// 4m .. 4m + 3, 16-byte chunk c of row 4m + k sits at byte
+//     256 (c >> 2) + 64 k + 16 ((c & 3) ^ (m & 3)),
+// so the 64-bank word address of a chunk is 4 k + ((c & 3) ^ (m & 3)) (mod 16
+// chunk slots).  Two read patterns use the same tile without bank conflicts:
 //  * RowOperand: an MFMA operand whose contraction runs along the tile's
 //    columns (lane (l32, g) takes 8 elements of row R + l32 at column
-//    16 s + 8 g) -- one ds_read_b128;
+//    16 s + 8 g) -- one ds_read_b128; the 16 lanes of one LDS cycle read 16
+//    consecutive rows of one chunk, slots 4 (r & 3) + (((r >> 2) & 3) ^ c):
+//    all distinct;
 //  * TrOperand: an MFMA operand whose contraction runs along the tile's rows
 //    (lane (l32, g) takes column 32 dt + l32 at the eight rows
 //    16 tt + {4g .. 4g+3, 8+4g .. 8+4g+3}, the k-slot order of an operand
 //    built from an accumulator, see b_from_acc) -- two ds_read_b64_tr_b16.
 //    Within each 16-lane group, lane 16b + 4i + e of ds_read_b64_tr_b16
 //    receives element e of the 8-byte chunks addressed by lanes 16b + 4k + i,
-//    k = 0..3 (in slot k).
+//    k = 0..3 (in slot k).  The 32 lanes of one LDS cycle read the four rows
+//    of one quad at the four chunks 4 dt .. 4 dt + 3: slots 4 k + (x ^ m),
+//    all distinct.
 // Every per-step offset is a lane base plus an immediate, and the same tile
 // serves S = Q K^T-type products and the transposed products (dK = dS^T Q,
 // dQ = dS K, O = P V), so no transposed copies are needed.
 template <int D>
 struct RowTile {
-  static constexpr int W = 2 * D, P = W + 64, BYTES = 64 * P, KB = BYTES / 1024;
-  static_assert(BYTES % 1024 == 0, "row tiles fill whole KB");
+  static constexpr int W = 2 * D, Q = 4 * W, BYTES = 64 * W, KB = BYTES / 1024;
+  static_assert(BYTES % 1024 == 0 && (1024 % Q == 0 || Q % 1024 == 0), "quads tile whole KB");
+  // byte offset of row R (a multiple of 4) in the tile
+  static constexpr int rows(int R) { return (R >> 2) * Q; }
   // global byte offset fetched by lane `lane` of KB-instruction i of the tile
-  // (lanes whose slot is row padding re-read the row's first chunk)
   static __device__ __forceinline__ uint32_t src_offset(int i, int lane) {
     const int pos = 1024 * i + 16 * lane;
-    const int row = pos / P, slot = (pos - row * P) >> 4;
-    if (slot >= W / 16) return (uint32_t)(row * W);
-    const int c = (slot & ~3) | ((slot & 3) ^ ((row >> 2) & 3));
-    return (uint32_t)(row * W + 16 * c);
+    const int rq = pos / Q, rem = pos - rq * Q;
+    const int k = (rem >> 6) & 3;
+    const int c = 4 * (rem >> 8) + (((rem >> 4) & 3) ^ (rq & 3));
+    return (uint32_t)((4 * rq + k) * W + 16 * c);
   }
 };
 
 struct RowOperand {
   uint32_t even, odd;  // byte offsets in the tile for even / odd k-steps s
   // rows R + l32 (R a multiple of 4, may be wave-uniform runtime)
-  template <int P>
+  template <class RT>
   __device__ __forceinline__ void init(int R, int l32, int g) {
-    const int x = g ^ ((l32 >> 2) & 3);
-    even = (uint32_t)((R + l32) * P + 16 * x);
-    odd = (uint32_t)((R + l32) * P + 16 * (x ^ 2));
+    const int r = R + l32, m = (r >> 2) & 3;
+    const int base = (r >> 2) * RT::Q + 64 * (r & 3);
+    even = (uint32_t)(base + 16 * (m ^ g));
+    odd = (uint32_t)(base + 16 * (m ^ (2 + g)));
   }
   __device__ __forceinline__ bf16x8 load(const uint8_t* tile, int s) const {
-    return *reinterpret_cast<const bf16x8*>(tile + ((s & 1) ? odd : even) + 64 * (s >> 1));
+    return *reinterpret_cast<const bf16x8*>(tile + ((s & 1) ? odd : even) + 256 * (s >> 1));
   }
 };
 
@@ -201,19 +212,19 @@ typedef __attribute__((address_space(3))) prism_v4s prism_lds_v4s;
 
 struct TrOperand {
   uint32_t h0, h1;  // byte offsets of rows 16tt + 4g + k and 16tt + 8 + 4g + k (tt = 0)
-  // R0: first tile row of k-step tt = 0 (a multiple of 16, may be wave-uniform)
-  template <int P>
+  // R0: first tile row of k-step tt = 0 (a multiple of 4, may be wave-uniform)
+  template <class RT>
   __device__ __forceinline__ void init(int R0, int lane) {
     const int b = lane >> 4, k = (lane >> 2) & 3, i = lane & 3;
-    const int x0 = (2 * (b & 1) + (i >> 1)) ^ (b >> 1);
-    const int rowb = (R0 + 4 * (b >> 1) + k) * P + 8 * (i & 1);
-    h0 = (uint32_t)(rowb + 16 * x0);
-    h1 = (uint32_t)(rowb + 8 * P + 16 * (x0 ^ 2));
+    const int x = 2 * (b & 1) + (i >> 1);  // chunk of the lane within its 4-chunk group
+    const int r0 = R0 + 4 * (b >> 1) + k, r1 = r0 + 8;
+    h0 = (uint32_t)((r0 >> 2) * RT::Q + 64 * k + 16 * (((r0 >> 2) & 3) ^ x) + 8 * (i & 1));
+    h1 = (uint32_t)((r1 >> 2) * RT::Q + 64 * k + 16 * (((r1 >> 2) & 3) ^ x) + 8 * (i & 1));
   }
-  template <int P>
+  template <class RT>
   __device__ __forceinline__ bf16x8 load(const uint8_t* tile, int tt, int dt) const {
-    const uint8_t* p0 = tile + h0 + 16 * P * tt + 64 * dt;
-    const uint8_t* p1 = tile + h1 + 16 * P * tt + 64 * dt;
+    const uint8_t* p0 = tile + h0 + 4 * RT::Q * tt + 256 * dt;
+    const uint8_t* p1 = tile + h1 + 4 * RT::Q * tt + 256 * dt;
     const prism_v4s r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((prism_lds_v4s*)(p0));
     const prism_v4s r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((prism_lds_v4s*)(p1));
     const prism_v8s v = __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
