@@ -66,7 +66,9 @@ struct BwdArgs {
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kStagesDkdv = 3;  // entry j + 2 is copied while entry j is multiplied
+// dK/dV: four LDS stages, entry j + 2 copied while entry j is multiplied (the
+// waves that run behind still read entry j - 1's stage)
+constexpr int kStagesDkdv = 4, kAheadDkdv = 2;
 constexpr int kStagesDq = 2;    // two 4-wave workgroups per CU, double-buffered each
 
 template <int D>
@@ -80,6 +82,7 @@ struct BwdTiles {
   static constexpr int NDT = D / 32;
   static constexpr int DKDV_RED = 4 * 64 * 2 * NDT * 16 * 4;  // qh = 1 partials of dK and dV
   static constexpr int DKDV_LDS = kStagesDkdv * DKDV_STAGE > DKDV_RED ? kStagesDkdv * DKDV_STAGE : DKDV_RED;
+  static_assert(kAheadDkdv + 2 <= kStagesDkdv, "stages of entries j - 1 .. j + kAheadDkdv");
   static constexpr int DQ_LDS = kStagesDq * DQ_STAGE;
   static_assert(DKDV_LDS <= 160 * 1024 && DQ_LDS <= 160 * 1024, "LDS budget");
 };
@@ -107,29 +110,26 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   // DMA plan: waves 0-3 (one per SIMD) issue KB-instructions w, w + 4, ...
   // (Q then dO), wave 3 also the m2 row and wave 2 the delta row; waves 4-7
   // issue none and start their MFMAs right after the barrier while the
-  // others queue their copies (−2.4% against all eight issuing, A/B on one
-  // box).  Instructions s and s + NOFF read the same lane offsets (of the
-  // Q and the dO tile), so NOFF offsets are kept.
+  // others queue their copies (-2.4% against all eight issuing, A/B on one
+  // box).  Instruction w + 4s of a tile reads 4096 s bytes past instruction w.
   constexpr int SL4 = 2 * T::SLOTS, NOFF = RT::KB / 4;
   static_assert(RT::KB % 4 == 0, "tile splits over four waves");
-  uint32_t soff[NOFF];
-#pragma unroll
-  for (int s = 0; s < NOFF; ++s) soff[s] = RT::src_offset((w & 3) + 4 * s, lane);
+  const uint32_t soff = RT::src_offset(w & 3, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int qtile, int st) {
     if (w >= 4) return;
     const int64_t toff = qoff + (int64_t)qtile * 64 * D;
-    const void* qb = uniform_ptr(a.q + toff);
-    const void* db = uniform_ptr(a.do_ + toff);
+    const char* qb = (const char*)uniform_ptr(a.q + toff);
+    const char* db = (const char*)uniform_ptr(a.do_ + toff);
     const uint32_t base = lds0 + (uint32_t)(st * SB);
 #pragma unroll
     for (int s = 0; s < SL4; ++s) {
       const int i = w + 4 * s;
-      dma_b128(soff[s % NOFF], i < RT::KB ? qb : db, base + (uint32_t)i * 1024u);
+      dma_b128(soff, (i < RT::KB ? qb : db) + 4096 * (s % NOFF), base + (uint32_t)i * 1024u);
     }
     if (w >= 2) {
       const float* rowsrc = (w == 3 ? m2h : dlh) + (int64_t)qtile * 64;
-      dma_b32((uint32_t)lane * 4u, uniform_ptr(rowsrc), base + 2u * RT::BYTES + (w == 3 ? 0u : 256u));
+      dma_b32_rows(uniform_ptr(rowsrc), base + 2u * RT::BYTES + (w == 3 ? 0u : 256u));
     }
   };
   RowOperand rop;                // Q / dO rows 32 qh + l32
@@ -137,10 +137,10 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   TrOperand top;                 // Q^T / dO^T over query rows 32 qh .. 32 qh + 31
   top.init<RT>(32 * qh, lane);
 
-  EntryRing<kStagesDkdv> ring;
+  EntryRing<kAheadDkdv + 1> ring;
   ring.init(U, n);
 #pragma unroll
-  for (int k = 0; k + 1 < kStagesDkdv; ++k)
+  for (int k = 0; k < kAheadDkdv; ++k)
     if (k < n) issue(ring.e[k] >> 3, k);
 
   const int kslot = 2 * pair + tk;
@@ -165,18 +165,10 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) { dk[dt] = f32x16_zero(); dv[dt] = f32x16_zero(); }
 
-  int st = 0;  // stage of entry j
-  for (int j = 0; j < n; ++j) {
-    if (w >= 4) stage_wait<kStagesDkdv, 0>(n - 1 - j);
-    else if (w >= 2) stage_wait<kStagesDkdv, SL4 + 1>(n - 1 - j);
-    else stage_wait<kStagesDkdv, SL4>(n - 1 - j);
-    __syncthreads();
-    if (j + kStagesDkdv - 1 < n) issue(ring.e[kStagesDkdv - 1] >> 3, stage_ahead<kStagesDkdv>(st));
-    const int e = ring.advance(U, n, j);
-    const uint8_t* sQ = smem + st * SB;
-    st = st + 1 == kStagesDkdv ? 0 : st + 1;
-    if (!(e & mybit)) continue;
-
+  // S = Q K^T and dP = dO V^T of one entry, then P and dS (bf16 B operands of
+  // the dV / dK products, query rows 32qh + 8j + 4g + i in register r = 4j + i,
+  // column = this lane's key)
+  auto sdp = [&](const uint8_t* sQ, bf16x8* pb, bf16x8* sb) {
     const uint8_t* sDO = sQ + RT::BYTES;
     const float* sM = reinterpret_cast<const float*>(sQ + 2 * RT::BYTES);
     const float* sDl = sM + 64;
@@ -186,7 +178,6 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sQ, s), kf[s], sacc, 0, 0, 0);
       pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sDO, s), vf[s], pacc, 0, 0, 0);
     }
-    // P and dS for query rows 32qh + 8j + 4g + i (register r = 4j + i), column = this lane's key
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const float4 m4 = *reinterpret_cast<const float4*>(sM + 32 * qh + 8 * jj + 4 * g);
@@ -204,14 +195,65 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
     }
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      const bf16x8 pb = b_from_acc(&sacc, t2);
-      const bf16x8 sb = b_from_acc(&pacc, t2);
+      pb[t2] = b_from_acc(&sacc, t2);
+      sb[t2] = b_from_acc(&pacc, t2);
+    }
+  };
+  // dV^T += dO^T P and dK^T += Q^T dS of one entry
+  auto dvdk = [&](const uint8_t* sQ, const bf16x8* pb, const bf16x8* sb) {
+    const uint8_t* sDO = sQ + RT::BYTES;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<RT>(sDO, t2, dt), pb, dv[dt], 0, 0, 0);
-        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<RT>(sQ, t2, dt), sb, dk[dt], 0, 0, 0);
+        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<RT>(sDO, t2, dt), pb[t2], dv[dt], 0, 0, 0);
+        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<RT>(sQ, t2, dt), sb[t2], dk[dt], 0, 0, 0);
+      }
+  };
+
+  // The two waves of a SIMD (tiles tk = 0 and 1) run half an entry apart: a
+  // tk = 0 wave takes entry j as S / dP, exponentials, dV / dK; a tk = 1 wave
+  // first does dV / dK of its previous entry, then S / dP and exponentials of
+  // entry j.  So each wave's exponentials run while the other wave's MFMAs
+  // hold the matrix core, instead of both SIMD waves leaving it idle at once.
+  // Each group has a loop of its own (the same barriers per entry), so the
+  // P / dS operands the tk = 1 waves carry to the next entry are not live in
+  // the tk = 0 loop.
+  if (tk == 0) {
+    int st = 0;  // stage of entry j
+    for (int j = 0; j < n; ++j) {
+      const int e = ring.e[0], enext = ring.e[kAheadDkdv];
+      ring.advance(U, n, j);
+      if (w >= 2) stage_wait<kAheadDkdv + 1, SL4 + 1>(n - 1 - j);
+      else stage_wait<kAheadDkdv + 1, SL4>(n - 1 - j);
+      __syncthreads();
+      if (j + kAheadDkdv < n) issue(enext >> 3, (st + kAheadDkdv) % kStagesDkdv);
+      const uint8_t* sQ = smem + st * SB;
+      st = st + 1 == kStagesDkdv ? 0 : st + 1;
+      if (!(e & mybit)) continue;
+      bf16x8 pb[2], sb[2];
+      sdp(sQ, pb, sb);
+      dvdk(sQ, pb, sb);
+    }
+  } else {
+    int st = 0;
+    bool pend = false;          // P / dS of the previous entry wait for their dV / dK
+    const uint8_t* sPrev = smem;
+    bf16x8 pb[2], sb[2];
+    for (int j = 0; j < n; ++j) {
+      const int e = ring.e[0];
+      ring.advance(U, n, j);
+      __syncthreads();
+      const uint8_t* sQ = smem + st * SB;
+      st = st + 1 == kStagesDkdv ? 0 : st + 1;
+      if (pend) dvdk(sPrev, pb, sb);
+      pend = (e & mybit) != 0;
+      if (pend) {
+        sdp(sQ, pb, sb);
+        sPrev = sQ;
       }
     }
+    if (pend) dvdk(sPrev, pb, sb);
   }
 
   // add the two query-half partials in a fixed order (qh = 0 + qh = 1)
@@ -272,20 +314,20 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   const int64_t qoff = (int64_t)bh * a.Sq * D, koff = (int64_t)bh * a.Sk * D;
   const float NINF = -__builtin_inff();
 
-  // DMA plan: wave w issues KB-instructions w, w + 4, ... (K then V)
-  uint32_t soff[SLOTS];
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) soff[s] = RT::src_offset((w + 4 * s) % RT::KB, lane);
+  // DMA plan: wave w issues KB-instructions w, w + 4, ... (K then V);
+  // instruction w + 4s of a tile reads 4096 s bytes past instruction w
+  constexpr int NOFF = RT::KB / 4;
+  const uint32_t soff = RT::src_offset(w, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int ktile, int st) {
     const int64_t toff = koff + (int64_t)ktile * 64 * D;
-    const void* kb = uniform_ptr(a.k + toff);
-    const void* vb = uniform_ptr(a.v + toff);
+    const char* kb = (const char*)uniform_ptr(a.k + toff);
+    const char* vb = (const char*)uniform_ptr(a.v + toff);
     const uint32_t base = lds0 + (uint32_t)(st * SB);
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
       const int i = w + 4 * s;
-      dma_b128(soff[s], i < RT::KB ? kb : vb, base + (uint32_t)i * 1024u);
+      dma_b128(soff, (i < RT::KB ? kb : vb) + 4096 * (s % NOFF), base + (uint32_t)i * 1024u);
     }
   };
   RowOperand rop;  // K / V rows l32 (+ 32 kh as an immediate)
@@ -323,10 +365,11 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
 
   int st = 0;  // stage of entry j
   for (int j = 0; j < n; ++j) {
+    const int e = ring.e[0], enext = ring.e[kStagesDq - 1];
+    ring.advance(U, n, j);
     stage_wait<kStagesDq, SLOTS>(n - 1 - j);
     __syncthreads();
-    if (j + kStagesDq - 1 < n) issue(ring.e[kStagesDq - 1] >> 3, stage_ahead<kStagesDq>(st));
-    const int e = ring.advance(U, n, j);
+    if (j + kStagesDq - 1 < n) issue(enext >> 3, stage_ahead<kStagesDq>(st));
     const uint8_t* sK = smem + st * SB;
     st = st + 1 == kStagesDq ? 0 : st + 1;
     if (!(e & mybit)) continue;

@@ -90,24 +90,23 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   // DMA plan: waves 0 and 1 issue KB-instructions w, w + 2, ... of each
   // stage (K then V); waves 2 and 3 issue none.  A wave stalls while the
   // CU's address path takes its copy instructions, so the two waves that
-  // issue none start their MFMAs right after the barrier (−1% against four
-  // waves issuing ten each, A/B on one box).  All twenty lane offsets stay
-  // in registers: keeping the ten distinct ones and indexing them modulo
-  // ten measured 1% slower here.
-  constexpr int SL2 = T::STAGE_KB / 2;
-  uint32_t soff[SL2];
-#pragma unroll
-  for (int s = 0; s < SL2; ++s) soff[s] = RT::src_offset(((w & 1) + 2 * s) % RT::KB, lane);
+  // issue none start their MFMAs right after the barrier (-1% against four
+  // waves issuing ten each, A/B on one box).  Instruction i + 4m of a tile
+  // reads 4096 m bytes past instruction i, so two lane offsets serve all.
+  constexpr int SL2 = T::STAGE_KB / 2, NOFF = RT::KB / 4;
+  static_assert(RT::KB % 4 == 0, "tile splits into fours");
+  const uint32_t soff0 = RT::src_offset(w & 1, lane), soff1 = RT::src_offset((w & 1) + 2, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int kt, int st) {
     if (w >= 2) return;
-    const void* kb = uniform_ptr(Kh + (int64_t)kt * 64 * D);
-    const void* vb = uniform_ptr(Vh + (int64_t)kt * 64 * D);
+    const char* kb = (const char*)uniform_ptr(Kh + (int64_t)kt * 64 * D);
+    const char* vb = (const char*)uniform_ptr(Vh + (int64_t)kt * 64 * D);
     const uint32_t base = lds0 + (uint32_t)(st * T::STAGE);
 #pragma unroll
     for (int s = 0; s < SL2; ++s) {
-      const int i = w + 2 * s;
-      dma_b128(soff[s], i < RT::KB ? kb : vb, base + (uint32_t)i * 1024u);
+      const int i = w + 2 * s;                  // instruction of the stage
+      const int t = i < RT::KB ? i : i - RT::KB;  // instruction of its tile
+      dma_b128((s & 1) ? soff1 : soff0, (i < RT::KB ? kb : vb) + 4096 * ((t >> 2) % NOFF), base + (uint32_t)i * 1024u);
     }
   };
   RowOperand kop;
@@ -137,10 +136,11 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
   int st = 0;  // stage of entry j
   for (int j = 0; j < n; ++j) {
+    const int e = ring.e[0], enext = ring.e[kStages - 1];
+    ring.advance(U, n, j);
     stage_wait<kStages, SL2>(n - 1 - j);
     __syncthreads();
-    if (j + kStages - 1 < n) issue(ring.e[kStages - 1] >> 3, stage_ahead<kStages>(st));
-    const int e = ring.advance(U, n, j);
+    if (j + kStages - 1 < n) issue(enext >> 3, stage_ahead<kStages>(st));
     const uint8_t* sK = smem + st * T::STAGE;
     st = st + 1 == kStages ? 0 : st + 1;
     if (!(e & mybit)) continue;

@@ -53,6 +53,17 @@ __device__ __forceinline__ void dma_b128(uint32_t voff, const void* base, uint32
 __device__ __forceinline__ void dma_b32(uint32_t voff, const void* base, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(m0) : "m0");
 }
+// 4 bytes per lane: LDS[m0 + 4*lane] <- global[base + 4*lane]; the lane
+// offset is formed inside the asm, so no register holds it between copies
+__device__ __forceinline__ void dma_b32_rows(const void* base, uint32_t m0) {
+  uint32_t t;
+  asm volatile(
+      "v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\tv_lshlrev_b32 %0, 2, %0\n\t"
+      "s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1"
+      : "=&v"(t)
+      : "s"(base), "s"(m0)
+      : "m0");
+}
 // wait until every load this wave issued (DMA included) has landed
 __device__ __forceinline__ void dma_wait_all() { asm volatile("s_waitcnt vmcnt(0)"); }
 
@@ -107,40 +118,26 @@ __device__ __forceinline__ void stage_wait(int after) {  // after = n - 1 - j
   dma_wait_le<0>();
 }
 
-// Wave-uniform ring of the next NST list entries.  The list is read 64
-// entries at a time into one VGPR (lane i holds entry 64c + i) and entries are
-// extracted with v_readlane, so there is no per-entry load on the critical
-// path.  The next window is loaded 64 entries ahead; the compiler's wait for
-// it (first use at the window switch) drains the copies in flight once per 64
-// entries.
+// Wave-uniform ring of the next NST list entries, read with scalar loads.
+// (A vector load of the list would put a vmcnt wait in the loop: the
+// compiler cannot tell which iteration issued it, so it waits for every load
+// in flight at the loop latch, tile copies included.)  The scalar loads wait
+// on lgkmcnt, which at the top of an iteration only covers the LDS reads of
+// the previous entry, all consumed by then; consecutive entries share a
+// scalar cache line.
 template <int NST>
 struct EntryRing {
-  int e[NST];   // entries j .. j + NST - 1 (0 past the end of the list)
-  int win_cur;  // lane i: entry 64 c + i
-  int win_nxt;  // lane i: entry 64 (c + 1) + i
-  // entries are requested in order, and the window switches exactly when the
-  // requested index reaches a multiple of 64, so entry k is always in win_cur
-  __device__ __forceinline__ int get(int k) const { return __builtin_amdgcn_readlane(win_cur, k & 63); }
+  int e[NST];  // entries j .. j + NST - 1 (0 past the end of the list)
   __device__ __forceinline__ void init(const int32_t* U, int n) {
-    const int lane = (int)(threadIdx.x & 63);
-    win_cur = lane < n ? U[lane] : 0;
-    win_nxt = 64 + lane < n ? U[64 + lane] : 0;
 #pragma unroll
-    for (int k = 0; k < NST; ++k) e[k] = k < n ? get(k) : 0;
+    for (int k = 0; k < NST; ++k) e[k] = k < n ? sload_i32(U + k) : 0;
   }
-  // entry j; shifts the ring to j + 1
-  __device__ __forceinline__ int advance(const int32_t* U, int n, int j) {
-    const int cur = e[0];
+  // shift the ring from entry j to j + 1
+  __device__ __forceinline__ void advance(const int32_t* U, int n, int j) {
 #pragma unroll
     for (int k = 0; k + 1 < NST; ++k) e[k] = e[k + 1];
     const int k = j + NST;
-    if ((k & 63) == 0 && k < n) {
-      const int lane = (int)(threadIdx.x & 63);
-      win_cur = win_nxt;
-      win_nxt = k + 64 + lane < n ? U[k + 64 + lane] : 0;
-    }
-    e[NST - 1] = k < n ? get(k) : 0;
-    return cur;
+    e[NST - 1] = k < n ? sload_i32(U + k) : 0;
   }
 };
 // stage holding entry j + NST - 1 when entry j is in stage st
@@ -181,7 +178,10 @@ struct RowTile {
   static_assert(BYTES % 1024 == 0 && (1024 % Q == 0 || Q % 1024 == 0), "quads tile whole KB");
   // byte offset of row R (a multiple of 4) in the tile
   static constexpr int rows(int R) { return (R >> 2) * Q; }
-  // global byte offset fetched by lane `lane` of KB-instruction i of the tile
+  // global byte offset fetched by lane `lane` of KB-instruction i of the tile.
+  // Instructions i and i + 4m fetch at offsets 4096 m apart (the swizzle of a
+  // quad depends on the quad index mod 4 only), so a wave that issues every
+  // fourth instruction keeps one lane offset and advances the scalar base.
   static __device__ __forceinline__ uint32_t src_offset(int i, int lane) {
     const int pos = 1024 * i + 16 * lane;
     const int rq = pos / Q, rem = pos - rq * Q;
