@@ -51,7 +51,7 @@ __device__ __forceinline__ void load_chan(const T* p, float* x) {
 }
 
 template <int D, typename T>
-__global__ __launch_bounds__(kZoneThreads) void zone_stats_kernel(
+__global__ __launch_bounds__(kZoneThreads, 6) void zone_stats_kernel(
     const T* __restrict__ v, int H, int64_t S, const uint8_t* __restrict__ valid,
     int ZH, int ZW, GridBox box, float invH, float* __restrict__ packed,
     uint8_t* __restrict__ axis_valid) {
@@ -104,15 +104,16 @@ __global__ __launch_bounds__(kZoneThreads) void zone_stats_kernel(
     for (int j = 0; j < CPL; ++j) r[j] = 0.0f;
     // the eight tokens of row (lt, lh), two heads per step: sixteen row loads
     // in flight per wave (positions outside the input grid read as zero); each
-    // token's head sum still runs over h in order from +0
-    int64_t tok[8];
+    // token's head sum still runs over h in order from +0.  The row's tokens
+    // are consecutive: the first one (or -1) and how many lie inside the grid.
+    const int64_t t0 = token_in(z, (lt * 8 + lh) * 8, ZH, ZW, box);
+    const int nw = t0 < 0 ? 0 : min(8, box.W - (z % ZW) * 8);
+    const T* row = v + (t0 < 0 ? 0 : t0) * D + lane * CPL;
     float acc[8][CPL];
 #pragma unroll
-    for (int lw = 0; lw < 8; ++lw) {
-      tok[lw] = token_in(z, (lt * 8 + lh) * 8 + lw, ZH, ZW, box);
+    for (int lw = 0; lw < 8; ++lw)
 #pragma unroll
       for (int j = 0; j < CPL; ++j) acc[lw][j] = 0.0f;
-    }
     for (int h = 0; h < H; h += 2) {
       const bool two = h + 1 < H;
       float x0[8][CPL], x1[8][CPL];
@@ -120,9 +121,9 @@ __global__ __launch_bounds__(kZoneThreads) void zone_stats_kernel(
       for (int lw = 0; lw < 8; ++lw) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) x0[lw][j] = x1[lw][j] = 0.0f;
-        if (tok[lw] >= 0) {
-          load_chan<T, CPL>(v + ((int64_t)h * S + tok[lw]) * D + lane * CPL, x0[lw]);
-          if (two) load_chan<T, CPL>(v + ((int64_t)(h + 1) * S + tok[lw]) * D + lane * CPL, x1[lw]);
+        if (lw < nw) {
+          load_chan<T, CPL>(row + ((int64_t)h * S + lw) * D, x0[lw]);
+          if (two) load_chan<T, CPL>(row + ((int64_t)(h + 1) * S + lw) * D, x1[lw]);
         }
       }
 #pragma unroll
