@@ -183,11 +183,13 @@ __device__ __forceinline__ void load8(const T* p, float* x) {
 // instruction in turn, fetched by lane shuffles); padding rows are written as
 // zeros, are invalid, and belong to no block when they lie past the last
 // block.
-template <int D, typename T, typename Map>
+template <int D, typename T, typename Map, bool POOL>
 __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs a, Map m) {
   constexpr int LPR = D / 8;     // lanes per row
   constexpr int RPI = 64 / LPR;  // rows per wave instruction
-  constexpr int NB = 2;          // wave instructions in flight (2: 0.256 ms, 4: 0.283, 8: 0.326 at C4)
+  // wave instructions in flight: with pooling 2 (2: 0.256 ms, 4: 0.283, 8:
+  // 0.326 averaged over the step's launches at C4), without it 4
+  constexpr int NB = POOL ? 2 : 4;
   constexpr int RB = RPI * NB;   // rows per batch (inside one block and one tile)
   static_assert(64 % RB == 0, "batches must not straddle tiles");
   const int bh = blockIdx.y;
@@ -198,7 +200,6 @@ __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs 
   const bool first_bh = bh == 0;
   const T* x = reinterpret_cast<const T*>(a.x) + (int64_t)bh * a.S_in * D + c8;
   const int64_t rowbase = (int64_t)bh * a.S_out;
-  const bool pooling = a.block_mean != nullptr || a.block_count != nullptr || a.tile_count != nullptr;
 
   float acc[8];
   int cnt = 0, tcnt = 0;  // (meaningful in the first row group)
@@ -244,7 +245,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs 
       }
       if (first_bh && cl == 0 && a.valid_re) a.valid_re[grow[b]] = ok[b] ? 1 : 0;
     }
-    if (pooling) {
+    if (POOL) {
       // rows of the batch in order: instruction b, row group g
 #pragma unroll
       for (int b = 0; b < NB; ++b)
@@ -332,15 +333,22 @@ __global__ __launch_bounds__(kGatherThreads) void scatter_rows_kernel(const uint
   }
 }
 
+template <typename Map, bool POOL>
+void launch_gather_t(const GatherArgs& a, const Map& m, int dtype, int D, dim3 grid, hipStream_t stream) {
+  if (dtype == PRISM_BF16) {
+    if (D == 128) gather_pool_kernel<128, uint16_t, Map, POOL><<<grid, kGatherThreads, 0, stream>>>(a, m);
+    else gather_pool_kernel<64, uint16_t, Map, POOL><<<grid, kGatherThreads, 0, stream>>>(a, m);
+  } else {
+    if (D == 128) gather_pool_kernel<128, float, Map, POOL><<<grid, kGatherThreads, 0, stream>>>(a, m);
+    else gather_pool_kernel<64, float, Map, POOL><<<grid, kGatherThreads, 0, stream>>>(a, m);
+  }
+}
 template <typename Map>
 void launch_gather(const GatherArgs& a, const Map& m, int dtype, int D, dim3 grid, hipStream_t stream) {
-  if (dtype == PRISM_BF16) {
-    if (D == 128) gather_pool_kernel<128, uint16_t, Map><<<grid, kGatherThreads, 0, stream>>>(a, m);
-    else gather_pool_kernel<64, uint16_t, Map><<<grid, kGatherThreads, 0, stream>>>(a, m);
-  } else {
-    if (D == 128) gather_pool_kernel<128, float, Map><<<grid, kGatherThreads, 0, stream>>>(a, m);
-    else gather_pool_kernel<64, float, Map><<<grid, kGatherThreads, 0, stream>>>(a, m);
-  }
+  if (a.block_mean != nullptr || a.block_count != nullptr || a.tile_count != nullptr)
+    launch_gather_t<Map, true>(a, m, dtype, D, grid, stream);
+  else
+    launch_gather_t<Map, false>(a, m, dtype, D, grid, stream);
 }
 
 template <typename Map>

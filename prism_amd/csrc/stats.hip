@@ -232,11 +232,24 @@ __global__ __launch_bounds__(64) void audio_zone_kernel(
     sCol[a][b] = c;
   }
   __syncthreads();
+  // valid-token counts per frame, row and column from one ballot per frame
+  // (lane 8 h + w of ballot t is token (t, h, w))
+  uint64_t vb[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) vb[t] = __ballot(sV[t * 64 + lane] != 0);
   if (lane == 0) {
     int cT[8], cH[8], cW[8], call = 0;
     for (int i = 0; i < 8; ++i) cT[i] = cH[i] = cW[i] = 0;
-    for (int i = 0; i < 512; ++i)
-      if (sV[i]) { cT[i >> 6]++; cH[(i >> 3) & 7]++; cW[i & 7]++; call++; }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      cT[t] = __popcll(vb[t]);
+      call += cT[t];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        cH[i] += __popcll(vb[t] & (0xffull << (8 * i)));
+        cW[i] += __popcll(vb[t] & (0x0101010101010101ull << i));
+      }
+    }
     float frame[8], hs[8], ws[8], total = 0.0f;
     for (int t = 0; t < 8; ++t) {
       frame[t] = 0.0f;
