@@ -440,11 +440,13 @@ int64_t oc_tile_maps(const int64_t *shape_ids, int Nz, int64_t *block_id_of_tile
 /* ------------------------------------------------------------------ */
 /* Masked block means of the rearranged q (or k): masked_mean_pooling_compression
  * (bsa_interface.py:177-201) + _logical_block_means
- * (dynamic_block_attention.py:173-188).  Canonical: fp32 sum over the block's
- * valid tokens in rearranged order, divided by max(count,1) (the reference
- * evaluates the same quantity as a count-weighted mean of tile means in q's
- * dtype).  x: [B,H,S,D] in THW order (padded grid).  out: [B,H,N_b,D] fp32;
- * block_count[N_b]; tile_count[N_tiles]. */
+ * (dynamic_block_attention.py:173-188).  Canonical: the block's valid tokens
+ * in rearranged order o = 0 .. bsz-1 fall into RPI = 512 / D row groups
+ * (o mod RPI); each group is summed in fp32 from +0 in row order, the block
+ * sum is ((p_0 + p_1) + ...) + p_{RPI-1}, divided by max(count,1) (the
+ * reference evaluates the same quantity as a count-weighted mean of tile
+ * means in q's dtype).  x: [B,H,S,D] in THW order (padded grid).
+ * out: [B,H,N_b,D] fp32; block_count[N_b]; tile_count[N_tiles]. */
 void oc_block_pool(const void *x, int dtype, int B, int H, int64_t S, int D,
                    const uint8_t *valid, const int64_t *shape_ids, int T, int Hg, int Wg,
                    float *out, int32_t *block_count, int32_t *tile_count) {
@@ -453,7 +455,8 @@ void oc_block_pool(const void *x, int dtype, int B, int H, int64_t S, int D,
     int64_t *inv = (int64_t *)malloc(sizeof(int64_t) * S);
     oc_rearrange_index(shape_ids, T, Hg, Wg, src, inv);
     int64_t nb = oc_tile_maps(shape_ids, Nz, NULL, NULL, NULL);
-    float *acc = (float *)malloc(sizeof(float) * D);
+    const int rpi = 512 / D;
+    float *acc = (float *)malloc(sizeof(float) * D * rpi);
     for (int b = 0; b < B; ++b)
         for (int h = 0; h < H; ++h) {
             int64_t blk = 0;
@@ -462,15 +465,18 @@ void oc_block_pool(const void *x, int dtype, int B, int H, int64_t S, int D,
                 int bsz = CAND[c][0] * CAND[c][1] * CAND[c][2];
                 for (int j = 0; j < 512 / bsz; ++j, ++blk) {
                     int cnt = 0;
-                    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+                    for (int d = 0; d < D * rpi; ++d) acc[d] = 0.0f;
                     for (int o = 0; o < bsz; ++o) {
                         int64_t rpos = (int64_t)z * 512 + j * bsz + o;
                         int64_t g = src[rpos];
                         if (valid && !valid[g]) continue;
                         cnt++;
                         const int64_t base = (((int64_t)b * H + h) * S + g) * D;
-                        for (int d = 0; d < D; ++d) acc[d] = acc[d] + ld(x, dtype, base + d);
+                        float *part = acc + (o % rpi) * D;
+                        for (int d = 0; d < D; ++d) part[d] = part[d] + ld(x, dtype, base + d);
                     }
+                    for (int r = 1; r < rpi; ++r)
+                        for (int d = 0; d < D; ++d) acc[d] = acc[d] + acc[r * D + d];
                     float den = (float)(cnt > 0 ? cnt : 1);
                     float *o = out + (((int64_t)b * H + h) * nb + blk) * D;
                     for (int d = 0; d < D; ++d) o[d] = acc[d] / den;

@@ -249,19 +249,25 @@ def chunk_source_index(grid, pgrid, chunk, rows: Optional[int] = None) -> np.nda
 
 def chunk_pool(x: np.ndarray, src: np.ndarray, valid: Optional[np.ndarray], csz: int, n_blocks: int):
     """(masked_)mean_pooling_compression (bsa_interface.py:164-201) of the
-    rearranged rows: per chunk, the fp32 sum of its valid rows taken in row
-    order, divided by max(count, 1).  x: [B,H,S_in,D] float32 (bf16 values
-    widened).  Returns (means [B,H,n_blocks,D] fp32, counts [n_blocks])."""
+    rearranged rows: per chunk, its valid rows j fall into RPI = 512 / D row
+    groups (j mod RPI), each summed in fp32 in row order from +0; the chunk
+    sum is ((p_0 + p_1) + ...) + p_{RPI-1}, divided by max(count, 1).
+    x: [B,H,S_in,D] float32 (bf16 values widened).  Returns (means
+    [B,H,n_blocks,D] fp32, counts [n_blocks])."""
     x = np.asarray(x, np.float32)
     rows = src[: n_blocks * csz].reshape(n_blocks, csz)
     ok = rows >= 0
     if valid is not None:
         ok &= np.asarray(valid).astype(bool)[np.maximum(rows, 0)]
     B, H, _, D = x.shape
-    acc = np.zeros((B, H, n_blocks, D), np.float32)
+    rpi = 512 // D
+    part = np.zeros((rpi, B, H, n_blocks, D), np.float32)
     for j in range(csz):
         xj = x[:, :, np.maximum(rows[:, j], 0), :]
-        acc = np.where(ok[None, None, :, j, None], acc + xj, acc)
+        part[j % rpi] = np.where(ok[None, None, :, j, None], part[j % rpi] + xj, part[j % rpi])
+    acc = part[0]
+    for r in range(1, rpi):
+        acc = (acc + part[r]).astype(np.float32)
     cnt = ok.sum(axis=1).astype(np.int32)
     mean = acc / np.maximum(cnt, 1).astype(np.float32)[None, None, :, None]
     return mean.astype(np.float32), cnt

@@ -178,11 +178,12 @@ __device__ __forceinline__ void load8(const T* p, float* x) {
 // unit u (blocks of 64 or 128 rows: one or two whole blocks, two tiles).  A
 // lane moves 8 channels (16 bytes of bf16): D / 8 lanes per row, 64 / (D / 8)
 // rows per wave instruction, NB instructions in flight (fewer registers, more
-// waves per SIMD beat more loads per wave here).  Block means are
-// fp32 sums in row order (lanes of the first row group add the rows of each
-// instruction in turn, fetched by lane shuffles); padding rows are written as
-// zeros, are invalid, and belong to no block when they lie past the last
-// block.
+// waves per SIMD beat more loads per wave here).  Block means: row group g
+// (rows o of the block with o mod RPI = g, RPI = 512 / D) is summed in fp32
+// in row order from +0 by the lanes that load it, and the block sum is
+// ((p_0 + p_1) + ...) + p_{RPI-1}, formed by the first group's lanes when the
+// block is complete; padding rows are written as zeros, are invalid, and
+// belong to no block when they lie past the last block.
 template <int D, typename T, typename Map, bool POOL>
 __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs a, Map m) {
   constexpr int LPR = D / 8;     // lanes per row
@@ -246,30 +247,35 @@ __global__ __launch_bounds__(kGatherThreads) void gather_pool_kernel(GatherArgs 
       if (first_bh && cl == 0 && a.valid_re) a.valid_re[grow[b]] = ok[b] ? 1 : 0;
     }
     if (POOL) {
-      // rows of the batch in order: instruction b, row group g
+      // this lane's row of each instruction, in row order within its group;
+      // valid rows counted from one ballot per instruction (a lane per row)
+      constexpr uint64_t kRowLead = LPR == 16 ? 0x0001000100010001ull : 0x0101010101010101ull;
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NB; ++b) {
 #pragma unroll
-        for (int g = 0; g < RPI; ++g) {
-          const int src = g * LPR + cl;
-          const bool okg = __shfl((int)ok[b], src, 64) != 0;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float xg = g == 0 ? xv[b][j] : __shfl(xv[b][j], src, 64);
-            acc[j] = okg ? acc[j] + xg : acc[j];
-          }
-          cnt += okg ? 1 : 0;
-          tcnt += okg ? 1 : 0;
-        }
+        for (int j = 0; j < 8; ++j) acc[j] = ok[b] ? acc[j] + xv[b][j] : acc[j];
+        const int nv = __popcll(__ballot(ok[b]) & kRowLead);
+        cnt += nv;
+        tcnt += nv;
+      }
       const int rlast = wid * 128 + o0 + RB - 1;
       if ((rlast + 1) % m.bsz == 0) {  // block complete
         const int64_t blk = m.block(rlast);
         if (blk < a.N_b) {
-          if (a.block_mean && sub == 0) {
-            const float den = (float)(cnt > 0 ? cnt : 1);
-            float* dst = a.block_mean + ((int64_t)bh * a.N_b + blk) * D + c8;
+          if (a.block_mean) {
+            float sum[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) dst[j] = acc[j] / den;
+            for (int j = 0; j < 8; ++j) sum[j] = acc[j];
+#pragma unroll
+            for (int g = 1; g < RPI; ++g)
+#pragma unroll
+              for (int j = 0; j < 8; ++j) sum[j] = sum[j] + __shfl(acc[j], g * LPR + cl, 64);
+            if (sub == 0) {
+              const float den = (float)(cnt > 0 ? cnt : 1);
+              float* dst = a.block_mean + ((int64_t)bh * a.N_b + blk) * D + c8;
+#pragma unroll
+              for (int j = 0; j < 8; ++j) dst[j] = sum[j] / den;
+            }
           }
           if (first_bh && lane == 0 && a.block_count) a.block_count[blk] = cnt;
         }

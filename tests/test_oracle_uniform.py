@@ -68,10 +68,16 @@ def test_chunk_pool_masked_mean_and_order():
         assert cnt[n] == len(ok)
         want = x[:, :, ok].astype(np.float64).sum(2) / max(len(ok), 1)
         np.testing.assert_allclose(mean[:, :, n], want, rtol=2e-6, atol=1e-7)
-        # the fp32 sum is taken in row order (the order the HIP kernel uses)
-        acc = np.zeros((1, 2, 64), np.float32)
-        for r in ok:
-            acc = (acc + x[:, :, r]).astype(np.float32)
+        # the fp32 sum is taken per row group (chunk row j mod 512 / D) in row
+        # order, then over the groups in order (the order the HIP kernel uses)
+        rpi = 512 // 64
+        part = np.zeros((rpi, 1, 2, 64), np.float32)
+        for j, r in enumerate(rows):
+            if r >= 0 and valid[r]:
+                part[j % rpi] = (part[j % rpi] + x[:, :, r]).astype(np.float32)
+        acc = part[0]
+        for g in range(1, rpi):
+            acc = (acc + part[g]).astype(np.float32)
         assert np.array_equal(mean[:, :, n], (acc / np.float32(max(len(ok), 1))).astype(np.float32))
     # unmasked pooling of an unpadded grid is the plain chunk mean (mean_pooling_compression)
     g2 = (4, 4, 8)
