@@ -29,29 +29,43 @@ constexpr int kZoneThreads = 512;  // 8 waves: wave index = frame lt
 
 // One workgroup per zone.  Wave lt walks frame lt row by row; lane l owns
 // channels [l*CPL, l*CPL + CPL).
+// Raw loads of CPL channels (kept unconverted until they are added, so a
+// load's wait is at its use) and their conversion to float
 template <typename T, int CPL>
-__device__ __forceinline__ void load_chan(const T* p, float* x) {
-  if (sizeof(T) == 2) {
-    if (CPL == 2) {
-      const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
-      x[0] = __uint_as_float(u << 16);
-      x[CPL - 1] = __uint_as_float(u & 0xffff0000u);
-    } else {
-      x[0] = bf2f(*reinterpret_cast<const uint16_t*>(p));
-    }
-  } else {
-    if (CPL == 2) {
-      const float2 f = *reinterpret_cast<const float2*>(p);
-      x[0] = f.x;
-      x[CPL - 1] = f.y;
-    } else {
-      x[0] = *reinterpret_cast<const float*>(p);
-    }
+struct ChanRaw;
+template <>
+struct ChanRaw<uint16_t, 2> {
+  using type = uint32_t;
+  static __device__ __forceinline__ type load(const uint16_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+  static __device__ __forceinline__ void unpack(type u, float* x) {
+    x[0] = __uint_as_float(u << 16);
+    x[1] = __uint_as_float(u & 0xffff0000u);
   }
-}
+};
+template <>
+struct ChanRaw<uint16_t, 1> {
+  using type = uint32_t;
+  static __device__ __forceinline__ type load(const uint16_t* p) { return *p; }
+  static __device__ __forceinline__ void unpack(type u, float* x) { x[0] = __uint_as_float(u << 16); }
+};
+template <>
+struct ChanRaw<float, 2> {
+  using type = float2;
+  static __device__ __forceinline__ type load(const float* p) { return *reinterpret_cast<const float2*>(p); }
+  static __device__ __forceinline__ void unpack(type f, float* x) {
+    x[0] = f.x;
+    x[1] = f.y;
+  }
+};
+template <>
+struct ChanRaw<float, 1> {
+  using type = float;
+  static __device__ __forceinline__ type load(const float* p) { return *p; }
+  static __device__ __forceinline__ void unpack(type f, float* x) { x[0] = f; }
+};
 
 template <int D, typename T>
-__global__ __launch_bounds__(kZoneThreads, 6) void zone_stats_kernel(
+__global__ __launch_bounds__(kZoneThreads, sizeof(T) == 2 ? 6 : 4) void zone_stats_kernel(
     const T* __restrict__ v, int H, int64_t S, const uint8_t* __restrict__ valid,
     int ZH, int ZW, GridBox box, float invH, float* __restrict__ packed,
     uint8_t* __restrict__ axis_valid) {
@@ -63,7 +77,7 @@ __global__ __launch_bounds__(kZoneThreads, 6) void zone_stats_kernel(
 
   const int z = blockIdx.x;
   const int tid = threadIdx.x;
-  const int lt = tid >> 6, lane = tid & 63;
+  const int lt = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // (lt is wave-uniform)
 
   __shared__ int sPart[8][17];    // per frame t: valid tokens, per h, per w
   {
@@ -98,58 +112,85 @@ __global__ __launch_bounds__(kZoneThreads, 6) void zone_stats_kernel(
 #pragma unroll
     for (int w = 0; w < 8; ++w) cacc[w][j] = 0.0f;
   }
-  for (int lh = 0; lh < 8; ++lh) {
-    float r[CPL];
+  // Steps k = 0 .. 8 NP - 1 (NP head pairs): row lh = k / NP, heads 2 hp and
+  // 2 hp + 1 of its eight tokens (hp = k mod NP).  The sixteen loads of step
+  // k + 1 are issued before step k is added, so a wave always has a step in
+  // flight; every step issues all sixteen loads (positions outside the input
+  // grid, or past the last head, re-read a valid address and are added as
+  // zero), so the waits count loads statically.  Each token's head sum runs
+  // over h in order from +0.
+  using Raw = typename ChanRaw<T, CPL>::type;
+  const int NP = (H + 1) >> 1, K = 8 * NP;
+  const int nw_in = min(8, box.W - (z % ZW) * 8);  // tokens of a row inside the grid (if the row is)
+  float acc[8][CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) r[j] = 0.0f;
-    // the eight tokens of row (lt, lh), two heads per step: sixteen row loads
-    // in flight per wave (positions outside the input grid read as zero); each
-    // token's head sum still runs over h in order from +0.  The row's tokens
-    // are consecutive: the first one (or -1) and how many lie inside the grid.
+  for (int lw = 0; lw < 8; ++lw)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) acc[lw][j] = 0.0f;
+  float r[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) r[j] = 0.0f;
+  auto load_step = [&](int k, Raw (&b)[8][2]) {
+    const int lh = k / NP, h = 2 * (k - lh * NP);
     const int64_t t0 = token_in(z, (lt * 8 + lh) * 8, ZH, ZW, box);
-    const int nw = t0 < 0 ? 0 : min(8, box.W - (z % ZW) * 8);
-    const T* row = v + (t0 < 0 ? 0 : t0) * D + lane * CPL;
-    float acc[8][CPL];
-#pragma unroll
-    for (int lw = 0; lw < 8; ++lw)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) acc[lw][j] = 0.0f;
-    for (int h = 0; h < H; h += 2) {
-      const bool two = h + 1 < H;
-      float x0[8][CPL], x1[8][CPL];
-#pragma unroll
-      for (int lw = 0; lw < 8; ++lw) {
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) x0[lw][j] = x1[lw][j] = 0.0f;
-        if (lw < nw) {
-          load_chan<T, CPL>(row + ((int64_t)h * S + lw) * D, x0[lw]);
-          if (two) load_chan<T, CPL>(row + ((int64_t)(h + 1) * S + lw) * D, x1[lw]);
-        }
-      }
-#pragma unroll
-      for (int lw = 0; lw < 8; ++lw)
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-          acc[lw][j] = acc[lw][j] + x0[lw][j];
-          if (two) acc[lw][j] = acc[lw][j] + x1[lw][j];
-        }
-    }
+    const int nw = t0 < 0 ? 0 : nw_in;
+    const int h1 = h + 1 < H ? h + 1 : h;
+    // wave-uniform row bases of the two heads, plus this lane's channels
+    const T* r0 = v + ((int64_t)h * S + (t0 < 0 ? 0 : t0)) * D;
+    const T* r1 = v + ((int64_t)h1 * S + (t0 < 0 ? 0 : t0)) * D;
 #pragma unroll
     for (int lw = 0; lw < 8; ++lw) {
-      const bool ok = sValid[(lt * 8 + lh) * 8 + lw] != 0;
+      const int c = lw < nw ? lw : 0;
+      b[lw][0] = ChanRaw<T, CPL>::load(r0 + c * D + lane * CPL);
+      b[lw][1] = ChanRaw<T, CPL>::load(r1 + c * D + lane * CPL);
+    }
+  };
+  auto add_step = [&](int k, const Raw (&b)[8][2]) {
+    const int lh = k / NP, hp = k - lh * NP;
+    const bool two = 2 * hp + 1 < H;
+    const int nw = token_in(z, (lt * 8 + lh) * 8, ZH, ZW, box) < 0 ? 0 : nw_in;
+#pragma unroll
+    for (int lw = 0; lw < 8; ++lw) {
+      float x0[CPL], x1[CPL];
+      ChanRaw<T, CPL>::unpack(b[lw][0], x0);
+      ChanRaw<T, CPL>::unpack(b[lw][1], x1);
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
-        float a = acc[lw][j] * invH;
-        if (sizeof(T) == 2) a = round_bf(a);
-        r[j] = ok ? r[j] + a : r[j];
-        cacc[lw][j] = ok ? cacc[lw][j] + a : cacc[lw][j];
+        const float y0 = lw < nw ? x0[j] : 0.0f, y1 = lw < nw ? x1[j] : 0.0f;
+        acc[lw][j] = acc[lw][j] + y0;
+        if (two) acc[lw][j] = acc[lw][j] + y1;
       }
     }
+    if (hp == NP - 1) {  // row lh complete
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      frame[j] = frame[j] + r[j];
-      sRC[lt][lh][lane * CPL + j] = r[j];
+      for (int lw = 0; lw < 8; ++lw) {
+        const bool ok = sValid[(lt * 8 + lh) * 8 + lw] != 0;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          float a = acc[lw][j] * invH;
+          if (sizeof(T) == 2) a = round_bf(a);
+          r[j] = ok ? r[j] + a : r[j];
+          cacc[lw][j] = ok ? cacc[lw][j] + a : cacc[lw][j];
+          acc[lw][j] = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        frame[j] = frame[j] + r[j];
+        sRC[lt][lh][lane * CPL + j] = r[j];
+        r[j] = 0.0f;
+      }
     }
+  };
+  // (K is even; the loop has no branch around a load, so each add waits for
+  // exactly its own step: the last iteration re-reads step K - 1 as a dummy)
+  Raw b0[8][2], b1[8][2];
+  load_step(0, b0);
+  for (int k = 0; k < K; k += 2) {
+    load_step(k + 1, b1);
+    add_step(k, b0);
+    load_step(k + 2 < K ? k + 2 : K - 1, b0);
+    add_step(k + 1, b1);
   }
 #pragma unroll
   for (int j = 0; j < CPL; ++j) sF[lt][lane * CPL + j] = frame[j];
