@@ -176,20 +176,22 @@ __device__ __forceinline__ uint64_t block_incl_scan_u64(uint64_t v, SelShared& s
 // 0 < thr <= S(0).  *above = S(v + 1), the weight strictly above v.  The
 // sums are exact integers, so v is the same as a bisection on S would find.
 // Per digit: an LDS histogram of wt over the elements that match the digits
-// found so far, a suffix scan over the 256 bins, and the largest digit whose
-// suffix reaches thr.
+// found so far, then wave 0 alone scans the 256 bins from the top digit down
+// and finds the largest digit whose suffix reaches thr, and clears the other
+// histogram buffer for the next digit (two buffers alternate), so a digit
+// costs two workgroup barriers.  hist: [2][256], buffer 0 zero on entry (and
+// again on return).
 template <int EPT, bool WEIGHTED>
 __device__ __forceinline__ uint32_t radix_search(const uint32_t* key, const uint64_t* W, uint64_t present, uint64_t thr,
                                                  uint64_t* above, SelShared& sh, unsigned long long* hist) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   uint32_t prefix = 0;
   uint64_t acc = 0;  // weight of keys whose decided digits exceed the prefix
 #pragma unroll 1
   for (int level = 0; level < 4; ++level) {
     const int shift = 24 - 8 * level;
     const uint32_t hmask = level == 0 ? 0u : (0xffffffffu << (shift + 8));
-    hist[tid] = 0ull;  // kSelThreads == 256 bins
-    __syncthreads();
+    unsigned long long* hb = hist + 256 * (level & 1);
     // A thread's elements are neighbouring blocks, whose weights mostly share
     // a digit (at the first level, all of a row's weights share one or two
     // exponent bytes): runs of one digit are summed in registers and added
@@ -203,24 +205,46 @@ __device__ __forceinline__ uint32_t radix_search(const uint32_t* key, const uint
         const uint32_t b = (key[e] >> shift) & 255u;
         const uint64_t w = WEIGHTED ? W[e] : 1ull;
         if (b != run_bin) {
-          if (run_bin != 0xffffffffu) atomicAdd(&hist[run_bin], (unsigned long long)run_w);
+          if (run_bin != 0xffffffffu) atomicAdd(&hb[run_bin], (unsigned long long)run_w);
           run_bin = b;
           run_w = 0;
         }
         run_w += w;
       }
-    if (run_bin != 0xffffffffu) atomicAdd(&hist[run_bin], (unsigned long long)run_w);
+    if (run_bin != 0xffffffffu) atomicAdd(&hb[run_bin], (unsigned long long)run_w);
     __syncthreads();
-    // thread t takes bin 255 - t, so its inclusive scan is the weight of the
-    // digits >= 255 - t; the first thread whose total reaches thr owns d*
-    const uint64_t h = hist[255 - tid];
-    const uint64_t incl = block_incl_scan_u64(h, sh);
-    const uint32_t tstar = block_sum_u32(acc + incl >= thr ? 0u : 1u, sh);
-    if ((uint32_t)tid == tstar) sh.u64[0] = incl - h;  // weight of the digits > d*
+    if (tid < 64) {
+      // lane l takes digits 255 - 4 l - i (i = 0..3): inclusive sums over the
+      // descending digits; the first t = 4 l + i with acc + incl >= thr is d*
+      uint64_t h[4], p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) h[i] = hb[255 - 4 * lane - i];
+      p[0] = h[0];
+#pragma unroll
+      for (int i = 1; i < 4; ++i) p[i] = p[i - 1] + h[i];
+      uint64_t incl = p[3];
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t lo = __shfl_up((uint32_t)incl, off, 64);
+        const uint32_t hi = __shfl_up((uint32_t)(incl >> 32), off, 64);
+        if (lane >= off) incl += ((uint64_t)hi << 32) | lo;
+      }
+      const uint64_t base = incl - p[3];
+      uint32_t below = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) below += acc + base + p[i] >= thr ? 0u : 1u;
+      const uint32_t tstar = min(wave_sum_u32(below), 255u);  // (<= 255: the bins hold >= thr - acc)
+      if ((uint32_t)lane == (tstar >> 2)) {
+        const int slot = (int)(tstar & 3);
+        sh.u64[0] = base + (slot == 0 ? 0ull : slot == 1 ? p[0] : slot == 2 ? p[1] : p[2]);  // weight of digits > d*
+        sh.u32[0] = tstar;
+      }
+      unsigned long long* hn = hist + 256 * ((level + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hn[4 * lane + i] = 0ull;
+    }
     __syncthreads();
     acc += sh.u64[0];
-    __syncthreads();
-    prefix |= (255u - tstar) << shift;
+    prefix |= (255u - sh.u32[0]) << shift;
   }
   *above = acc;
   return prefix;
@@ -248,11 +272,15 @@ template <int EPT>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   static_assert(kSelThreads == 256, "one radix bin per thread");
   __shared__ SelShared sh;
-  __shared__ unsigned long long hist[256];
+  __shared__ unsigned long long hist[2 * 256];
   const int tid = threadIdx.x;
+  hist[tid] = 0ull;  // buffer 0 of the radix searches
+  __syncthreads();
   const int64_t row = blockIdx.x;
   const float* s = a.scores + row * a.N;
   const int64_t N = a.N;
+
+  const int64_t j0 = (int64_t)tid * EPT;
 
   uint32_t key[EPT];
   uint64_t W[EPT];
@@ -357,26 +385,50 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   // ranks the ties and one scan of per-thread output counts places the lists.
   int32_t* trow = a.tiles + row * a.tcap;
   int32_t* brow = a.sel_blocks ? a.sel_blocks + row * a.bcap : nullptr;
-  const int64_t j0 = (int64_t)tid * EPT;
   uint32_t nties = 0;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) nties += (eff > 0 && ((present >> e) & 1) && key[e] == v_e) ? 1u : 0u;
   uint32_t tot;
   uint32_t rank = block_excl_scan_u32(nties, sh, &tot);
   uint64_t selm = 0;  // bit e: block j0 + e is selected
-  uint32_t packed = 0;  // tiles | blocks << 16 of this thread
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const bool pres = (present >> e) & 1;
     const bool tie = eff > 0 && pres && key[e] == v_e;
     const bool sel = eff > 0 && pres && (key[e] > v_e || (tie && rank < need));
     rank += tie ? 1u : 0u;
-    if (sel) {
-      const int32_t t0 = a.block_first_tile[j0 + e], t1 = a.block_first_tile[j0 + e + 1];
-      uint32_t nt = 0;
-      for (int32_t t = t0; t < t1; ++t) nt += (a.tile_count == nullptr || a.tile_count[t] > 0) ? 1u : 0u;
-      packed += nt | (1u << 16);
-      selm |= 1ull << e;
+    selm |= sel ? 1ull << e : 0ull;
+  }
+  // tiles of the selected blocks: all first-tile entries are read at once,
+  // then the tile counts of the selected blocks' tiles (two round trips, not
+  // two per selected block); tinfo[e] = first / second tile listed, or
+  // bit 2 for a block of more than two tiles (counted by a loop)
+  int32_t fb[EPT + 1];
+#pragma unroll
+  for (int e = 0; e <= EPT; ++e) {
+    // (first tile of a selected block e, or end of a selected block e - 1)
+    const bool need = (e < EPT && ((selm >> e) & 1)) || (e > 0 && ((selm >> (e - 1)) & 1));
+    fb[e] = need ? a.block_first_tile[j0 + e] : 0;
+  }
+  uint32_t tinfo[EPT];
+  uint32_t packed = 0;  // tiles | blocks << 16 of this thread
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    tinfo[e] = 0;
+    if ((selm >> e) & 1) {
+      const int32_t t0 = fb[e], nt = fb[e + 1] - t0;
+      uint32_t cnt;
+      if (nt <= 2) {
+        const bool ok0 = nt >= 1 && (a.tile_count == nullptr || a.tile_count[t0] > 0);
+        const bool ok1 = nt >= 2 && (a.tile_count == nullptr || a.tile_count[t0 + 1] > 0);
+        tinfo[e] = (ok0 ? 1u : 0u) | (ok1 ? 2u : 0u);
+        cnt = (ok0 ? 1u : 0u) + (ok1 ? 1u : 0u);
+      } else {
+        tinfo[e] = 4u;
+        cnt = 0;
+        for (int32_t t = t0; t < t0 + nt; ++t) cnt += (a.tile_count == nullptr || a.tile_count[t] > 0) ? 1u : 0u;
+      }
+      packed += cnt | (1u << 16);
     }
   }
   const uint32_t pos = block_excl_scan_u32(packed, sh, &tot);
@@ -384,12 +436,23 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     if ((selm >> e) & 1) {
-      const int32_t t0 = a.block_first_tile[j0 + e], t1 = a.block_first_tile[j0 + e + 1];
-      for (int32_t t = t0; t < t1; ++t)
-        if (a.tile_count == nullptr || a.tile_count[t] > 0) {
-          if (p < a.tcap) trow[p] = t;
+      const int32_t t0 = fb[e];
+      if (tinfo[e] < 4u) {
+        if (tinfo[e] & 1u) {
+          if (p < a.tcap) trow[p] = t0;
           ++p;
         }
+        if (tinfo[e] & 2u) {
+          if (p < a.tcap) trow[p] = t0 + 1;
+          ++p;
+        }
+      } else {
+        for (int32_t t = t0; t < fb[e + 1]; ++t)
+          if (a.tile_count == nullptr || a.tile_count[t] > 0) {
+            if (p < a.tcap) trow[p] = t;
+            ++p;
+          }
+      }
       if (brow) brow[q] = (int32_t)(j0 + e);
       ++q;
     }
