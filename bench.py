@@ -397,6 +397,9 @@ def main():
     ap.add_argument("--bridge", action="store_true",
                     help="the a2v bridge o-projection with fused residual norms (prism_linear_rownorm) at the "
                          "config's tokens and C, against torch F.linear + the norm kernel (one JSON line)")
+    ap.add_argument("--compact-lists", action="store_true",
+                    help="keep the work lists in compact CSR form (bsa_params compact_lists); reported in config, "
+                         "not the default headline")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=8.0,
@@ -450,7 +453,7 @@ def main():
         sparsity, cdf = inp["sp_only"], None
     else:
         sparsity, cdf = 1.0 - (inp["topk"] + 0.5) / N_b, inp["cdf"]
-    dyn.bsa_params.update({"sparsity": sparsity, "cdf_threshold": cdf})
+    dyn.bsa_params.update({"sparsity": sparsity, "cdf_threshold": cdf, "compact_lists": bool(args.compact_lists)})
     log(f"[bench] N_b={N_b} sparsity={sparsity:.6f} cdf={cdf}")
 
     q = inp["q"].clone().requires_grad_(True)
@@ -491,7 +494,13 @@ def main():
     # the plan of these inputs (deterministic: identical to the one inside each step)
     with torch.no_grad():
         plan = plan_dynamic(q.detach(), k.detach(), v.detach(), gp, method="ivpq", sparsity=sparsity,
-                            cdf_threshold=cdf, audio_token_norms=norms0, input_grid=grid)
+                            cdf_threshold=cdf, audio_token_norms=norms0, input_grid=grid,
+                            compact_lists=bool(args.compact_lists))
+        plan.build_key_lists()
+    # bytes of the work lists a step keeps until its backward (per-query-tile
+    # lists and their pair unions, per-key-tile lists and theirs)
+    list_bytes = sum(t.numel() * t.element_size() for t in (plan.qcols, plan.qunion[2], plan.klists[2],
+                                                            plan.kunion[2]))
     sum_lens = plan.sum_lens()
     Nt, Nb, Sp = plan.lay.Nt, plan.lay.N_b, plan.S
     density = sum_lens / (B * H * Nt * Nt)
@@ -574,6 +583,7 @@ def main():
                    "density_valid_q": round(density_valid, 4), "pair_union_efficiency": round(union_eff, 4),
                    "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3),
                    "ms_per_step_median": round(ms_median, 3),
+                   "compact_lists": bool(args.compact_lists), "list_bytes": list_bytes,
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "dense": dense, "breakdown": breakdown,

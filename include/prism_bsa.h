@@ -236,6 +236,24 @@ int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* co
                      int64_t col_tiles, const int32_t* pairmap, const uint64_t* tile_masks, int64_t ucap,
                      int64_t* ustart, int32_t* ulen, int32_t* ucols, hipStream_t stream);
 
+/* Compact CSR of per-row lists (the select and list-transpose output form of
+ * the drop-in operators: offsets int32 [rows + 1], entries int32 [nnz]) from the
+ * (start, len, cols) lists the other entry points produce, whose rows sit
+ * anywhere in cols (prism_select_tiles + prism_tile_rows: bsa_interface.py
+ * :235-304 with dynamic_block_attention.py:297-319; prism_transpose_lists:
+ * create_indices_k_from_indices_q_varlen, bsa_interface.py:147-161;
+ * prism_pair_union).  Two calls so that the caller can allocate the entries:
+ * prism_lists_csr_offsets writes offsets[r] = sum of len[0..r) (negative
+ * lengths count as 0) and the int64 total to *total (one int64 on the
+ * device; a total past 2^31 - 1 does not fit the offsets); then
+ * prism_lists_csr_fill copies row r's len[r] entries from cols + start[r] to
+ * out_cols + offsets[r].  The attention kernels take the result as lists
+ * with start = offsets[r], len = offsets[r + 1] - offsets[r]. */
+int prism_lists_csr_offsets(const int32_t* len, int64_t rows, int32_t* offsets, int64_t* total,
+                            hipStream_t stream);
+int prism_lists_csr_fill(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows,
+                         const int32_t* offsets, int32_t* out_cols, hipStream_t stream);
+
 /* Pairing of the tiles that the paired kernels process together: inside each
  * group of 8 consecutive tiles of a head (fewer at a head's end), the perfect
  * matching with the largest summed list overlap |A n B| over its pairs (ties:

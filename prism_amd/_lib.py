@@ -42,6 +42,8 @@ SIGNATURES = {
     "prism_pair_union": [P, P, P, I64, I64, I64, P, P, I64, P, P, P, P],
     "prism_pair_tiles": [P, P, P, I64, I64, I64, P, P],
     "prism_pair_order": [P, I64, I32, I64, P, P],
+    "prism_lists_csr_offsets": [P, I64, P, P, P],
+    "prism_lists_csr_fill": [P, P, P, I64, P, P, P],
     "prism_tile_masks": [P, I64, P, P],
     "prism_lse_to_m2": [P, I64, P, P],
     "prism_bsa_fwd": [P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P],

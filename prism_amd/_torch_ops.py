@@ -160,6 +160,11 @@ def _register_fakes():
     def _(ulen, group, tail):
         return _empty(ulen, (ulen.numel(),), i32)
 
+    @reg("prism::lists_to_csr")
+    def _(start, length, cols):
+        nnz = torch.library.get_ctx().new_dynamic_size()
+        return _empty(start, (start.numel() + 1,), i32), _empty(start, (nnz,), i32)
+
     @reg("prism::tile_masks")
     def _(valid):
         return _empty(valid, (valid.numel() // 64,), i64)

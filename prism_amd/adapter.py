@@ -77,7 +77,9 @@ def valid_mask_for(grid_size, device) -> Optional[torch.Tensor]:
 class DynamicBlockSparseAttention:
     """State the reference keeps on SelfAttention for the dynamic path: the
     bsa_params dict, the method switch and the per-pass shape cache
-    (wan_video_dit.py:22-33, :401-427)."""
+    (wan_video_dit.py:22-33, :401-427).  One key beyond the reference's:
+    bsa_params["compact_lists"] = True keeps the work lists in compact CSR
+    form until the backward (O(nnz) memory; identical results)."""
 
     def __init__(self, method: str = "ivpq", bsa_params: Optional[dict] = None):
         if method not in ("ivpq", "penalty"):
@@ -117,7 +119,8 @@ class DynamicBlockSparseAttention:
             audio_token_norms=None if audio_token_norms is None else audio_token_norms.reshape(-1),
             lambda_a=p.get("dynamic_block_lambda_a", 0.5), tau_128=p.get("dynamic_block_tau_128", 0.15),
             lambda_128=p.get("dynamic_block_lambda_128", 1.0), shape_ids=cached, return_shape_ids=True,
-            input_grid=(T, H, W), compute_padded_queries=False)  # padded rows are sliced away (:429-431)
+            input_grid=(T, H, W), compute_padded_queries=False,  # padded rows are sliced away (:429-431)
+            compact_lists=bool(p.get("compact_lists", False)))
         if self.training:
             self._dyn_shape_cache = (self.pass_id, grid_padded, used)
         return out
@@ -137,7 +140,8 @@ def run_bsa_uniform(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid_size
     chunk_3d_shape_q / _k (default 4x4x4), the padding is masked, and the
     output has the unpadded THW shape.  Here the padding, the rearrangement
     and the unpadding happen inside the chunk gather / scatter kernels (no
-    padded copies of q, k, v or the output)."""
+    padded copies of q, k, v or the output).  bsa_params["compact_lists"]
+    keeps the work lists in compact CSR form, as in the dynamic branch."""
     B, Hn, S, D = q.shape
     T, H, W = (int(x) for x in grid_size)
     assert T * H * W == S
@@ -149,5 +153,6 @@ def run_bsa_uniform(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid_size
     lq = ops.ChunkLayout((T, H, W), cq, q.device, pgrid=pgrid)
     lk = ops.ChunkLayout((T, H, W), ck, q.device, pgrid=pgrid)
     return bsa_chunked(q, k, v, lq, lk, sparsity=kw.get("sparsity", 0.875), cdf_threshold=kw.get("cdf_threshold"),
-                       sm_scale=1.0 / (D ** 0.5), compute_padded_queries=compute_padded_queries)
+                       sm_scale=1.0 / (D ** 0.5), compute_padded_queries=compute_padded_queries,
+                       compact_lists=bool(kw.get("compact_lists", False)))
 

@@ -14,6 +14,8 @@
 // natural-log LSE into the base-2 row maximum the backward exponentiates
 // against, with -inf (a row that saw no valid key) mapped to +inf so that
 // exp2(s - m2) is exactly 0 for it without a per-element test.
+// prism_lists_csr_offsets / prism_lists_csr_fill turn any (start, len, cols)
+// lists into compact CSR (int32 offsets, entries stored once, O(nnz) memory).
 #include "common.h"
 
 namespace {
@@ -244,9 +246,84 @@ __global__ __launch_bounds__(1024) void pair_order_kernel(const int32_t* __restr
   for (int i = threadIdx.x; i < T; i += blockDim.x) order[k + i] = (int32_t)(key[i] & 0xffffffffu);
 }
 
+// ------------------------------------------------------------------ compact CSR
+// offsets[r] = sum of len[0..r) as int32, *total = the int64 sum (so the
+// caller can reject a total past int32).  One workgroup: thread t sums a
+// contiguous chunk of rows, a block scan places the chunks.
+constexpr int kCsrThreads = 1024;
+
+__global__ __launch_bounds__(kCsrThreads) void csr_offsets_kernel(const int32_t* __restrict__ len, int64_t rows,
+                                                                  int32_t* __restrict__ offsets,
+                                                                  int64_t* __restrict__ total) {
+  __shared__ int64_t wsum[kCsrThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t chunk = (rows + kCsrThreads - 1) / kCsrThreads;
+  const int64_t r0 = (int64_t)tid * chunk, r1 = r0 + chunk < rows ? r0 + chunk : rows;
+  int64_t part = 0;
+  for (int64_t r = r0; r < r1; ++r) part += len[r] > 0 ? len[r] : 0;
+  // inclusive scan of the 64-bit chunk sums over the workgroup
+  int64_t incl = part;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t lo = __shfl_up((uint32_t)incl, off, 64);
+    const uint32_t hi = __shfl_up((uint32_t)((uint64_t)incl >> 32), off, 64);
+    if (lane >= off) incl += (int64_t)(((uint64_t)hi << 32) | lo);
+  }
+  if (lane == 63) wsum[wid] = incl;
+  __syncthreads();
+  int64_t before = 0, all = 0;
+  for (int v = 0; v < kCsrThreads / 64; ++v) {
+    before += v < wid ? wsum[v] : 0;
+    all += wsum[v];
+  }
+  int64_t run = before + incl - part;
+  for (int64_t r = r0; r < r1; ++r) {
+    offsets[r] = (int32_t)run;
+    run += len[r] > 0 ? len[r] : 0;
+  }
+  if (tid == 0) {
+    offsets[rows] = (int32_t)all;
+    *total = all;
+  }
+}
+
+// one wave per row: row r's len[r] entries from cols + start[r] to
+// out + offsets[r]
+__global__ __launch_bounds__(256) void csr_fill_kernel(const int64_t* __restrict__ start,
+                                                       const int32_t* __restrict__ len,
+                                                       const int32_t* __restrict__ cols, int64_t rows,
+                                                       const int32_t* __restrict__ offsets,
+                                                       int32_t* __restrict__ out) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int32_t n = len[r];
+  const int32_t* src = cols + start[r];
+  int32_t* dst = out + offsets[r];
+  for (int32_t i = lane; i < n; i += 64) dst[i] = src[i];
+}
+
 }  // namespace
 
 extern "C" {
+
+int prism_lists_csr_offsets(const int32_t* len, int64_t rows, int32_t* offsets, int64_t* total,
+                            hipStream_t stream) {
+  PRISM_REQUIRE(offsets && total && (len || rows == 0), "prism_lists_csr_offsets: null pointer");
+  PRISM_REQUIRE(rows >= 0, "prism_lists_csr_offsets: negative row count");
+  csr_offsets_kernel<<<1, kCsrThreads, 0, stream>>>(len, rows, offsets, total);
+  PRISM_LAUNCH_CHECK("prism_lists_csr_offsets");
+  return PRISM_OK;
+}
+
+int prism_lists_csr_fill(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows,
+                         const int32_t* offsets, int32_t* out_cols, hipStream_t stream) {
+  PRISM_REQUIRE(rows >= 0 && rows < (1ll << 33), "prism_lists_csr_fill: row count out of range");
+  if (rows == 0) return PRISM_OK;
+  PRISM_REQUIRE(start && len && cols && offsets && out_cols, "prism_lists_csr_fill: null pointer");
+  csr_fill_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, stream>>>(start, len, cols, rows, offsets, out_cols);
+  PRISM_LAUNCH_CHECK("prism_lists_csr_fill");
+  return PRISM_OK;
+}
 
 int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
                      int64_t col_tiles, const int32_t* pairmap, const uint64_t* tile_masks, int64_t ucap,

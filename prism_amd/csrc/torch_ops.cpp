@@ -440,6 +440,28 @@ std::tuple<Tensor, Tensor, Tensor> pair_union(const Tensor& s_, const Tensor& l_
   return {ustart, ulen, ucols};
 }
 
+// compact CSR of (start, len, cols) lists: offsets int32 [rows + 1], cols
+// int32 [nnz].  One host read of nnz (the allocation size) between the two
+// launches.
+std::tuple<Tensor, Tensor> lists_to_csr(const Tensor& s_, const Tensor& l_, const Tensor& c_) {
+  check_lists(s_, l_, c_);
+  TORCH_CHECK(s_.numel() == l_.numel(), "prism.lists_to_csr: start and len differ in length");
+  const c10::DeviceGuard guard(s_.device());
+  const Tensor s = s_.contiguous(), l = l_.contiguous(), c = c_.contiguous();
+  const int64_t rows = s.numel();
+  Tensor offsets = at::empty({rows + 1}, opts(s, at::kInt));
+  Tensor total = at::empty({1}, opts(s, at::kLong));
+  PRISM_TORCH_CALL(prism_lists_csr_offsets, l.data_ptr<int32_t>(), rows, offsets.data_ptr<int32_t>(),
+                   total.data_ptr<int64_t>(), stream_of(s));
+  const int64_t nnz = total.item<int64_t>();
+  TORCH_CHECK_VALUE(nnz <= 2147483647ll, "prism.lists_to_csr: more than 2^31 - 1 list entries (int32 offsets)");
+  Tensor out = at::empty({nnz}, opts(s, at::kInt));
+  if (nnz > 0)
+    PRISM_TORCH_CALL(prism_lists_csr_fill, s.data_ptr<int64_t>(), l.data_ptr<int32_t>(), c.data_ptr<int32_t>(), rows,
+                   offsets.data_ptr<int32_t>(), out.data_ptr<int32_t>(), stream_of(s));
+  return {offsets, out};
+}
+
 Tensor pair_order(const Tensor& ulen_, int64_t group, int64_t tail) {
   on_gpu(ulen_, "ulen");
   check_dtype(ulen_, at::kInt, "ulen");
@@ -614,6 +636,7 @@ TORCH_LIBRARY(prism, m) {
   m.def("pair_union(Tensor start, Tensor len, Tensor cols, int row_tiles, int col_tiles, Tensor? pairmap, "
         "Tensor? tile_masks) -> (Tensor, Tensor, Tensor)");
   m.def("pair_order(Tensor ulen, int group, int tail) -> Tensor");
+  m.def("lists_to_csr(Tensor start, Tensor len, Tensor cols) -> (Tensor, Tensor)");
   m.def("tile_masks(Tensor valid) -> Tensor");
   m.def("lse_to_m2(Tensor lse) -> Tensor");
   m.def("bsa_fwd(Tensor q, Tensor k, Tensor v, Tensor? tile_masks, Tensor ustart, Tensor ulen, Tensor ucols, "
@@ -647,6 +670,7 @@ TORCH_LIBRARY_IMPL(prism, CUDA, m) {
   m.impl("pair_tiles", &pair_tiles);
   m.impl("pair_union", &pair_union);
   m.impl("pair_order", &pair_order);
+  m.impl("lists_to_csr", &lists_to_csr);
   m.impl("tile_masks", &tile_masks);
   m.impl("lse_to_m2", &lse_to_m2);
   m.impl("bsa_fwd", &bsa_fwd);

@@ -52,7 +52,7 @@ class _Plan:
     """Everything the attention kernels need for one call, built under no_grad."""
 
     def __init__(self, q, k, v, grid, shape_ids, valid_mask, sparsity, cdf_threshold, sm_scale,
-                 compute_padded_queries=False, box=None, keep_scores=False):
+                 compute_padded_queries=False, box=None, keep_scores=False, compact_lists=False):
         B, H, _, D = q.shape
         self.lay = ops.ZoneLayout(shape_ids, grid, box)
         lay = self.lay
@@ -80,12 +80,22 @@ class _Plan:
         self.qstart, self.qlen = ops.tile_rows(sel["ntiles"], lay.block_id_of_tile, B * H, lay.Nt, lay.N_b,
                                                sel["tcap"], self.tile_count if skip else None)
         self.qcols = sel["tiles"].view(-1)
+        # compact lists: every list the plan keeps (per query tile, pair
+        # unions, and in the backward per key tile and its unions) in CSR
+        # form, O(nnz) memory instead of rows x capacity (one host read of
+        # nnz each); same entries in the same order, so identical results
+        self.compact = compact_lists
+        if compact_lists:
+            self.qstart, self.qlen, self.qcols = self._compact(self.qstart, self.qlen, self.qcols)
+            self.sel = {key: val for key, val in sel.items() if key != "tiles"}
         # pair unions of the per-query-tile key lists (forward, dQ) and the key
         # validity words of padded key tiles
         self.tmasks = ops.tile_masks(self.kv_valid) if masked else None
         # pair the query tiles of each zone by list overlap (fewest idle wave slots)
         self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lay.Nt)
         self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks, pairmap=self.qpair)
+        if compact_lists:
+            self.qunion = self._compact(*self.qunion)
         # launch order of the forward and dQ kernels (the last workgroups ids
         # take the longest lists first: the launch does not end on a long one)
         self.qorder = ops.pair_order(self.qunion[1], 64)
@@ -93,6 +103,26 @@ class _Plan:
         self.kpair = None
         self.kunion = None
         self.korder = None
+
+    @staticmethod
+    def _compact(start, length, cols):
+        offsets, entries = ops.lists_to_csr(start, length, cols)
+        return (*ops.csr_lists(offsets), entries)
+
+    def build_key_lists(self):
+        """Per-key-tile query lists, their pairing, unions and launch order
+        (the dK/dV side), built on first use."""
+        if self.kunion is not None:
+            return
+        Nt = self.lay.Nt
+        self.klists = ops.transpose_lists(self.qstart, self.qlen, self.qcols, self.B * self.H, Nt)
+        if self.compact:
+            self.klists = self._compact(*self.klists)
+        self.kpair = ops.pair_tiles(*self.klists, Nt)
+        self.kunion = ops.pair_union(*self.klists, Nt, pairmap=self.kpair)
+        if self.compact:
+            self.kunion = self._compact(*self.kunion)
+        self.korder = ops.pair_order(self.kunion[1], 32)
 
     def sum_lens(self) -> int:
         """Executed (query tile, key tile) pairs (host sync)."""
@@ -121,11 +151,7 @@ class _DynBSA(torch.autograd.Function):
         lay = plan.lay
         gd = ops.gather_pool(do.contiguous(), lay, None, rows=True, dot_with=o_re)
         do_re, delta = gd["rows"], gd["rowdot"]
-        if plan.kunion is None:
-            plan.klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, plan.B * plan.H, lay.Nt)
-            plan.kpair = ops.pair_tiles(*plan.klists, lay.Nt)
-            plan.kunion = ops.pair_union(*plan.klists, lay.Nt, pairmap=plan.kpair)
-            plan.korder = ops.pair_order(plan.kunion[1], 32)
+        plan.build_key_lists()
         m2 = ops.lse_to_m2(lse)
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid,
                                           plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale, plan.qpair, plan.kpair,
@@ -139,7 +165,7 @@ class _DynBSA(torch.autograd.Function):
 
 def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold=None, audio_token_norms=None,
                  valid_mask=None, lambda_a=0.5, tau_128=0.15, lambda_128=1.0, shape_ids=None,
-                 compute_padded_queries=False, input_grid=None, keep_scores=False) -> _Plan:
+                 compute_padded_queries=False, input_grid=None, keep_scores=False, compact_lists=False) -> _Plan:
     """Steps (1)-(5) of flash_attn_bsa_3d_dynamic: shape ids, layout, pooled
     scores, selection and tile lists (no attention).
 
@@ -149,7 +175,9 @@ def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold
     kernels, with results identical to padding first.  compute_padded_queries
     defaults to False here, the adapters' setting (flash_attn_bsa_3d_dynamic
     passes True unless told otherwise).  keep_scores keeps the fp32 block
-    scores on the plan (plan.scores) for inspection."""
+    scores on the plan (plan.scores) for inspection.  compact_lists keeps every
+    work list in compact CSR form (memory O(nnz): ~0.3 GB instead of ~2.3 GB
+    of list buffers per call at config 4), at one host read per list."""
     B, Hn, S, D = q.shape
     T, H, W = grid_padded
     box = tuple(input_grid) if input_grid is not None else (T, H, W)
@@ -168,7 +196,7 @@ def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold
             shape_ids = _gradient_and_shapes(v.detach(), audio_token_norms, (T, H, W), method, lambda_a, tau_128,
                                              lambda_128, valid_mask, box)[2]
         return _Plan(q.detach(), k.detach(), v.detach(), (T, H, W), shape_ids, valid_mask, sparsity, cdf_threshold,
-                     sm_scale, compute_padded_queries, box, keep_scores)
+                     sm_scale, compute_padded_queries, box, keep_scores, compact_lists)
 
 
 def flash_attn_bsa_3d_dynamic(
@@ -189,6 +217,7 @@ def flash_attn_bsa_3d_dynamic(
     return_shape_ids: bool = False,
     compute_padded_queries: bool = True,
     input_grid: Optional[Tuple[int, int, int]] = None,
+    compact_lists: bool = False,
 ):
     """Dynamic-block-shape BSA for video self-attention; returns [B,H,S,D] in
     THW order (dynamic_block_attention.py:194-332).  q, k, v: [B,H,S,D] THW
@@ -209,11 +238,16 @@ def flash_attn_bsa_3d_dynamic(
     grid_padded is its round-up to multiples of 8, and the output (and the
     gradients) come back unpadded.  This is the padding, valid mask and
     unpadding of wan_video_dit.py:342-431 done inside the gather and scatter
-    kernels; the result equals padding first and slicing after, bit for bit."""
+    kernels; the result equals padding first and slicing after, bit for bit.
+
+    compact_lists (not in the reference's signature) keeps the work lists in
+    compact CSR form (O(nnz) memory) until the backward; results are
+    identical."""
     plan = plan_dynamic(q, k, v, grid_padded, method=method, sparsity=sparsity, cdf_threshold=cdf_threshold,
                         audio_token_norms=audio_token_norms, valid_mask=valid_mask, lambda_a=lambda_a,
                         tau_128=tau_128, lambda_128=lambda_128, shape_ids=shape_ids,
-                        compute_padded_queries=compute_padded_queries, input_grid=input_grid)
+                        compute_padded_queries=compute_padded_queries, input_grid=input_grid,
+                        compact_lists=compact_lists)
     sm_scale = 1.0 / (q.shape[-1] ** 0.5)
     out = _DynBSA.apply(q, k, v, plan, sm_scale)
     if return_shape_ids:

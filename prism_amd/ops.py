@@ -403,6 +403,47 @@ def transpose_lists(qstart: torch.Tensor, qlen: torch.Tensor, qcols: torch.Tenso
     return _op("transpose_lists", qstart, qlen, qcols, int(BH), Ntq, Ntk)
 
 
+def lists_to_csr(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor):
+    """Compact CSR of per-row lists given as (start int64, len int32, cols
+    int32) with rows anywhere in cols (the outputs of tile_rows over
+    select_tiles, transpose_lists and pair_union): returns (offsets int32
+    [rows + 1], entries int32 [nnz]), row r's entries at
+    [offsets[r], offsets[r + 1]).  Memory O(nnz) instead of the producers'
+    rows x capacity buffers; one host read of nnz."""
+    _cuda(start, length, cols)
+    return _op("lists_to_csr", start, length, cols)
+
+
+def csr_lists(offsets: torch.Tensor):
+    """(start int64 [rows], len int32 [rows]) of CSR offsets: the list form the
+    pair, union and attention kernels take (entries unchanged)."""
+    o = offsets.to(torch.int64)
+    return o[:-1].contiguous(), (o[1:] - o[:-1]).to(torch.int32)
+
+
+def select_csr(scores: torch.Tensor, sparsity, cdf_threshold, sm_scale: float, lay: "ZoneLayout",
+               tile_count: Optional[torch.Tensor] = None, q_tile_count: Optional[torch.Tensor] = None):
+    """Block selection as CSR per query tile (get_select_indices_* of
+    bsa_interface.py:235-304 expanded to tiles, dynamic_block_attention.py
+    :297-319): scores [BH, N_b, N_b] fp32 -> (offsets int32 [BH*Nt + 1], key
+    tiles int32 [nnz]), each query tile's list ascending.  tile_count drops
+    padded key tiles; q_tile_count gives query tiles without a valid token an
+    empty list.  The dense-compat form is select_tiles + tile_rows."""
+    BH = scores.shape[0]
+    sel = select_tiles(scores, sparsity, cdf_threshold, sm_scale, lay.block_first_tile, tile_count)
+    qstart, qlen = tile_rows(sel["ntiles"], lay.block_id_of_tile, BH, lay.Nt, lay.N_b, sel["tcap"], q_tile_count)
+    return lists_to_csr(qstart, qlen, sel["tiles"].view(-1))
+
+
+def transpose_csr(offsets: torch.Tensor, cols: torch.Tensor, BH: int, Nt: int, Ntk: Optional[int] = None):
+    """CSR per query tile -> CSR per key tile (csr_transpose;
+    create_indices_k_from_indices_q_varlen, bsa_interface.py:147-161): each key
+    tile's ascending query tiles.  Returns (offsets int32 [BH*Ntk + 1],
+    query tiles int32 [nnz])."""
+    start, length = csr_lists(offsets)
+    return lists_to_csr(*transpose_lists(start, length, cols, BH, Nt, Ntk))
+
+
 # ------------------------------------------------------------------ attention
 def pair_tiles(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt: int,
                col_tiles: Optional[int] = None) -> torch.Tensor:

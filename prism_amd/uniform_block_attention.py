@@ -38,11 +38,16 @@ import torch
 from . import ops
 
 
+def _compact(start, length, cols):
+    offsets, entries = ops.lists_to_csr(start, length, cols)
+    return (*ops.csr_lists(offsets), entries)
+
+
 class _ChunkPlan:
     """Rearranged rows, selection and work lists of one call (built under no_grad)."""
 
     def __init__(self, q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, q_valid, k_valid, sparsity,
-                 cdf_threshold, sm_scale, compute_padded_queries=False, keep_scores=False):
+                 cdf_threshold, sm_scale, compute_padded_queries=False, keep_scores=False, compact_lists=False):
         B, H, _, D = q.shape
         BH = B * H
         self.lq, self.lk = lq, lk
@@ -71,10 +76,17 @@ class _ChunkPlan:
         self.qstart, self.qlen = ops.tile_rows(sel["ntiles"], lq.block_id_of_tile, BH, lq.Nt, lq.N_b, sel["tcap"],
                                                qcount)
         self.qcols = sel["tiles"].view(-1)
+        # compact lists: the kept lists in CSR form, O(nnz) memory (same entries)
+        self.compact = compact_lists
+        if compact_lists:
+            self.qstart, self.qlen, self.qcols = _compact(self.qstart, self.qlen, self.qcols)
+            self.sel = {key: val for key, val in sel.items() if key != "tiles"}
         self.tmasks = ops.tile_masks(self.kv_valid) if k_masked else None
         self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lq.Nt, lk.Nt)
         self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lq.Nt, self.tmasks, col_tiles=lk.Nt,
                                      pairmap=self.qpair)
+        if compact_lists:
+            self.qunion = _compact(*self.qunion)
         # launch order of the forward and dQ kernels (longest lists last-dispatched first)
         self.qorder = ops.pair_order(self.qunion[1], 64)
         self.klists = None
@@ -86,8 +98,12 @@ class _ChunkPlan:
         if self.kunion is None:
             self.klists = ops.transpose_lists(self.qstart, self.qlen, self.qcols, self.B * self.H, self.lq.Nt,
                                               self.lk.Nt)
+            if self.compact:
+                self.klists = _compact(*self.klists)
             self.kpair = ops.pair_tiles(*self.klists, self.lk.Nt, self.lq.Nt)
             self.kunion = ops.pair_union(*self.klists, self.lk.Nt, None, col_tiles=self.lq.Nt, pairmap=self.kpair)
+            if self.compact:
+                self.kunion = _compact(*self.kunion)
             self.korder = ops.pair_order(self.kunion[1], 32)
         return self.kunion
 
@@ -138,22 +154,25 @@ def _check_qkv(q, k, v):
 
 
 def plan_chunked(q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, *, sparsity, cdf_threshold, sm_scale,
-                 q_valid=None, k_valid=None, compute_padded_queries=False, keep_scores=False) -> _ChunkPlan:
+                 q_valid=None, k_valid=None, compute_padded_queries=False, keep_scores=False,
+                 compact_lists=False) -> _ChunkPlan:
     """Selection half of the uniform path (no attention).  keep_scores keeps
-    the fp32 chunk scores on the plan (plan.scores) for inspection."""
+    the fp32 chunk scores on the plan (plan.scores) for inspection;
+    compact_lists keeps the work lists in compact CSR form (O(nnz) memory)."""
     if sparsity is None and cdf_threshold is None:
         raise ValueError("Either sparsity or cdf_threshold must be provided")
     with torch.no_grad():
         return _ChunkPlan(q.detach(), k.detach(), v.detach(), lq, lk, q_valid, k_valid, sparsity, cdf_threshold,
-                          sm_scale, compute_padded_queries, keep_scores)
+                          sm_scale, compute_padded_queries, keep_scores, compact_lists)
 
 
 def bsa_chunked(q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, *, sparsity, cdf_threshold, sm_scale,
-                q_valid=None, k_valid=None, compute_padded_queries=False) -> torch.Tensor:
+                q_valid=None, k_valid=None, compute_padded_queries=False, compact_lists=False) -> torch.Tensor:
     """Uniform BSA of q [B,H,Sq,D] (THW of lq.grid) over k, v [B,H,Sk,D] (THW
     of lk.grid); returns [B,H,Sq,D] in q's dtype and order."""
     plan = plan_chunked(q, k, v, lq, lk, sparsity=sparsity, cdf_threshold=cdf_threshold, sm_scale=sm_scale,
-                        q_valid=q_valid, k_valid=k_valid, compute_padded_queries=compute_padded_queries)
+                        q_valid=q_valid, k_valid=k_valid, compute_padded_queries=compute_padded_queries,
+                        compact_lists=compact_lists)
     return _ChunkBSA.apply(q, k, v, plan, sm_scale)
 
 

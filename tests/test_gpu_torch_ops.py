@@ -77,6 +77,11 @@ def test_opcheck_selection_and_lists(plan):
     _check("pair_tiles", p.qstart, p.qlen, p.qcols, lay.Nt, lay.Nt)
     _check("pair_union", p.qstart, p.qlen, p.qcols, lay.Nt, lay.Nt, p.qpair, p.tmasks)
     _check("pair_order", p.qunion[1], 64, 8)
+    # (data-dependent output length: schema check; the fake's symbolic size is
+    # covered on the CPU)
+    print("[case] opcheck lists_to_csr", flush=True)
+    torch.library.opcheck(torch.ops.prism.lists_to_csr.default, (p.qstart, p.qlen, p.qcols),
+                          test_utils=("test_schema",))
     _check("tile_masks", p.kv_valid)
 
 

@@ -10,7 +10,7 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 OPS = ["zone_stats", "audio_zone_stats", "zone_gradient", "zone_shapes", "assign_shapes", "a2v_norms", "zone_layout",
        "rearrange_index", "gather_pool", "scatter_rows", "chunk_gather_pool", "chunk_scatter_rows", "block_scores",
        "select_tiles", "tile_rows", "transpose_lists", "pair_tiles", "pair_union", "pair_order", "tile_masks",
-       "lse_to_m2", "bsa_fwd", "bwd_preprocess", "bsa_bwd_dkdv", "bsa_bwd_dq", "linear_rownorm"]
+       "lse_to_m2", "bsa_fwd", "bwd_preprocess", "bsa_bwd_dkdv", "bsa_bwd_dq", "linear_rownorm", "lists_to_csr"]
 
 
 @pytest.fixture(scope="module")
@@ -78,6 +78,17 @@ def test_fake_shapes(prism):
                                     True, True, None)
         assert r[0].shape == (B, H, 256, D) and r[1].shape == (B, H, 4, D) and r[3].shape == (4,)
         assert prism.chunk_scatter_rows(r[0], [1, 1, 200], [1, 1, 256], [1, 1, 64], 1).shape == (B, H, 200, D)
+
+
+def test_fake_csr_has_a_data_dependent_size(prism):
+    """lists_to_csr's entry count is data-dependent: under a shape
+    environment its fake output has an unbacked symbolic length."""
+    from torch.fx.experimental.symbolic_shapes import ShapeEnv
+    i32, i64 = torch.int32, torch.int64
+    with FakeTensorMode(shape_env=ShapeEnv()):
+        off, cols = prism.lists_to_csr(_t((10,), i64), _t((10,), i32), _t((100,), i32))
+        assert off.shape == (11,) and off.dtype == i32 and cols.dtype == i32
+        assert isinstance(cols.shape[0], torch.SymInt)
 
 
 def test_operators_reject_cpu_tensors(prism):
