@@ -11,7 +11,7 @@ Public surface (reference names):
   a2v_token_norms             wan_video_dit.py:742-752 (A2V residual norms)
   a2v_bridge_projection       interactionv2.py:348 o-projection with the norms fused
 All compute runs in libprism_bsa.so, reached through the torch.ops.prism
-operators of libprism_torch.so (build: python -m prism_amd.build).
+operators of libprism_torch.so (build: python prism_amd/build.py).
 """
 from .dynamic_block_shape import (  # noqa: F401
     ALL_CANDIDATE_SHAPES, CANDIDATE_SHAPES_64, CANDIDATE_SHAPES_128, NUM_CANDIDATES, NUM_CANDIDATES_64, ZONE_SIZE,

@@ -70,7 +70,7 @@ def load() -> ctypes.CDLL:
             return _lib
         if not os.path.exists(LIB_PATH):
             raise ImportError(
-                f"{LIB_PATH} not found: build the HIP library first (python -m prism_amd.build); "
+                f"{LIB_PATH} not found: build the HIP library first (python prism_amd/build.py); "
                 "prism_amd has no fallback path")
         lib = ctypes.CDLL(LIB_PATH)
         lib.prism_last_error.restype = ctypes.c_char_p

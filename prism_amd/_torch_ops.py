@@ -28,7 +28,7 @@ def load():
     with _lock:
         if not _loaded:
             if not os.path.exists(LIB_PATH):
-                raise ImportError(f"{LIB_PATH} not found: build it first (python -m prism_amd.build); "
+                raise ImportError(f"{LIB_PATH} not found: build it first (python prism_amd/build.py); "
                                   "prism_amd has no fallback path")
             torch.ops.load_library(LIB_PATH)
             _register_fakes()

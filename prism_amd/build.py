@@ -1,6 +1,7 @@
 """Build libprism_bsa.so (HIP, gfx950) in-tree.
 
-    python -m prism_amd.build          # or prism_amd.build.build()
+    python prism_amd/build.py          # run as a file: importing the package
+                                       # would load the library it builds
 
 Each csrc/*.hip file is compiled by hipcc for gfx950 only and linked into one
 shared library exporting the C-ABI declared in include/prism_bsa.h;

@@ -26,7 +26,11 @@ def exported():
 @pytest.fixture(scope="module", autouse=True)
 def built():
     if not os.path.exists(LIB):
-        from prism_amd import build
+        # by file path: importing the package would load the library first
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("_prism_amd_build", os.path.join(ROOT, "prism_amd", "build.py"))
+        build = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(build)
         build.build()
 
 
