@@ -154,7 +154,6 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   }
   const bool kvalid = a.kv_valid ? a.kv_valid[key] != 0 : true;
   const float kbias = kvalid ? 0.0f : -__builtin_inff();
-  const bool all_valid = __builtin_amdgcn_ballot_w64(!kvalid) == 0;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     consume_regs(kf[s]);
@@ -173,11 +172,29 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
     const float* sM = reinterpret_cast<const float*>(sQ + 2 * RT::BYTES);
     const float* sDl = sM + 64;
     f32x16 sacc = f32x16_zero(), pacc = f32x16_zero();
+    // The 2 NS row operands (Q and dO of k-steps 0, 0, 1, 1, ...) go through
+    // a ring of three registers: operand i + 2 is read while MFMA i runs.
+    constexpr int NO = 2 * NS;
+    bf16x8 op[3];
+    auto rd = [&](int i) { return rop.load((i & 1) ? sDO : sQ, i >> 1); };
+    op[0] = rd(0);
+    op[1] = rd(1);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sQ, s), kf[s], sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sDO, s), vf[s], pacc, 0, 0, 0);
+    for (int i = 0; i < NO; ++i) {
+      if (i + 2 < NO) op[(i + 2) % 3] = rd(i + 2);
+      if (i & 1) pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[i % 3], vf[i >> 1], pacc, 0, 0, 0);
+      else sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[i % 3], kf[i >> 1], sacc, 0, 0, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+    for (int i = 0; i + 3 < NO; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    // P = 2^(S log2e scale - m2 + kbias) and dS = P (dP - delta); kbias is
+    // -inf at this lane's key when it is invalid, else 0 (one add per
+    // element instead of a select on a wave-uniform flag)
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const float4 m4 = *reinterpret_cast<const float4*>(sM + 32 * qh + 8 * jj + 4 * g);
@@ -186,9 +203,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * jj + i;
-        float x = __builtin_fmaf(sacc[r], a.scale_log2, -mv[i]);
-        if (!all_valid) x += kbias;
-        const float p = fast_exp2(x);
+        const float p = fast_exp2(__builtin_fmaf(sacc[r], a.scale_log2, -mv[i]) + kbias);
         sacc[r] = p;
         pacc[r] = p * (pacc[r] - dl4[i]);
       }
@@ -359,6 +374,11 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   }
   consume_regs(mq);
   consume_regs(dlt);
+  // -delta of this lane's query in every accumulator slot: the dP^T chains
+  // start from it, so they produce dP - delta without a per-element subtract
+  f32x16 ndl;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) ndl[r] = -dlt;
   f32x16 dq[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) dq[dt] = f32x16_zero();
@@ -375,14 +395,31 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
     if (!(e & mybit)) continue;
 
     const uint8_t* sV = sK + RT::BYTES;
-    f32x16 sacc[2] = {f32x16_zero(), f32x16_zero()}, pacc[2] = {f32x16_zero(), f32x16_zero()};
+    f32x16 sacc[2] = {f32x16_zero(), f32x16_zero()}, pacc[2] = {ndl, ndl};
+    // the 4 NS row operands (K then V of key half 0, then 1, of k-step 0,
+    // then of step 1, ...) go through a ring of four registers: operand
+    // i + 3 is read while MFMA i runs
+    {
+      constexpr int NO = 4 * NS, RING = 4;
+      bf16x8 op[RING];
+      auto rd = [&](int i) { return rop.load(((i & 1) ? sV : sK) + RT::rows(32 * ((i >> 1) & 1)), i >> 2); };
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
+      for (int i = 0; i + 1 < RING; ++i) op[i] = rd(i);
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sK + RT::rows(32 * kh), s), qf[s], sacc[kh], 0, 0, 0);
-        pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rop.load(sV + RT::rows(32 * kh), s), df[s], pacc[kh], 0, 0, 0);
+      for (int i = 0; i < NO; ++i) {
+        if (i + RING - 1 < NO) op[(i + RING - 1) % RING] = rd(i + RING - 1);
+        const int kh = (i >> 1) & 1;
+        if (i & 1) pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[i % RING], df[i >> 2], pacc[kh], 0, 0, 0);
+        else sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[i % RING], qf[i >> 2], sacc[kh], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, RING - 1, 0);
+#pragma unroll
+      for (int i = 0; i + RING - 1 < NO; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, RING - 1, 0);
+    }
     // exponentials, dS and dQ at raised wave priority (as in the forward
     // kernel; measured 1% faster; the same in dK/dV was 4% slower)
     __builtin_amdgcn_s_setprio(1);
@@ -402,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(__builtin_fmaf(sacc[kh][r], a.scale_log2, -mq));
-        pacc[kh][r] = p * (pacc[kh][r] - dlt);
+        pacc[kh][r] = p * pacc[kh][r];
       }
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {

@@ -146,18 +146,29 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     if (!(e & mybit)) continue;
 
     const uint8_t* sV = sK + RT::BYTES;
-    // S^T[key][q] = K Q^T, two 32-key halves as interleaved MFMA chains; all
-    // K operands are read first so the LDS latency is paid once
-    bf16x8 kfr[2][NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) kfr[kh][s] = kop.load(sK + RT::rows(32 * kh), s);
+    // S^T[key][q] = K Q^T, two 32-key halves as interleaved MFMA chains; the
+    // 2 NS K operands (half 0, 1 of k-step 0, then of step 1, ...) go through
+    // a ring of four registers: operand i + 3 is read while MFMA i runs
     f32x16 sacc[2] = {f32x16_zero(), f32x16_zero()};
+    {
+      constexpr int NO = 2 * NS, RING = 4;
+      bf16x8 kfr[RING];
+      auto rd = [&](int i) { return kop.load(sK + RT::rows(32 * (i & 1)), i >> 1); };
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
+      for (int i = 0; i + 1 < RING; ++i) kfr[i] = rd(i);
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[kh][s], qf[s], sacc[kh], 0, 0, 0);
+      for (int i = 0; i < NO; ++i) {
+        if (i + RING - 1 < NO) kfr[(i + RING - 1) % RING] = rd(i + RING - 1);
+        sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[i % RING], qf[i >> 1], sacc[i & 1], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, RING - 1, 0);
+#pragma unroll
+      for (int i = 0; i + RING - 1 < NO; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, RING - 1, 0);
+    }
     // V^T operands of the P V product, in flight while the softmax runs
     bf16x8 vfr[4][NDT];
 #pragma unroll
