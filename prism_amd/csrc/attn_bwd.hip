@@ -42,6 +42,8 @@
 // [32 qh, 32 qh + 32) of tile 2p + tq over all 64 keys of every listed key
 // tile (qh = w & 1, tq = w >> 1).  S^T = K Q^T and dP^T = V dO^T keep one
 // query per lane column; dQ^T = K^T dS^T.
+#include <type_traits>
+
 #include "common.h"
 #include "mfma.h"
 #include "tile_dma.h"
@@ -160,14 +162,17 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
     consume_regs(vf[s]);
   }
   consume_regs(kbias);
+  const bool all_valid = __builtin_amdgcn_ballot_w64(!kvalid) == 0;
   f32x16 dk[NDT], dv[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) { dk[dt] = f32x16_zero(); dv[dt] = f32x16_zero(); }
 
   // S = Q K^T and dP = dO V^T of one entry, then P and dS (bf16 B operands of
   // the dV / dK products, query rows 32qh + 8j + 4g + i in register r = 4j + i,
-  // column = this lane's key)
-  auto sdp = [&](const uint8_t* sQ, bf16x8* pb, bf16x8* sb) {
+  // column = this lane's key); allv: std::true_type when every key of this
+  // wave is valid
+  auto sdp = [&](auto allv, const uint8_t* sQ, bf16x8* pb, bf16x8* sb) {
+    constexpr bool AV = decltype(allv)::value;
     const uint8_t* sDO = sQ + RT::BYTES;
     const float* sM = reinterpret_cast<const float*>(sQ + 2 * RT::BYTES);
     const float* sDl = sM + 64;
@@ -192,9 +197,9 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-    // P = 2^(S log2e scale - m2 + kbias) and dS = P (dP - delta); kbias is
-    // -inf at this lane's key when it is invalid, else 0 (one add per
-    // element instead of a select on a wave-uniform flag)
+    // P = 2^(S log2e scale - m2 [+ kbias]) and dS = P (dP - delta); kbias
+    // is -inf at this lane's key when it is invalid, else 0; waves whose
+    // keys are all valid (AV) skip the add
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const float4 m4 = *reinterpret_cast<const float4*>(sM + 32 * qh + 8 * jj + 4 * g);
@@ -203,7 +208,9 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * jj + i;
-        const float p = fast_exp2(__builtin_fmaf(sacc[r], a.scale_log2, -mv[i]) + kbias);
+        float x = __builtin_fmaf(sacc[r], a.scale_log2, -mv[i]);
+        if constexpr (!AV) x += kbias;
+        const float p = fast_exp2(x);
         sacc[r] = p;
         pacc[r] = p * (pacc[r] - dl4[i]);
       }
@@ -233,7 +240,9 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   // hold the matrix core, instead of both SIMD waves leaving it idle at once.
   // Each group has a loop of its own (the same barriers per entry), so the
   // P / dS operands the tk = 1 waves carry to the next entry are not live in
-  // the tk = 0 loop.
+  // the tk = 0 loop.  Both loops are instantiated for waves with and without
+  // invalid keys (a wave-uniform choice made once).
+  auto run = [&](auto allv) {
   if (tk == 0) {
     int st = 0;  // stage of entry j
     for (int j = 0; j < n; ++j) {
@@ -247,7 +256,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
       st = st + 1 == kStagesDkdv ? 0 : st + 1;
       if (!(e & mybit)) continue;
       bf16x8 pb[2], sb[2];
-      sdp(sQ, pb, sb);
+      sdp(allv, sQ, pb, sb);
       dvdk(sQ, pb, sb);
     }
   } else {
@@ -264,12 +273,16 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
       if (pend) dvdk(sPrev, pb, sb);
       pend = (e & mybit) != 0;
       if (pend) {
-        sdp(sQ, pb, sb);
+        sdp(allv, sQ, pb, sb);
         sPrev = sQ;
       }
     }
     if (pend) dvdk(sPrev, pb, sb);
   }
+
+  };
+  if (all_valid) run(std::true_type{});
+  else run(std::false_type{});
 
   // add the two query-half partials in a fixed order (qh = 0 + qh = 1)
   __syncthreads();
