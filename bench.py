@@ -110,11 +110,23 @@ def make_inputs(cfg_name, seed=0, device="cuda"):
         qkv.append(x.to(torch.bfloat16).contiguous())
         del low, x
     del fields
-    # A2V bridge residual [B, S, C]: audio coupling concentrated in ~10% of zones
+    # A2V bridge residual [B, S, C]: audio coupling concentrated in ~10% of
+    # the zones.  There each channel is correlated with the token's keys at
+    # rho = 0.8 (rho * a fixed random projection of the heads' keys, unit
+    # variance, + sqrt(1 - rho^2) * noise) and the amplitude is 3; elsewhere
+    # the residual is unit noise.
     zone_amp = torch.zeros(gp[0] // 8, gp[1] // 8, gp[2] // 8, device=device)
     zone_amp.view(-1)[torch.randperm(zone_amp.numel(), generator=gen, device=device)[: max(1, zone_amp.numel() // 10)]] = 2.0
     amp = zone_amp.repeat_interleave(8, 0).repeat_interleave(8, 1).repeat_interleave(8, 2)[:T, :Hg, :Wg].reshape(S, 1)
-    res = (torch.randn((B, S, C), generator=gen, device=device, dtype=torch.bfloat16) * (1.0 + amp).to(torch.bfloat16))
+    rho = 0.8
+    proj = torch.randn((H * D, C), generator=gen, device=device) / math.sqrt(H * D)
+    res = torch.empty((B, S, C), device=device, dtype=torch.bfloat16)
+    for b in range(B):
+        z = qkv[1][b].float().permute(1, 0, 2).reshape(S, H * D) @ proj
+        z /= z.std()
+        eps = torch.randn((S, C), generator=gen, device=device)
+        res[b] = (torch.where(amp > 0, rho * z + math.sqrt(1 - rho * rho) * eps, eps) * (1.0 + amp)).to(torch.bfloat16)
+        del z, eps
     do = torch.randn((B, H, S, D), generator=gen, device=device).to(torch.bfloat16)
     if str(device).startswith("cuda"):
         torch.cuda.synchronize()
