@@ -433,6 +433,14 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
       }
       __builtin_amdgcn_sched_group_barrier(0x008, RING - 1, 0);
     }
+    // the first K^T operands of the dQ product are read before the
+    // exponentials, so their LDS latency hides behind them; the rest go
+    // through a ring of RQ registers, operand i + RQ - 1 read while MFMA i runs
+    constexpr int NQ = 4 * NDT, RQ = 4;
+    bf16x8 kt[RQ];
+    auto rdk = [&](int i) { return top.load<RT>(sK, i / NDT, i % NDT); };
+#pragma unroll
+    for (int i = 0; i + 1 < RQ; ++i) kt[i] = rdk(i);
     // exponentials, dS and dQ at raised wave priority (as in the forward
     // kernel; measured 1% faster; the same in dK/dV was 4% slower)
     __builtin_amdgcn_s_setprio(1);
@@ -458,8 +466,11 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
     for (int tt = 0; tt < 4; ++tt) {
       const bf16x8 sb = b_from_acc(pacc, tt);
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(top.load<RT>(sK, tt, dt), sb, dq[dt], 0, 0, 0);
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int i = tt * NDT + dt;
+        if (i + RQ - 1 < NQ) kt[(i + RQ - 1) % RQ] = rdk(i + RQ - 1);
+        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kt[i % RQ], sb, dq[dt], 0, 0, 0);
+      }
     }
     __builtin_amdgcn_s_setprio(0);
   }
