@@ -103,15 +103,29 @@ class _Plan:
         self.kpair = None
         self.kunion = None
         self.korder = None
+        self.keys_ready = None  # event of a key-list build on the side stream
 
     @staticmethod
     def _compact(start, length, cols):
         offsets, entries = ops.lists_to_csr(start, length, cols)
         return (*ops.csr_lists(offsets), entries)
 
+    def build_key_lists_side(self):
+        """build_key_lists on the side stream, after the work queued so far on
+        the current stream (compact lists read nnz on the host, so they are
+        built in place on first use instead)."""
+        if self.kunion is not None or self.compact:
+            return
+        _, self.keys_ready = ops.side_launch(
+            self.qcols.device, self.build_key_lists, reads=(self.qstart, self.qlen, self.qcols),
+            produces=lambda _: (*self.klists, self.kpair, *self.kunion, self.korder))
+
     def build_key_lists(self):
         """Per-key-tile query lists, their pairing, unions and launch order
         (the dK/dV side), built on first use."""
+        if self.keys_ready is not None:
+            torch.cuda.current_stream().wait_event(self.keys_ready)
+            self.keys_ready = None
         if self.kunion is not None:
             return
         Nt = self.lay.Nt
@@ -136,6 +150,8 @@ class _DynBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _Plan, sm_scale: float):
+        if ops.OVERLAP_SIDE_WORK and any(ctx.needs_input_grad[:3]):
+            plan.build_key_lists_side()  # the backward's lists, beside the forward kernel
         o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
                                 plan.qorder)
         ctx.plan = plan
@@ -153,13 +169,26 @@ class _DynBSA(torch.autograd.Function):
         do_re, delta = gd["rows"], gd["rowdot"]
         plan.build_key_lists()
         m2 = ops.lse_to_m2(lse)
+        tq, tk, tv = ctx.in_dtypes
+        side = {}
+
+        def scatter_dkdv(dk_re, dv_re):
+            # dK and dV back to THW order on the side stream, during the dQ kernel
+            if ops.OVERLAP_SIDE_WORK:
+                side["dkdv"] = ops.side_launch(
+                    dk_re.device, lambda: (ops.scatter_rows(dk_re, lay, tk), ops.scatter_rows(dv_re, lay, tv)),
+                    reads=(dk_re, dv_re), produces=lambda out: out)
+
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid,
                                           plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale, plan.qpair, plan.kpair,
-                                          plan.qorder, plan.korder)
-        tq, tk, tv = ctx.in_dtypes
+                                          plan.qorder, plan.korder, after_dkdv=scatter_dkdv)
         dq = ops.scatter_rows(dq_re, lay, tq)
-        dk = ops.scatter_rows(dk_re, lay, tk)
-        dv = ops.scatter_rows(dv_re, lay, tv)
+        if "dkdv" in side:
+            (dk, dv), done = side["dkdv"]
+            torch.cuda.current_stream().wait_event(done)
+        else:
+            dk = ops.scatter_rows(dk_re, lay, tk)
+            dv = ops.scatter_rows(dv_re, lay, tv)
         return dq, dk, dv, None, None
 
 

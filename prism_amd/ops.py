@@ -539,13 +539,43 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return st
 
 
+# Side work that the attention launches do not depend on runs on the side
+# stream while they run: the per-key-tile lists of the backward during the
+# forward kernel, the dK / dV scatters during the dQ kernel.  Inputs and
+# outputs of the side work are recorded on the stream that did not allocate
+# them (the caching allocator keeps their memory until that work is done).
+OVERLAP_SIDE_WORK = True
+
+
+def side_launch(device: torch.device, fn, reads=(), produces=None):
+    """Run fn() on the side stream after the work queued so far on the
+    current stream; returns (fn's result, event marking its end).  `reads`:
+    current-stream tensors fn reads; `produces(result)`: the side-stream
+    tensors the current stream will use."""
+    main = torch.cuda.current_stream()
+    side = _side_stream(device)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        out = fn()
+        done = torch.cuda.Event()
+        done.record(side)
+    for t in reads:
+        if t is not None:
+            t.record_stream(side)
+    for t in (produces(out) if produces is not None else ()):
+        if t is not None:
+            t.record_stream(main)
+    return out, done
+
+
 def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float,
             qpair: Optional[torch.Tensor] = None, kpair: Optional[torch.Tensor] = None,
-            qorder: Optional[torch.Tensor] = None, korder: Optional[torch.Tensor] = None):
+            qorder: Optional[torch.Tensor] = None, korder: Optional[torch.Tensor] = None, after_dkdv=None):
     """Backward over tile-order bf16 tensors; qunion / kunion = pair unions of
     the per-query-tile key lists and of the per-key-tile query lists, built
     with the pairings qpair / kpair (None: neighbouring tiles).  Returns
-    dq, dk, dv (bf16, tile order)."""
+    dq, dk, dv (bf16, tile order).  after_dkdv(dk, dv), if given, is called
+    between the dK/dV and the dQ launches."""
     _cuda(q, k, v, do, m2, delta, kv_valid, tmasks, qpair, kpair, qorder, korder)
     q, k, v, do = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"), _bf16(do, "do")
     B, H, Sq, Sk, D = _attn_shapes(q, k, v)
@@ -568,6 +598,8 @@ def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: 
                 t.record_stream(side)
     else:
         dk, dv = dkdv()
+    if after_dkdv is not None:
+        after_dkdv(dk, dv)
     dq = _op("bsa_bwd_dq", q, k, v, do, m2, delta, tmasks, qunion[0], qunion[1], qunion[2], qpair, qorder,
              float(sm_scale))
     if BWD_CONCURRENT:

@@ -93,8 +93,21 @@ class _ChunkPlan:
         self.kpair = None
         self.kunion = None
         self.korder = None
+        self.keys_ready = None  # event of a key-list build on the side stream
+
+    def key_lists_side(self):
+        """key_lists on the side stream, after the work queued so far on the
+        current stream (not for compact lists, which read nnz on the host)."""
+        if self.kunion is not None or self.compact:
+            return
+        _, self.keys_ready = ops.side_launch(
+            self.qcols.device, self.key_lists, reads=(self.qstart, self.qlen, self.qcols),
+            produces=lambda _: (*self.klists, self.kpair, *self.kunion, self.korder))
 
     def key_lists(self):
+        if getattr(self, "keys_ready", None) is not None:
+            torch.cuda.current_stream().wait_event(self.keys_ready)
+            self.keys_ready = None
         if self.kunion is None:
             self.klists = ops.transpose_lists(self.qstart, self.qlen, self.qcols, self.B * self.H, self.lq.Nt,
                                               self.lk.Nt)
@@ -119,6 +132,8 @@ class _ChunkBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _ChunkPlan, sm_scale: float):
+        if ops.OVERLAP_SIDE_WORK and any(ctx.needs_input_grad[:3]):
+            plan.key_lists_side()  # the backward's lists, beside the forward kernel
         o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
                                 plan.qorder)
         ctx.plan = plan
@@ -134,12 +149,28 @@ class _ChunkBSA(torch.autograd.Function):
         gd = ops.chunk_gather_pool(do.contiguous(), plan.lq, None, rows=True, dot_with=o_re)
         kunion = plan.key_lists()
         m2 = ops.lse_to_m2(lse)
+        tq, tk, tv = ctx.in_dtypes
+        side = {}
+
+        def scatter_dkdv(dk_re, dv_re):
+            # dK and dV back to the input order on the side stream, during the dQ kernel
+            if ops.OVERLAP_SIDE_WORK:
+                side["dkdv"] = ops.side_launch(
+                    dk_re.device,
+                    lambda: (ops.chunk_scatter_rows(dk_re, plan.lk, tk), ops.chunk_scatter_rows(dv_re, plan.lk, tv)),
+                    reads=(dk_re, dv_re), produces=lambda out: out)
+
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, gd["rows"], m2, gd["rowdot"],
                                           plan.kv_valid, plan.tmasks, plan.qunion, kunion, ctx.sm_scale, plan.qpair,
-                                          plan.kpair, plan.qorder, plan.korder)
-        tq, tk, tv = ctx.in_dtypes
-        return (ops.chunk_scatter_rows(dq_re, plan.lq, tq), ops.chunk_scatter_rows(dk_re, plan.lk, tk),
-                ops.chunk_scatter_rows(dv_re, plan.lk, tv), None, None)
+                                          plan.kpair, plan.qorder, plan.korder, after_dkdv=scatter_dkdv)
+        dq = ops.chunk_scatter_rows(dq_re, plan.lq, tq)
+        if "dkdv" in side:
+            (dk, dv), done = side["dkdv"]
+            torch.cuda.current_stream().wait_event(done)
+        else:
+            dk = ops.chunk_scatter_rows(dk_re, plan.lk, tk)
+            dv = ops.chunk_scatter_rows(dv_re, plan.lk, tv)
+        return dq, dk, dv, None, None
 
 
 def _check_qkv(q, k, v):
