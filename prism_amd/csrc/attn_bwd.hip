@@ -257,7 +257,13 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
       if (!(e & mybit)) continue;
       bf16x8 pb[2], sb[2];
       sdp(allv, sQ, pb, sb);
+      // dV / dK of a tk = 0 wave at raised priority: its SIMD partner (a
+      // tk = 1 wave, half an entry behind) is then in its S / dP phase
+      // (-1% against equal priority; raising the tk = 1 waves instead, or
+      // also the exponentials, was slower)
+      __builtin_amdgcn_s_setprio(1);
       dvdk(sQ, pb, sb);
+      __builtin_amdgcn_s_setprio(0);
     }
   } else {
     int st = 0;
