@@ -412,6 +412,9 @@ def main():
     ap.add_argument("--compact-lists", action="store_true",
                     help="keep the work lists in compact CSR form (bsa_params compact_lists); reported in config, "
                          "not the default headline")
+    ap.add_argument("--forward-only", action="store_true",
+                    help="time the forward alone (inference, no autograd), as BASELINE config 2 is quoted; one JSON "
+                         "line of its own, not the headline")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=8.0,
@@ -468,12 +471,17 @@ def main():
     dyn.bsa_params.update({"sparsity": sparsity, "cdf_threshold": cdf, "compact_lists": bool(args.compact_lists)})
     log(f"[bench] N_b={N_b} sparsity={sparsity:.6f} cdf={cdf}")
 
-    q = inp["q"].clone().requires_grad_(True)
-    k = inp["k"].clone().requires_grad_(True)
-    v = inp["v"].clone().requires_grad_(True)
+    fwd_only = bool(args.forward_only)
+    q = inp["q"].clone().requires_grad_(not fwd_only)
+    k = inp["k"].clone().requires_grad_(not fwd_only)
+    v = inp["v"].clone().requires_grad_(not fwd_only)
     do = inp["do"]
 
     def step():
+        if fwd_only:
+            with torch.no_grad():
+                dyn(q, k, v, grid, a2v_token_norms(inp["res"]))
+            return
         q.grad = k.grad = v.grad = None
         norms = a2v_token_norms(inp["res"])
         out = dyn(q, k, v, grid, norms)
@@ -521,7 +529,7 @@ def main():
     # fraction of (wave, key tile) slots of the paired-tile kernels that do math
     union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
     fl = 64 * 64 * D * sum_lens  # one 64x64xD product over all kept tile pairs
-    kept_flops = 14 * fl          # FA convention: fwd 4, bwd 10
+    kept_flops = (4 if fwd_only else 14) * fl  # FA convention: fwd 4, bwd 10
 
     # attention kernels: algorithmic FLOPs per launch (executed in parentheses)
     attn = {"prism_bsa_fwd": (4 * fl, 4 * fl), "prism_bsa_bwd_dkdv": (8 * fl, 8 * fl),
@@ -553,7 +561,8 @@ def main():
     roof = {"kernel": dom, "bound": "mfma", "achieved": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12, 2),
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic(dom)}
+            # the committed counter summary is of config 4's launches
+            "traffic": measured_traffic(dom) if args.config == "c4" else None}
     att_ms = sum(kt[n][1] for n in attn if n in kt)
 
     dense = None
@@ -564,22 +573,27 @@ def main():
         vd = inp["v"].clone().requires_grad_(True)
 
         def dstep():
+            if fwd_only:
+                with torch.no_grad():
+                    torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)
+                return
             qd.grad = kd.grad = vd.grad = None
             o = torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)
             o.backward(do)
 
         try:
             dmean, dms, _ = time_region(dstep, DENSE_STEPS, DENSE_WARMUP)
-            dense = {"impl": "torch SDPA (ROCm) fwd+bwd, same shape, unpadded", "ms": round(dms, 2),
+            dense = {"impl": f"torch SDPA (ROCm) {'forward' if fwd_only else 'fwd+bwd'}, same shape, unpadded",
+                     "ms": round(dms, 2),
                      "ms_mean": round(dmean, 2), "timing": f"median of {DENSE_STEPS} after {DENSE_WARMUP} warm-ups",
-                     "tflops": round(14 * S * S * D * B * H / (dms * 1e-3) / 1e12, 1),
+                     "tflops": round((4 if fwd_only else 14) * S * S * D * B * H / (dms * 1e-3) / 1e12, 1),
                      "speedup_sparse_vs_dense": round(dms / ms_median, 2)}
         except Exception as e:  # report, do not fail the bench
             dense = {"error": repr(e)[:200]}
         del qd, kd, vd
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not fwd_only:
         log("[bench] CPU baseline (the reference's torch path, float32, host cores)")
         cpu = cpu_baseline(inp, sparsity, cdf, args.cpu_budget, step_pairs=sum_lens)
 
@@ -588,7 +602,8 @@ def main():
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"{args.config}: BASELINE config {'4 (2K fwd+bwd)' if args.config == 'c4' else args.config}",
+        "config": {"workload": f"{args.config}: BASELINE config {'4 (2K fwd+bwd)' if args.config == 'c4' else args.config}"
+                               + (" forward only" if fwd_only else ""),
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(gp),
                    "audio_tokens": CONFIGS[args.config][4], "topk": inp["topk"], "cdf_threshold": cdf,
                    "sparsity": sparsity, "N_b": Nb, "sum_lens": sum_lens, "density": round(density, 4),
