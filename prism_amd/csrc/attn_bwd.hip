@@ -495,6 +495,14 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
         dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kt[i % RQ], sb, dq[dt], 0, 0, 0);
       }
     }
+    // one MFMA, then the two transposing reads of the ring's next operand;
+    // the exponentials are left to the scheduler (pinning them into groups
+    // between the MFMAs measured slower)
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + RQ - 1 < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
     __builtin_amdgcn_s_setprio(0);
   }
 
