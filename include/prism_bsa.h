@@ -180,7 +180,9 @@ int prism_block_scores(const float* qc, const float* kc, const int32_t* block_co
  * filtering: dynamic_block_attention.py:297-319 (tile_count NULL = keep all).
  * tiles: [rows, tcap] ascending tile ids (tcap >= the tiles of the widest
  * selection: tiles per block x selected blocks), ntiles: [rows];
- * sel_blocks: [rows, bcap] ascending block ids (NULL to skip), nsel: [rows]. */
+ * sel_blocks: [rows, bcap] ascending block ids (NULL to skip), nsel: [rows].
+ * 1 <= N <= 2^30 (rows of more than 16384 blocks take a slower pass-by-pass
+ * kernel with the same results). */
 int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, int64_t k_lo, int64_t ub,
                        float scale, uint64_t thr, const int32_t* block_first_tile, const int32_t* tile_count,
                        int64_t tcap, int32_t* tiles, int32_t* ntiles, int32_t* sel_blocks, int64_t bcap,

@@ -97,54 +97,61 @@ __global__ __launch_bounds__(256) void block_scores_kernel(const float* __restri
 constexpr int kSelThreads = 256;
 constexpr int kSelWaves = kSelThreads / 64;
 
-struct SelShared {
-  uint64_t u64[kSelWaves];
-  uint32_t u32[kSelWaves];
-  float f32[kSelWaves];
+template <int NW>
+struct SelSharedT {
+  uint64_t u64[NW];
+  uint32_t u32[NW];
+  float f32[NW];
 };
+using SelShared = SelSharedT<kSelWaves>;
 
-__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, SelShared& sh) {
+// Workgroup reductions and scans over NW waves; every thread gets the result.
+template <int NW>
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, SelSharedT<NW>& sh) {
   v = wave_sum_u64(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   if (lane == 0) sh.u64[wid] = v;
   __syncthreads();
   uint64_t t = 0;
 #pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) t += sh.u64[w];
+  for (int w = 0; w < NW; ++w) t += sh.u64[w];
   __syncthreads();
   return t;
 }
-__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, SelShared& sh) {
+template <int NW>
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, SelSharedT<NW>& sh) {
   v = wave_sum_u32(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   if (lane == 0) sh.u32[wid] = v;
   __syncthreads();
   uint32_t t = 0;
 #pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) t += sh.u32[w];
+  for (int w = 0; w < NW; ++w) t += sh.u32[w];
   __syncthreads();
   return t;
 }
-__device__ __forceinline__ float block_max_f32(float v, SelShared& sh) {
+template <int NW>
+__device__ __forceinline__ float block_max_f32(float v, SelSharedT<NW>& sh) {
   v = wave_max_xor(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   if (lane == 0) sh.f32[wid] = v;
   __syncthreads();
   float t = sh.f32[0];
 #pragma unroll
-  for (int w = 1; w < kSelWaves; ++w) t = fmaxf(t, sh.f32[w]);
+  for (int w = 1; w < NW; ++w) t = fmaxf(t, sh.f32[w]);
   __syncthreads();
   return t;
 }
 // exclusive scan in thread order; returns the block total in *total
-__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, SelShared& sh, uint32_t* total) {
+template <int NW>
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, SelSharedT<NW>& sh, uint32_t* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const uint32_t incl = wave_incl_scan_u32(v, lane);
   if (lane == 63) sh.u32[wid] = incl;
   __syncthreads();
   uint32_t before = 0, t = 0;
 #pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const uint32_t x = sh.u32[w];
     before += (w < wid) ? x : 0u;
     t += x;
@@ -153,21 +160,63 @@ __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, SelShared& s
   *total = t;
   return before + incl - v;
 }
-
-__device__ __forceinline__ uint64_t block_incl_scan_u64(uint64_t v, SelShared& sh) {
+template <int NW>
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, SelSharedT<NW>& sh, uint64_t* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  uint64_t incl = v;
   for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t lo = __shfl_up((uint32_t)v, off, 64);
-    const uint32_t hi = __shfl_up((uint32_t)(v >> 32), off, 64);
-    if (lane >= off) v += ((uint64_t)hi << 32) | lo;
+    const uint32_t lo = __shfl_up((uint32_t)incl, off, 64);
+    const uint32_t hi = __shfl_up((uint32_t)(incl >> 32), off, 64);
+    if (lane >= off) incl += ((uint64_t)hi << 32) | lo;
   }
-  if (lane == 63) sh.u64[wid] = v;
+  if (lane == 63) sh.u64[wid] = incl;
   __syncthreads();
-  uint64_t before = 0;
+  uint64_t before = 0, t = 0;
 #pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) before += (w < wid) ? sh.u64[w] : 0ull;
+  for (int w = 0; w < NW; ++w) {
+    const uint64_t x = sh.u64[w];
+    before += (w < wid) ? x : 0ull;
+    t += x;
+  }
   __syncthreads();
-  return before + v;
+  *total = t;
+  return before + incl - v;
+}
+
+// Wave 0's step of a radix digit: given the histogram hb of the elements that
+// match the digits found so far and acc, the weight of the keys whose decided
+// digits exceed them, find the largest digit d* whose suffix sum reaches
+// thr - acc; sh.u64[0] = weight of the digits above d*, sh.u32[0] = 255 - d*.
+// Also clears hn, the histogram buffer of the next digit.
+template <int NW>
+__device__ __forceinline__ void radix_pick(const unsigned long long* hb, unsigned long long* hn, uint64_t acc,
+                                           uint64_t thr, SelSharedT<NW>& sh, int lane) {
+  // lane l takes digits 255 - 4 l - i (i = 0..3): inclusive sums over the
+  // descending digits; the first t = 4 l + i with acc + incl >= thr is d*
+  uint64_t h[4], p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h[i] = hb[255 - 4 * lane - i];
+  p[0] = h[0];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) p[i] = p[i - 1] + h[i];
+  uint64_t incl = p[3];
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t lo = __shfl_up((uint32_t)incl, off, 64);
+    const uint32_t hi = __shfl_up((uint32_t)(incl >> 32), off, 64);
+    if (lane >= off) incl += ((uint64_t)hi << 32) | lo;
+  }
+  const uint64_t base = incl - p[3];
+  uint32_t below = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) below += acc + base + p[i] >= thr ? 0u : 1u;
+  const uint32_t tstar = min(wave_sum_u32(below), 255u);  // (<= 255: the bins hold >= thr - acc)
+  if ((uint32_t)lane == (tstar >> 2)) {
+    const int slot = (int)(tstar & 3);
+    sh.u64[0] = base + (slot == 0 ? 0ull : slot == 1 ? p[0] : slot == 2 ? p[1] : p[2]);  // weight of digits > d*
+    sh.u32[0] = tstar;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hn[4 * lane + i] = 0ull;
 }
 
 // Radix search over the 32-bit keys of one row (4 digits of 8 bits, most
@@ -213,35 +262,7 @@ __device__ __forceinline__ uint32_t radix_search(const uint32_t* key, const uint
       }
     if (run_bin != 0xffffffffu) atomicAdd(&hb[run_bin], (unsigned long long)run_w);
     __syncthreads();
-    if (tid < 64) {
-      // lane l takes digits 255 - 4 l - i (i = 0..3): inclusive sums over the
-      // descending digits; the first t = 4 l + i with acc + incl >= thr is d*
-      uint64_t h[4], p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) h[i] = hb[255 - 4 * lane - i];
-      p[0] = h[0];
-#pragma unroll
-      for (int i = 1; i < 4; ++i) p[i] = p[i - 1] + h[i];
-      uint64_t incl = p[3];
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t lo = __shfl_up((uint32_t)incl, off, 64);
-        const uint32_t hi = __shfl_up((uint32_t)(incl >> 32), off, 64);
-        if (lane >= off) incl += ((uint64_t)hi << 32) | lo;
-      }
-      const uint64_t base = incl - p[3];
-      uint32_t below = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) below += acc + base + p[i] >= thr ? 0u : 1u;
-      const uint32_t tstar = min(wave_sum_u32(below), 255u);  // (<= 255: the bins hold >= thr - acc)
-      if ((uint32_t)lane == (tstar >> 2)) {
-        const int slot = (int)(tstar & 3);
-        sh.u64[0] = base + (slot == 0 ? 0ull : slot == 1 ? p[0] : slot == 2 ? p[1] : p[2]);  // weight of digits > d*
-        sh.u32[0] = tstar;
-      }
-      unsigned long long* hn = hist + 256 * ((level + 1) & 1);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) hn[4 * lane + i] = 0ull;
-    }
+    if (tid < 64) radix_pick(hb, hist + 256 * ((level + 1) & 1), acc, thr, sh, lane);
     __syncthreads();
     acc += sh.u64[0];
     prefix |= (255u - sh.u32[0]) << shift;
@@ -463,6 +484,216 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   }
 }
 
+// ------------------------------------------------------------ wide rows
+// Rows of more than 64 kSelThreads blocks: one 1024-thread workgroup per row;
+// element j is taken by thread j mod 1024 in pass j / 1024 (coalesced reads),
+// and each pass recomputes the keys and weights from the row's scores (the row
+// stays in the L2 / Infinity Cache) instead of holding them in registers.
+// The arithmetic is select_kernel's (same canonical exp, same exact integer
+// sums), so the selection is identical; the emit phase ranks the ties and
+// places the outputs with one ordered workgroup scan per pass and running
+// carries.
+constexpr int kWideThreads = 1024, kWideWaves = kWideThreads / 64;
+constexpr int64_t kWideMaxN = (int64_t)1 << 30;
+
+// Adds w to bin b of hb for the active lanes of a wave: the lanes that share
+// the first active lane's bin (a row's keys mostly share their leading
+// digits) are summed across the wave and added with one LDS atomic; the other
+// active lanes add their own.
+__device__ __forceinline__ void hist_add_wave(unsigned long long* hb, bool act, uint32_t b, uint64_t w, int lane) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(act);
+  if (m == 0) return;
+  const int leader = (int)__builtin_ctzll(m);
+  const uint32_t lb = (uint32_t)__builtin_amdgcn_readlane((int)b, leader);
+  const bool same = act && b == lb;
+  const uint64_t sum = wave_sum_u64(same ? w : 0ull);
+  if (lane == leader) atomicAdd(&hb[lb], (unsigned long long)sum);
+  if (act && !same) atomicAdd(&hb[b], (unsigned long long)w);
+}
+
+// radix_search over the row's N elements, element j's (key, weight) from
+// elem(j, key, weight); the passes over the row are wave-uniform
+template <bool WEIGHTED, class Elem>
+__device__ __forceinline__ uint32_t radix_search_wide(const Elem& elem, int64_t N, uint64_t thr, uint64_t* above,
+                                                      SelSharedT<kWideWaves>& sh, unsigned long long* hist) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t prefix = 0;
+  uint64_t acc = 0;
+#pragma unroll 1
+  for (int level = 0; level < 4; ++level) {
+    const int shift = 24 - 8 * level;
+    const uint32_t hmask = level == 0 ? 0u : (0xffffffffu << (shift + 8));
+    unsigned long long* hb = hist + 256 * (level & 1);
+    for (int64_t base = 0; base < N; base += kWideThreads) {
+      const int64_t j = base + tid;
+      bool act = false;
+      uint32_t b = 0;
+      uint64_t w = 0;
+      if (j < N) {
+        uint32_t k;
+        uint64_t wt;
+        elem(j, k, wt);
+        if ((k & hmask) == prefix) {
+          act = true;
+          b = (k >> shift) & 255u;
+          w = WEIGHTED ? wt : 1ull;
+        }
+      }
+      hist_add_wave(hb, act, b, w, lane);
+    }
+    __syncthreads();
+    if (tid < 64) radix_pick(hb, hist + 256 * ((level + 1) & 1), acc, thr, sh, lane);
+    __syncthreads();
+    acc += sh.u64[0];
+    prefix |= (255u - sh.u32[0]) << shift;
+  }
+  *above = acc;
+  return prefix;
+}
+
+__global__ __launch_bounds__(kWideThreads) void select_wide_kernel(SelArgs a) {
+  __shared__ SelSharedT<kWideWaves> sh;
+  __shared__ unsigned long long hist[2 * 256];
+  const int tid = threadIdx.x;
+  if (tid < 256) hist[tid] = 0ull;  // buffer 0 of the radix searches
+  __syncthreads();
+  const int64_t row = blockIdx.x;
+  const float* s = a.scores + row * a.N;
+  const int64_t N = a.N;
+  const float NINF = -__uint_as_float(0x7f800000u);
+
+  // top-k keys: the order-preserving u32 of the score
+  auto key_topk = [&](int64_t j, uint32_t& k, uint64_t& w) {
+    const uint32_t u = __float_as_uint(s[j]);
+    k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    w = 1ull;
+  };
+  // cdf keys: the fp32 bits of the softmax weight, and its 2^-60 fixed point
+  float m = NINF, sum = 1.0f;
+  auto key_cdf = [&](int64_t j, uint32_t& k, uint64_t& w) {
+    const float x = s[j] * a.scale;
+    const float p = canon_exp(x - m) / sum;
+    k = __float_as_uint(p);
+    w = fixp(p, 60);
+  };
+
+  int64_t eff = 0;
+  uint32_t v_e = 0;
+  uint64_t need = 0;
+  if (a.mode == 0) {
+    eff = a.k_lo < N ? a.k_lo : N;
+  } else {
+    float mx = NINF;
+    for (int64_t j = tid; j < N; j += kWideThreads) mx = fmaxf(mx, s[j] * a.scale);
+    m = block_max_f32(mx, sh);
+    if (m == NINF) {
+      eff = 0;
+    } else {
+      uint64_t E = 0;
+      for (int64_t j = tid; j < N; j += kWideThreads) {
+        const float x = s[j] * a.scale;
+        E += fixp(canon_exp(x - m), 40);
+      }
+      E = block_sum_u64(E, sh);
+      sum = (float)E * 9.094947017729282e-13f;  // 2^-40
+      uint64_t g0 = 0;
+      for (int64_t j = tid; j < N; j += kWideThreads) {
+        uint32_t k;
+        uint64_t w;
+        key_cdf(j, k, w);
+        g0 += w;
+      }
+      g0 = block_sum_u64(g0, sh);
+      int64_t c = a.ub;
+      bool crossed = false;
+      uint32_t vc = 0;
+      uint64_t jt = 0;
+      if (g0 >= a.thr) {
+        // crossing value vc: G(vc) >= thr > G(vc + 1) = A
+        uint64_t A;
+        vc = radix_search_wide<true>(key_cdf, N, a.thr, &A, sh, hist);
+        uint32_t ngt = 0;
+        for (int64_t j = tid; j < N; j += kWideThreads) {
+          uint32_t k;
+          uint64_t w;
+          key_cdf(j, k, w);
+          ngt += k >= vc + 1 ? 1u : 0u;
+        }
+        ngt = block_sum_u32(ngt, sh);
+        const uint64_t Wv = fixp(__uint_as_float(vc), 60);
+        jt = (a.thr - A - 1) / Wv;  // smallest j with A + (j+1) Wv >= thr
+        const int64_t k = (int64_t)ngt + (int64_t)jt;
+        if (k < a.ub) { c = k; crossed = true; }
+      }
+      int64_t n = c + 1;
+      if (n < a.k_lo) n = a.k_lo;
+      if (n > N) n = N;
+      eff = n < a.ub ? n : a.ub;
+      if (crossed && eff == c + 1) {
+        v_e = vc;
+        need = jt + 1;
+        eff = -eff;  // marks "v_e already known"
+      }
+    }
+  }
+
+  if (eff > 0) {  // count search: largest v with #(key >= v) >= eff
+    uint64_t above;
+    v_e = a.mode == 0 ? radix_search_wide<false>(key_topk, N, (uint64_t)eff, &above, sh, hist)
+                      : radix_search_wide<false>(key_cdf, N, (uint64_t)eff, &above, sh, hist);
+    need = (uint64_t)eff - above;
+  } else {
+    eff = -eff;
+  }
+
+  // emit in ascending block order, pass by pass: ties ranked by an ordered
+  // scan plus the ties of earlier passes; (tiles | blocks << 32) placed the
+  // same way
+  int32_t* trow = a.tiles + row * a.tcap;
+  int32_t* brow = a.sel_blocks ? a.sel_blocks + row * a.bcap : nullptr;
+  uint32_t ties_before = 0;
+  uint64_t out_before = 0;
+  for (int64_t base = 0; base < N; base += kWideThreads) {
+    const int64_t j = base + tid;
+    const bool pres = eff > 0 && j < N;
+    uint32_t k = 0;
+    if (pres) {
+      uint64_t w;
+      if (a.mode == 0) key_topk(j, k, w);
+      else key_cdf(j, k, w);
+    }
+    const bool tie = pres && k == v_e;
+    uint32_t ties_here;
+    const uint32_t rank = ties_before + block_excl_scan_u32(tie ? 1u : 0u, sh, &ties_here);
+    ties_before += ties_here;
+    const bool sel = pres && (k > v_e || (tie && rank < need));
+    int32_t t0 = 0, t1 = 0;
+    uint32_t cnt = 0;
+    if (sel) {
+      t0 = a.block_first_tile[j];
+      t1 = a.block_first_tile[j + 1];
+      for (int32_t t = t0; t < t1; ++t) cnt += (a.tile_count == nullptr || a.tile_count[t] > 0) ? 1u : 0u;
+    }
+    uint64_t out_here;
+    const uint64_t pos =
+        out_before + block_excl_scan_u64(sel ? ((uint64_t)cnt | (1ull << 32)) : 0ull, sh, &out_here);
+    out_before += out_here;
+    if (sel) {
+      int64_t p = (int64_t)(pos & 0xffffffffu);
+      for (int32_t t = t0; t < t1; ++t)
+        if (a.tile_count == nullptr || a.tile_count[t] > 0) {
+          if (p < a.tcap) trow[p] = t;
+          ++p;
+        }
+      if (brow) brow[pos >> 32] = (int32_t)j;
+    }
+  }
+  if (tid == 0) {
+    a.ntiles[row] = (int32_t)(out_before & 0xffffffffu);
+    if (a.nsel) a.nsel[row] = (int32_t)(out_before >> 32);
+  }
+}
+
 // q tile t of head bh uses the list of its block (shared by the block's tiles);
 // with q_tile_count, tiles without a valid query token get an empty list
 __global__ void tile_rows_kernel(const int32_t* __restrict__ ntiles, const int32_t* __restrict__ block_id_of_tile,
@@ -629,21 +860,23 @@ int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, i
                        hipStream_t stream) {
   PRISM_REQUIRE(scores && block_first_tile && tiles && ntiles, "prism_select_tiles: null pointer");
   PRISM_REQUIRE(mode >= 0 && mode <= 2, "prism_select_tiles: mode %d unknown", mode);
-  PRISM_REQUIRE(N >= 1 && N <= 64 * kSelThreads, "prism_select_tiles: N=%lld out of range [1, %d]",
-                (long long)N, 64 * kSelThreads);
+  PRISM_REQUIRE(N >= 1 && N <= kWideMaxN, "prism_select_tiles: N=%lld out of range [1, %lld]", (long long)N,
+                (long long)kWideMaxN);
   PRISM_REQUIRE(k_lo >= 0 && ub >= 0 && ub <= N, "prism_select_tiles: bad k/ub");
   PRISM_REQUIRE(mode == 0 || thr > 0, "prism_select_tiles: threshold must be positive");
   PRISM_REQUIRE(tcap >= (mode == 0 ? (k_lo < N ? k_lo : N) : ub), "prism_select_tiles: tcap too small");
   PRISM_REQUIRE(sel_blocks == nullptr || bcap >= (mode == 0 ? (k_lo < N ? k_lo : N) : ub),
                 "prism_select_tiles: bcap too small");
-  PRISM_REQUIRE(2 * N < 65536, "prism_select_tiles: N too large for the packed scan");
   if (rows == 0) return PRISM_OK;
   SelArgs a;
   a.scores = scores; a.rows = rows; a.N = N; a.mode = mode; a.k_lo = k_lo; a.ub = ub; a.scale = scale; a.thr = thr;
   a.block_first_tile = block_first_tile; a.tile_count = tile_count; a.tcap = tcap; a.tiles = tiles;
   a.ntiles = ntiles; a.sel_blocks = sel_blocks; a.bcap = bcap; a.nsel = nsel;
   const int64_t need = (N + kSelThreads - 1) / kSelThreads;
-  if (need <= 8) select_kernel<8><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
+  // rows of up to 64 kSelThreads blocks in registers (the per-thread packed
+  // scan then holds 2 N < 65536 tiles and blocks); wider rows pass by pass
+  if (need > 64) select_wide_kernel<<<(unsigned)rows, kWideThreads, 0, stream>>>(a);
+  else if (need <= 8) select_kernel<8><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   else if (need <= 16) select_kernel<16><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   else if (need <= 24) select_kernel<24><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   else if (need <= 32) select_kernel<32><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);

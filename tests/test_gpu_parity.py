@@ -229,6 +229,34 @@ def test_select_tile_expansion_any_tile_count(N):
             assert np.array_equal(tiles[r, : nt[r]], want), (N, sp, p, r)
 
 
+@pytest.mark.parametrize("kind", ["plain", "ties", "neginf", "peaked"])
+def test_select_bitexact_wide_rows(kind):
+    """Rows of more than 16384 blocks (the pass-by-pass workgroup kernel):
+    bit-exact against the oracle in all three modes, with blocks of 0-3 tiles
+    and padded tiles dropped."""
+    from prism_amd import ops
+    rng = np.random.default_rng(13)
+    for N in (16385, 23000, 70000):
+        rows = 6
+        s = _random_scores(rng, rows, N, kind)
+        per = rng.integers(0, 4, N)
+        first = np.concatenate([[0], np.cumsum(per)]).astype(np.int32)
+        tc = (rng.random(int(first[-1])) > 0.2).astype(np.int32)
+        for sp, p in ((0.9, None), (None, 0.9), (1 - 5.5 / N, 0.9), (0.5, 0.3), (None, 0.2)):
+            say("select wide", kind, N, sp, p)
+            ref_sel, ref_n = O.select(s, sp, p, 0.125)
+            res = ops.select_tiles(dev(s), sp, p, 0.125, dev(first), dev(tc), want_blocks=True, tiles_per_block=3)
+            n, got = host(res["nsel"]), host(res["sel_blocks"])
+            assert np.array_equal(n, ref_n), (kind, N, sp, p)
+            nt, tiles = host(res["ntiles"]), host(res["tiles"])
+            for r in range(rows):
+                assert np.array_equal(got[r, : n[r]], ref_sel[r, : n[r]]), (kind, N, sp, p, r)
+                want = np.concatenate([np.arange(first[b], first[b + 1]) for b in ref_sel[r, : n[r]]] + [np.zeros(0, int)])
+                want = want[tc[want] > 0] if want.size else want
+                assert nt[r] == want.size, (kind, N, sp, p, r)
+                assert np.array_equal(tiles[r, : nt[r]], want), (kind, N, sp, p, r)
+
+
 def test_select_tile_expansion_bitexact(case):
     from prism_amd import ops
     sid = _shape_ids_for(case)
