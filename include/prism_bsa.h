@@ -270,8 +270,8 @@ int prism_pair_tiles(const int64_t* start, const int32_t* len, const int32_t* co
                      int64_t col_tiles, int32_t* pairmap, hipStream_t stream);
 
 /* Launch order of an attention kernel: order[id] = the pair (index into the
- * prism_pair_union arrays, n = BH * pairs per head) that workgroup id
- * processes.  Ids [0, n - tail) keep the XCD group mapping the kernel uses
+ * prism_pair_union arrays, n = BH * pairs per head) that work id processes
+ * (workgroup id without a work counter, work-queue position with one).  Ids [0, n - tail) keep the XCD group mapping the kernel uses
  * without an order (G = 64 for prism_bsa_fwd and prism_bsa_bwd_dq, 32 for
  * prism_bsa_bwd_dkdv); the last tail ids (tail <= 16384) take the pairs that
  * mapping gives them, longest union list (ulen) first, so the launch does not
@@ -289,6 +289,16 @@ int prism_tile_masks(const uint8_t* valid, int64_t Nt, uint64_t* masks, hipStrea
  * mapped to +inf so that its probabilities are exactly 0. */
 int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
 
+/* Work counter of the attention kernels (work_counter argument): one int32 of
+ * device memory, which the call zeroes on its stream before the launch.  With
+ * it, the launch is persistent: as many workgroups as the GPU holds at once,
+ * each taking the next pair of `order` from an atomic work queue until none
+ * is left, so the work spreads over the XCDs as they free up (the hardware
+ * hands workgroup ids to the XCDs round-robin, whatever their load).  Calls
+ * that may overlap need counters of their own.  NULL: one workgroup per
+ * pair.  The results are bit-identical either way.  No counterpart in the
+ * reference (a Triton launch of one program per tile). */
+
 /* attn_fwd_bsa_varlen_triton (bsa_interface.py:328-385) with
  * _attn_fwd_bsa_varlen_align (flash_attn_bsa_varlen_mask.py:191-319), on
  * 64-token tiles (larger chunks are lists of their tiles).  Sq, Sk (query and
@@ -303,7 +313,7 @@ int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
 int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
                   const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen, const int32_t* ucols,
                   const int32_t* pairmap, const int32_t* order, float sm_scale, void* o, float* lse,
-                  hipStream_t stream);
+                  int32_t* work_counter, hipStream_t stream);
 
 /* _attn_bwd_preprocess (common.py:110-127): delta[r] = sum_d o[r][d] * do[r][d]
  * over rows of bf16 [rows, D] tensors; fp32 out. */
@@ -322,7 +332,8 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
                        const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint8_t* kv_valid,
                        const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap,
-                       const int32_t* order, float sm_scale, void* dk, void* dv, hipStream_t stream);
+                       const int32_t* order, float sm_scale, void* dk, void* dv, int32_t* work_counter,
+                       hipStream_t stream);
 
 /* dQ of attn_bwd_bsa_varlen_triton (bsa_interface.py:489-523;
  * _attn_bwd_dq_bsa_varlen_align_wrapper, flash_attn_bsa_varlen_mask.py:879-1014).
@@ -331,7 +342,7 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
 int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
                      int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart,
                      const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap, const int32_t* order,
-                     float sm_scale, void* dq, hipStream_t stream);
+                     float sm_scale, void* dq, int32_t* work_counter, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -46,10 +46,10 @@ SIGNATURES = {
     "prism_lists_csr_fill": [P, P, P, I64, P, P, P],
     "prism_tile_masks": [P, I64, P, P],
     "prism_lse_to_m2": [P, I64, P, P],
-    "prism_bsa_fwd": [P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P],
+    "prism_bsa_fwd": [P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P, P],
     "prism_bwd_preprocess": [P, P, I64, I32, P, P],
-    "prism_bsa_bwd_dkdv": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P],
-    "prism_bsa_bwd_dq": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P],
+    "prism_bsa_bwd_dkdv": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P, P],
+    "prism_bsa_bwd_dq": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P],
 }
 
 _lib = None

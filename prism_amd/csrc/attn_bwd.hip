@@ -14,8 +14,8 @@
 // key at +inf (prism_lse_to_m2).
 //
 // MI355X design, shared by both kernels:
-//  * one workgroup per PAIR of tiles (2p, 2p+1) walking the sorted union of
-//    the two tiles' lists (prism_pair_union);
+//  * a PAIR of tiles (2p, 2p+1) is taken by one workgroup, which walks the
+//    sorted union of the two tiles' lists (prism_pair_union);
 //  * the operand tiles of list entry j + NST - 1 are copied HBM -> LDS by
 //    global_load_lds_dwordx4 while entry j is multiplied (NST = 3 stages for
 //    dK/dV, 2 for dQ; one barrier per entry, no VGPR staging);
@@ -23,8 +23,10 @@
 //    S / dP products, transposing reads (ds_read_b64_tr_b16) for the products
 //    that contract over the tile's rows (see RowTile), so no transposed
 //    copies of Q, K or dO are made;
-//  * workgroup ids are remapped per XCD (xcd_group_remap: runs of
-//    neighbouring pairs per L2, one head region at a time GPU-wide).
+//  * pairs in the launch order of prism_pair_order; with a work counter,
+//    persistent workgroups take them from an atomic work queue (as in the
+//    forward kernel), without one a workgroup per pair with its id remapped
+//    per XCD (xcd_group_remap).
 // dK/dV: one 8-wave workgroup per CU (two waves per SIMD).  The waves split
 // each (tile, tile) product in two halves of the query rows, so every wave
 // holds half-size partial accumulators; the two partials are added in a
@@ -65,6 +67,8 @@ struct BwdArgs {
   int npairs;               // tile pairs per head of the side the grid walks
   float sm_scale, scale_log2;
   uint16_t *dq, *dk, *dv;
+  int total;                // pairs of the launch (BH * npairs)
+  int* queue;               // work-queue counter (persistent launch), or null: one pair per workgroup
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -89,18 +93,17 @@ struct BwdTiles {
   static_assert(DKDV_LDS <= 160 * 1024 && DQ_LDS <= 160 * 1024, "LDS budget");
 };
 
+// one pair-union work list: the two key tiles of pair `logical`
 template <int D>
-__global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
+__device__ __forceinline__ void bsa_bwd_dkdv_pair(const BwdArgs& a, uint8_t* smem, int logical) {
   using T = BwdTiles<D>;
   using RT = typename T::RT;
   constexpr int NS = D / 16, NDT = D / 32;
   constexpr int SB = T::DKDV_STAGE;
-  __shared__ __align__(16) uint8_t smem[T::DKDV_LDS];
 
-  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int tid = opaque_thread_id(), lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
   const int kh = w & 1, qh = (w >> 1) & 1, tk = w >> 2;
-  const int logical = a.order ? a.order[blockIdx.x] : xcd_group_remap<32>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
@@ -345,19 +348,33 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   }
 }
 
+// One workgroup per pair (no work counter), or persistent workgroups that
+// take pairs from the work queue (work_queue_next).  The pair body re-reads
+// the arguments (kernel_args) and recomputes its lane offsets
+// (opaque_thread_id), so nothing stays in registers across pairs.
 template <int D>
-__global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
+  __shared__ __align__(16) uint8_t smem[BwdTiles<D>::DKDV_LDS];
+  __shared__ int next_id;
+  for (int pid = (int)blockIdx.x;;) {
+    const BwdArgs ap = kernel_args<BwdArgs>();
+    bsa_bwd_dkdv_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<32>(pid, a.total));
+    if (!work_queue_next(a.queue, a.total, &next_id, &pid)) return;
+  }
+}
+
+// one pair-union work list: the two query tiles of pair `logical`
+template <int D>
+__device__ __forceinline__ void bsa_bwd_dq_pair(const BwdArgs& a, uint8_t* smem, int logical) {
   using T = BwdTiles<D>;
   using RT = typename T::RT;
   constexpr int NS = D / 16, NDT = D / 32;
   constexpr int SB = T::DQ_STAGE;
   constexpr int SLOTS = 2 * RT::KB / 4;  // KB-instructions per wave and stage (4 waves)
-  __shared__ __align__(16) uint8_t smem[kStagesDq * SB];
 
-  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int tid = opaque_thread_id(), lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
   const int qh = w & 1, tq = w >> 1;
-  const int logical = a.order ? a.order[blockIdx.x] : xcd_group_remap<64>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
@@ -518,6 +535,21 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
     }
 }
 
+// One workgroup per pair (no work counter), or persistent workgroups that
+// take pairs from the work queue (work_queue_next).  The pair body re-reads
+// the arguments (kernel_args) and recomputes its lane offsets
+// (opaque_thread_id), so nothing stays in registers across pairs.
+template <int D>
+__global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
+  __shared__ __align__(16) uint8_t smem[kStagesDq * BwdTiles<D>::DQ_STAGE];
+  __shared__ int next_id;
+  for (int pid = (int)blockIdx.x;;) {
+    const BwdArgs ap = kernel_args<BwdArgs>();
+    bsa_bwd_dq_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<64>(pid, a.total));
+    if (!work_queue_next(a.queue, a.total, &next_id, &pid)) return;
+  }
+}
+
 // delta[row] = sum_d o[row][d] * do[row][d]: one wave per row, 4 rows per block
 template <int D>
 __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dO,
@@ -540,6 +572,7 @@ int check_common(const void* q, const void* k, int BH, int64_t Sq, int64_t Sk, i
   return PRISM_OK;
 }
 
+
 }  // namespace
 
 extern "C" {
@@ -558,8 +591,7 @@ int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, fl
 int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* do_, const float* m2,
                        const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint8_t* kv_valid,
                        const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap,
-                       const int32_t* order, float sm_scale, void* dk,
-                       void* dv,
+                       const int32_t* order, float sm_scale, void* dk, void* dv, int32_t* work_counter,
                        hipStream_t stream) {
   int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dkdv");
   if (rc) return rc;
@@ -570,7 +602,12 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
   a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.order = order; a.Sq = Sq; a.Sk = Sk;
   a.npairs = (int)(Sk / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
-  const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
+  a.total = (int)((int64_t)BH * a.npairs);
+  a.queue = work_counter;
+  if (a.queue) zero_counter_kernel<<<1, 1, 0, stream>>>(a.queue);
+  const int res = !a.queue ? 0 : D == 128 ? resident_workgroups<bsa_bwd_dkdv_kernel<128>>(512)
+                                          : resident_workgroups<bsa_bwd_dkdv_kernel<64>>(512);
+  const unsigned blocks = (unsigned)(a.queue && res < a.total ? res : a.total);
   if (D == 128) bsa_bwd_dkdv_kernel<128><<<blocks, 512, 0, stream>>>(a);
   else bsa_bwd_dkdv_kernel<64><<<blocks, 512, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_bsa_bwd_dkdv");
@@ -580,7 +617,7 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
 int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do_, const float* m2, const float* delta,
                      int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen,
                      const int32_t* ucols, const int32_t* pairmap, const int32_t* order, float sm_scale, void* dq,
-                     hipStream_t stream) {
+                     int32_t* work_counter, hipStream_t stream) {
   int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dq");
   if (rc) return rc;
   PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq: null pointer");
@@ -590,7 +627,12 @@ int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do
   a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.order = order; a.Sq = Sq; a.Sk = Sk;
   a.npairs = (int)(Sq / 128);
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
-  const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
+  a.total = (int)((int64_t)BH * a.npairs);
+  a.queue = work_counter;
+  if (a.queue) zero_counter_kernel<<<1, 1, 0, stream>>>(a.queue);
+  const int res = !a.queue ? 0 : D == 128 ? resident_workgroups<bsa_bwd_dq_kernel<128>>(256)
+                                          : resident_workgroups<bsa_bwd_dq_kernel<64>>(256);
+  const unsigned blocks = (unsigned)(a.queue && res < a.total ? res : a.total);
   if (D == 128) bsa_bwd_dq_kernel<128><<<blocks, 256, 0, stream>>>(a);
   else bsa_bwd_dq_kernel<64><<<blocks, 256, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_bsa_bwd_dq");

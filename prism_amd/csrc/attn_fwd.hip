@@ -8,8 +8,8 @@
 // without a valid key), natural-log LSE out.
 //
 // MI355X design:
-//  * one workgroup (4 waves) per PAIR of query tiles (2p, 2p+1) of a zone,
-//    two workgroups per CU (two waves per SIMD).  The two tiles of a
+//  * a PAIR of query tiles (2p, 2p+1) of a zone is taken by one workgroup
+//    (4 waves), two workgroups per CU (two waves per SIMD).  The two tiles of a
 //    128-token block share one list and neighbouring 64-token blocks share
 //    most of theirs; the workgroup walks the sorted union of the two lists
 //    (prism_pair_union), so each K/V tile it stages in LDS serves up to 128
@@ -29,10 +29,14 @@
 //    reads (ds_read_b64_tr_b16, see RowTile), so V needs no transposed copy.
 //  * key validity: union entries flag tiles that contain padding; only those
 //    load their 64-bit validity word and mask.
-//  * workgroup ids are remapped (xcd_group_remap) so that each XCD (own L2)
-//    processes runs of neighbouring tile pairs, whose lists overlap, while the
-//    whole GPU sweeps one head region at a time (K/V stay in the Infinity
-//    Cache).
+//  * pairs are taken in the launch order of prism_pair_order (one head region
+//    at a time GPU-wide, so K/V stay in the Infinity Cache; the longest lists
+//    of the last quarter first).  With a work counter the launch is
+//    persistent: as many workgroups as the GPU holds, each taking the next
+//    pair from an atomic work queue, so the work spreads over the XCDs as
+//    they free up (without one, the hardware hands workgroup ids to the XCDs
+//    round-robin whatever their load, and xcd_group_remap gives each XCD runs
+//    of neighbouring pairs).
 #include "common.h"
 #include "mfma.h"
 #include "tile_dma.h"
@@ -54,6 +58,8 @@ struct FwdArgs {
   float scale_log2;        // sm_scale * log2(e)
   uint16_t* o;             // [BH, Sq, D]
   float* lse;              // [BH, Sq] natural log
+  int total;               // pairs of the launch (BH * npairs)
+  int* queue;              // work-queue counter (persistent launch), or null: one pair per workgroup
 };
 
 constexpr int kStages = 2;  // two workgroups per CU: 2 x 2 stages of K and V fill the LDS
@@ -66,17 +72,16 @@ struct FwdTiles {
   static_assert(STAGE_KB % 2 == 0, "stage must split evenly over 2 waves");
 };
 
+// one pair-union work list: the two query tiles of pair `logical`
 template <int D>
-__global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
+__device__ __forceinline__ void bsa_fwd_pair(const FwdArgs& a, uint8_t* smem, int logical) {
   using T = FwdTiles<D>;
   using RT = typename T::RT;
   constexpr int NS = D / 16;   // MFMA k-steps over d
   constexpr int NDT = D / 32;  // 32-row d blocks of O^T
-  __shared__ __align__(16) uint8_t smem[kStages * T::STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int tid = opaque_thread_id(), lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
-  const int logical = a.order ? a.order[blockIdx.x] : xcd_group_remap<64>((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / a.npairs, pair = logical - bh * a.npairs;
   const int32_t* U = a.ucols + a.ustart[logical];
   const int n = a.ulen[logical];
@@ -257,6 +262,21 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   if (g == 0) a.lse[(int64_t)bh * a.Sq + qrow] = (m + __log2f(l)) * 0.6931471805599453f;
 }
 
+// One workgroup per pair (no work counter), or persistent workgroups that
+// take pairs from the work queue (work_queue_next).  The pair body re-reads
+// the arguments (kernel_args) and recomputes its lane offsets
+// (opaque_thread_id), so nothing stays in registers across pairs.
+template <int D>
+__global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
+  __shared__ __align__(16) uint8_t smem[kStages * FwdTiles<D>::STAGE];
+  __shared__ int next_id;
+  for (int pid = (int)blockIdx.x;;) {
+    const FwdArgs ap = kernel_args<FwdArgs>();
+    bsa_fwd_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<64>(pid, a.total));
+    if (!work_queue_next(a.queue, a.total, &next_id, &pid)) return;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -264,7 +284,7 @@ extern "C" {
 int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
                   const uint64_t* tile_masks,
                   const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap,
-                  const int32_t* order, float sm_scale, void* o, float* lse,
+                  const int32_t* order, float sm_scale, void* o, float* lse, int32_t* work_counter,
                   hipStream_t stream) {
   PRISM_REQUIRE(q && k && v && ustart && ulen && ucols && o && lse, "prism_bsa_fwd: null pointer");
   PRISM_REQUIRE(D == 64 || D == 128, "prism_bsa_fwd: head_dim %d unsupported (64, 128)", D);
@@ -278,7 +298,12 @@ int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S
   a.npairs = (int)(Sq / 128);
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.o = (uint16_t*)o; a.lse = lse;
-  const unsigned blocks = (unsigned)((int64_t)BH * a.npairs);
+  a.total = (int)((int64_t)BH * a.npairs);
+  a.queue = work_counter;
+  if (a.queue) zero_counter_kernel<<<1, 1, 0, stream>>>(a.queue);
+  const int res = !a.queue ? 0 : D == 128 ? resident_workgroups<bsa_fwd_kernel<128>>(256)
+                                          : resident_workgroups<bsa_fwd_kernel<64>>(256);
+  const unsigned blocks = (unsigned)(a.queue && res < a.total ? res : a.total);
   if (D == 128) bsa_fwd_kernel<128><<<blocks, 256, 0, stream>>>(a);
   else bsa_fwd_kernel<64><<<blocks, 256, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_bsa_fwd");

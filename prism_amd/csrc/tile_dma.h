@@ -146,6 +146,68 @@ __device__ __forceinline__ int stage_ahead(int st) {
   return st == 0 ? NST - 1 : st - 1;
 }
 
+// ------------------------------------------------------------ work queue
+// Persistent launches (queue != null): workgroup b first takes pair id b,
+// then the ids gridDim.x + atomicAdd(queue, 1) until they run past total.
+// The id is published through LDS between two barriers (the first also keeps
+// the next pair's tile copies off the LDS that slower waves still read), so
+// all waves of the workgroup take the same ids and leave the loop together.
+// Returns false when the workgroup is done (always, without a queue).
+__device__ __forceinline__ bool work_queue_next(int* queue, int total, int* slot, int* pid) {
+  if (queue == nullptr) return false;
+  __syncthreads();
+  if (threadIdx.x == 0) *slot = (int)gridDim.x + atomicAdd(queue, 1);
+  __syncthreads();
+  *pid = (int)uniform_u32((uint32_t)*slot);
+  return *pid < total;
+}
+
+// Workgroups of Kernel (threads each, static LDS only) that the current
+// device holds at once: the grid of a persistent launch (looked up once per
+// device and kernel)
+template <auto Kernel>
+int resident_workgroups(int threads) {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0, per = 0;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, Kernel, threads, 0);
+  const int n = cus * per > 0 ? cus * per : 1;
+  if (dev < 64) cached[dev] = n;
+  return n;
+}
+
+// zeroes the work-queue counter of a persistent launch on its stream (a
+// kernel, not a memset, so the launch pair can be captured in a graph)
+static __global__ void zero_counter_kernel(int* counter) { *counter = 0; }
+
+// The kernel's argument struct, re-read from the kernarg segment through a
+// pointer the compiler cannot see through: a persistent kernel then reloads
+// its arguments (scalar loads) per pair instead of holding them in SGPRs
+// across the whole loop, where they spill.  A is the kernel's only argument.
+template <class A>
+__device__ __forceinline__ A kernel_args() {
+#if __HIP_DEVICE_COMPILE__
+  typedef __attribute__((address_space(4))) const A* cptr;
+  cptr p = (cptr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return *p;
+#else
+  return A{};  // (host pass; device code only)
+#endif
+}
+
+// threadIdx.x as a value the compiler cannot see through: the lane-dependent
+// offsets of a pair are then computed per pair, not hoisted out of a
+// persistent kernel's loop to stay live (and spill) across it
+__device__ __forceinline__ int opaque_thread_id() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // ------------------------------------------------------------ row tiles
 // A bf16 tile [64][D] (rows of W = 2D bytes) is kept in LDS without padding,
 // one quad of rows (4 rows, Q = 4W bytes) after the other, each quad being a

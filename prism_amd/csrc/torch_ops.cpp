@@ -513,6 +513,11 @@ AttnShape attn_shape(const Tensor& q, const Tensor& k, const Tensor& v) {
 }
 void check_union(const Tensor& us, const Tensor& ul, const Tensor& uc) { check_lists(us, ul, uc); }
 
+// a work-queue counter for one attention launch (persistent workgroups; the
+// entry point zeroes it on the stream), from the caching allocator: each call
+// has its own, and the temporary lives until the launch call returns
+Tensor work_counter(const Tensor& like) { return at::empty({1}, opts(like, at::kInt)); }
+
 std::tuple<Tensor, Tensor> bsa_fwd(const Tensor& q_, const Tensor& k_, const Tensor& v_, const OptT& masks_,
                                    const Tensor& us_, const Tensor& ul_, const Tensor& uc_, const OptT& pairmap_,
                                    const OptT& order_, double sm_scale) {
@@ -530,7 +535,7 @@ std::tuple<Tensor, Tensor> bsa_fwd(const Tensor& q_, const Tensor& k_, const Ten
   PRISM_TORCH_CALL(prism_bsa_fwd, q.data_ptr(), k.data_ptr(), v.data_ptr(), (int)(s.B * s.H), s.Sq, s.Sk, (int)s.D,
                    (const uint64_t*)p(masks), us.data_ptr<int64_t>(), ul.data_ptr<int32_t>(), uc.data_ptr<int32_t>(),
                    (const int32_t*)p(pairmap), (const int32_t*)p(order), (float)sm_scale, o.data_ptr(),
-                   lse.data_ptr<float>(), stream_of(q));
+                   lse.data_ptr<float>(), work_counter(q).data_ptr<int32_t>(), stream_of(q));
   return {o, lse};
 }
 
@@ -575,7 +580,8 @@ std::tuple<Tensor, Tensor> bsa_bwd_dkdv(const Tensor& q_, const Tensor& k_, cons
   PRISM_TORCH_CALL(prism_bsa_bwd_dkdv, q.data_ptr(), k.data_ptr(), v.data_ptr(), d.data_ptr(), m2.data_ptr<float>(),
                    delta.data_ptr<float>(), (int)(s.B * s.H), s.Sq, s.Sk, (int)s.D, (const uint8_t*)p(kv),
                    us.data_ptr<int64_t>(), ul.data_ptr<int32_t>(), uc.data_ptr<int32_t>(), (const int32_t*)p(pairmap),
-                   (const int32_t*)p(order), (float)sm_scale, dk.data_ptr(), dv.data_ptr(), stream_of(q));
+                   (const int32_t*)p(order), (float)sm_scale, dk.data_ptr(), dv.data_ptr(),
+                   work_counter(q).data_ptr<int32_t>(), stream_of(q));
   return {dk, dv};
 }
 
@@ -603,7 +609,7 @@ Tensor bsa_bwd_dq(const Tensor& q_, const Tensor& k_, const Tensor& v_, const Te
   PRISM_TORCH_CALL(prism_bsa_bwd_dq, q.data_ptr(), k.data_ptr(), v.data_ptr(), d.data_ptr(), m2.data_ptr<float>(),
                    delta.data_ptr<float>(), (int)(s.B * s.H), s.Sq, s.Sk, (int)s.D, (const uint64_t*)p(masks),
                    us.data_ptr<int64_t>(), ul.data_ptr<int32_t>(), uc.data_ptr<int32_t>(), (const int32_t*)p(pairmap),
-                   (const int32_t*)p(order), (float)sm_scale, dq.data_ptr(), stream_of(q));
+                   (const int32_t*)p(order), (float)sm_scale, dq.data_ptr(), work_counter(q).data_ptr<int32_t>(), stream_of(q));
   return dq;
 }
 

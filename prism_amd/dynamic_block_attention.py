@@ -174,7 +174,7 @@ class _DynBSA(torch.autograd.Function):
 
         def scatter_dkdv(dk_re, dv_re):
             # dK and dV back to THW order on the side stream, during the dQ kernel
-            if ops.OVERLAP_SIDE_WORK:
+            if ops.OVERLAP_SIDE_WORK and ops.OVERLAP_DKDV_SCATTER:
                 side["dkdv"] = ops.side_launch(
                     dk_re.device, lambda: (ops.scatter_rows(dk_re, lay, tk), ops.scatter_rows(dv_re, lay, tv)),
                     reads=(dk_re, dv_re), produces=lambda out: out)

@@ -541,10 +541,14 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 
 # Side work that the attention launches do not depend on runs on the side
 # stream while they run: the per-key-tile lists of the backward during the
-# forward kernel, the dK / dV scatters during the dQ kernel.  Inputs and
-# outputs of the side work are recorded on the stream that did not allocate
-# them (the caching allocator keeps their memory until that work is done).
+# forward kernel (OVERLAP_SIDE_WORK), and, with OVERLAP_DKDV_SCATTER as well,
+# the dK / dV scatters during the dQ kernel.  Inputs and outputs of the side
+# work are recorded on the stream that did not allocate them (the caching
+# allocator keeps their memory until that work is done).  The dQ launch keeps
+# every CU busy until its work queue drains, so scatters queued beside it
+# mostly wait for its end and then delay its last workgroups: off by default.
 OVERLAP_SIDE_WORK = True
+OVERLAP_DKDV_SCATTER = False
 
 
 def side_launch(device: torch.device, fn, reads=(), produces=None):

@@ -154,7 +154,7 @@ class _ChunkBSA(torch.autograd.Function):
 
         def scatter_dkdv(dk_re, dv_re):
             # dK and dV back to the input order on the side stream, during the dQ kernel
-            if ops.OVERLAP_SIDE_WORK:
+            if ops.OVERLAP_SIDE_WORK and ops.OVERLAP_DKDV_SCATTER:
                 side["dkdv"] = ops.side_launch(
                     dk_re.device,
                     lambda: (ops.chunk_scatter_rows(dk_re, plan.lk, tk), ops.chunk_scatter_rows(dv_re, plan.lk, tv)),

@@ -82,11 +82,12 @@ def test_invalid_arguments_raise_without_gpu():
         _lib.call("prism_scatter_rows", 1, 1, 1, 500, 64, 1, 8, 8, 8, 7, 8, 8, 1, 0, None)
     with pytest.raises(ValueError, match="null pointer"):
         _lib.call("prism_bsa_fwd", None, None, None, 1, 128, 128, 64, None, None, None, None, None, None, 0.1, None,
-                  None, None)
+                  None, None, None)
     with pytest.raises(ValueError, match="head_dim"):
-        _lib.call("prism_bsa_fwd", 1, 1, 1, 1, 128, 128, 96, None, 1, 1, 1, None, None, 0.1, 1, 1, None)
+        _lib.call("prism_bsa_fwd", 1, 1, 1, 1, 128, 128, 96, None, 1, 1, 1, None, None, 0.1, 1, 1, None, None)
     with pytest.raises(ValueError, match="multiples of 128"):
-        _lib.call("prism_bsa_bwd_dq", 1, 1, 1, 1, 1, 1, 1, 128, 192, 64, None, 1, 1, 1, None, None, 0.1, 1, None)
+        _lib.call("prism_bsa_bwd_dq", 1, 1, 1, 1, 1, 1, 1, 128, 192, 64, None, 1, 1, 1, None, None, 0.1, 1, None,
+                  None)
     with pytest.raises(ValueError, match="tail must be"):
         _lib.call("prism_pair_order", 1, 100, 64, 101, 1, None)
     with pytest.raises(ValueError, match="group"):
@@ -98,4 +99,4 @@ def test_invalid_arguments_raise_without_gpu():
                   None, None, None, None, None, None, None, None)
     with pytest.raises(ValueError, match="multiple of the chunk|multiples of the chunk"):
         _lib.call("prism_chunk_scatter_rows", 1, 1, 1, 64, 4, 4, 4, 4, 4, 6, 4, 4, 4, 128, 1, 1, None)
-    assert _lib.load().prism_abi_version() == 8
+    assert _lib.load().prism_abi_version() == 9

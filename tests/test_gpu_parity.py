@@ -449,6 +449,53 @@ def test_attention_fwd_bwd_tolerance(case):
         _tol(O.bf16_bits_to_f32(host(g)).reshape(B * H, S, D), r, name)
 
 
+def test_work_queue_bit_identical(case):
+    """The attention entry points through the C-ABI with work_counter = NULL
+    (one workgroup per pair) and with a counter (persistent workgroups taking
+    pairs from a work queue; the counter starts with garbage, which the call
+    clears, and is reused by the next call) give the same bits as the
+    operators, which always pass a counter."""
+    from prism_amd import ops, plan_dynamic
+    valid = case["valid"] if case["pad"] else None
+    B, H, S, D = case["q"].shape
+    BH, sm = B * H, 1 / math.sqrt(D)
+    plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
+                        sparsity=0.6, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
+    ptr = lambda t: None if t is None else t.data_ptr()
+    stream = torch.cuda.current_stream().cuda_stream
+    qorder = ops.pair_order(plan.qunion[1], 64)
+    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, qorder)
+    counter = torch.full((1,), 12345, dtype=torch.int32, device="cuda")
+    for ctr in (None, counter, counter):
+        say("work queue: forward, counter", ctr is not None)
+        o2, lse2 = torch.empty_like(o), torch.empty_like(lse)
+        ops._lib.call("prism_bsa_fwd", ptr(plan.q_re), ptr(plan.k_re), ptr(plan.v_re), BH, S, S, D, ptr(plan.tmasks),
+                      *(ptr(t) for t in plan.qunion), ptr(plan.qpair), ptr(qorder), sm, ptr(o2), ptr(lse2), ptr(ctr),
+                      stream)
+        assert bits_equal(host(o), host(o2)) and bits_equal(host(lse), host(lse2))
+    rng = np.random.default_rng(98)
+    do_t = dev(bf16(rng.standard_normal((B, H, S, D)).astype(np.float32)))
+    delta = ops.bwd_preprocess(o, do_t)
+    m2 = ops.lse_to_m2(lse)
+    klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, BH, plan.lay.Nt)
+    kpair = ops.pair_tiles(*klists, plan.lay.Nt)
+    kunion = ops.pair_union(*klists, plan.lay.Nt, pairmap=kpair)
+    korder = ops.pair_order(kunion[1], 32)
+    dq, dk, dv = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_t, m2, delta, plan.kv_valid, plan.tmasks,
+                             plan.qunion, kunion, sm, plan.qpair, kpair, qorder, korder)
+    common = (ptr(plan.q_re), ptr(plan.k_re), ptr(plan.v_re), ptr(do_t), ptr(m2), ptr(delta), BH, S, S, D)
+    for ctr in (None, counter, counter):
+        say("work queue: backward, counter", ctr is not None)
+        dk2, dv2, dq2 = torch.empty_like(dk), torch.empty_like(dv), torch.empty_like(dq)
+        counter.fill_(-7)
+        ops._lib.call("prism_bsa_bwd_dkdv", *common, ptr(plan.kv_valid), *(ptr(t) for t in kunion), ptr(kpair),
+                      ptr(korder), sm, ptr(dk2), ptr(dv2), ptr(ctr), stream)
+        ops._lib.call("prism_bsa_bwd_dq", *common, ptr(plan.tmasks), *(ptr(t) for t in plan.qunion), ptr(plan.qpair),
+                      ptr(qorder), sm, ptr(dq2), ptr(ctr), stream)
+        for g, g2 in ((dq, dq2), (dk, dk2), (dv, dv2)):
+            assert bits_equal(host(g), host(g2))
+
+
 @pytest.mark.parametrize("compute_padded", [False, True, None])
 def test_end_to_end_autograd(case, compute_padded):
     """flash_attn_bsa_3d_dynamic forward + backward through autograd in THW
