@@ -49,16 +49,20 @@ def summarize(timings) -> Dict[str, Tuple[int, float]]:
 
 def _op(name: str, *args):
     """torch.ops.prism.<name>(*args), timed under kernel_timing() (key
-    "prism_<name>", the C-ABI entry point the operator wraps)."""
+    "prism_<name>", the C-ABI entry point the operator wraps; launches on the
+    side stream get the key "prism_<name> (side stream)": their time includes
+    waiting there for CUs that the main stream's kernels hold)."""
     fn = getattr(_ops, name)
     if _timings is None:
         return fn(*args)
+    cur = torch.cuda.current_stream()
+    key = "prism_" + name + (" (side stream)" if any(cur == s for s in _side_streams.values()) else "")
     st = torch.cuda.Event(enable_timing=True)
     en = torch.cuda.Event(enable_timing=True)
     st.record()
     out = fn(*args)
     en.record()
-    _timings.setdefault("prism_" + name, []).append((st, en))
+    _timings.setdefault(key, []).append((st, en))
     return out
 
 
