@@ -289,15 +289,17 @@ int prism_tile_masks(const uint8_t* valid, int64_t Nt, uint64_t* masks, hipStrea
  * mapped to +inf so that its probabilities are exactly 0. */
 int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
 
-/* Work counter of the attention kernels (work_counter argument): one int32 of
- * device memory, which the call zeroes on its stream before the launch.  With
- * it, the launch is persistent: as many workgroups as the GPU holds at once,
- * each taking the next pair of `order` from an atomic work queue until none
- * is left, so the work spreads over the XCDs as they free up (the hardware
- * hands workgroup ids to the XCDs round-robin, whatever their load).  Calls
- * that may overlap need counters of their own.  NULL: one workgroup per
- * pair.  The results are bit-identical either way.  No counterpart in the
- * reference (a Triton launch of one program per tile). */
+/* Work counters of the attention kernels (work_counter argument): 8 int32 of
+ * device memory (one per XCD), which the call zeroes on its stream before the
+ * launch.  With them, the launch is persistent: as many workgroups as the GPU
+ * holds at once, each taking pairs of `order` from atomic work queues until
+ * none is left: first the positions b = 8 k + x of its own XCD x (the pairs a
+ * one-workgroup-per-pair launch would run there, since the hardware hands
+ * workgroup ids to the XCDs round-robin), then the remaining positions of
+ * slower XCDs.  The work spreads over the XCDs as they free up.  Calls that
+ * may overlap need counters of their own.  NULL: one workgroup per pair.  The
+ * results are bit-identical either way.  No counterpart in the reference (a
+ * Triton launch of one program per tile). */
 
 /* attn_fwd_bsa_varlen_triton (bsa_interface.py:328-385) with
  * _attn_fwd_bsa_varlen_align (flash_attn_bsa_varlen_mask.py:191-319), on

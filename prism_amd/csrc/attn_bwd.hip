@@ -349,17 +349,18 @@ __device__ __forceinline__ void bsa_bwd_dkdv_pair(const BwdArgs& a, uint8_t* sme
 }
 
 // One workgroup per pair (no work counter), or persistent workgroups that
-// take pairs from the work queue (work_queue_next).  The pair body re-reads
+// take pairs from the work queue (work_queue_take).  The pair body re-reads
 // the arguments (kernel_args) and recomputes its lane offsets
 // (opaque_thread_id), so nothing stays in registers across pairs.
 template <int D>
 __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   __shared__ __align__(16) uint8_t smem[BwdTiles<D>::DKDV_LDS];
-  __shared__ int next_id;
-  for (int pid = (int)blockIdx.x;;) {
+  __shared__ WorkQueueState wq;
+  work_queue_init(&wq);
+  for (int pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : (int)blockIdx.x; pid >= 0;
+       pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : -1) {
     const BwdArgs ap = kernel_args<BwdArgs>();
     bsa_bwd_dkdv_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<32>(pid, a.total));
-    if (!work_queue_next(a.queue, a.total, &next_id, &pid)) return;
   }
 }
 
@@ -536,17 +537,18 @@ __device__ __forceinline__ void bsa_bwd_dq_pair(const BwdArgs& a, uint8_t* smem,
 }
 
 // One workgroup per pair (no work counter), or persistent workgroups that
-// take pairs from the work queue (work_queue_next).  The pair body re-reads
+// take pairs from the work queue (work_queue_take).  The pair body re-reads
 // the arguments (kernel_args) and recomputes its lane offsets
 // (opaque_thread_id), so nothing stays in registers across pairs.
 template <int D>
 __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   __shared__ __align__(16) uint8_t smem[kStagesDq * BwdTiles<D>::DQ_STAGE];
-  __shared__ int next_id;
-  for (int pid = (int)blockIdx.x;;) {
+  __shared__ WorkQueueState wq;
+  work_queue_init(&wq);
+  for (int pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : (int)blockIdx.x; pid >= 0;
+       pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : -1) {
     const BwdArgs ap = kernel_args<BwdArgs>();
     bsa_bwd_dq_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<64>(pid, a.total));
-    if (!work_queue_next(a.queue, a.total, &next_id, &pid)) return;
   }
 }
 
@@ -604,7 +606,7 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
   a.total = (int)((int64_t)BH * a.npairs);
   a.queue = work_counter;
-  if (a.queue) zero_counter_kernel<<<1, 1, 0, stream>>>(a.queue);
+  if (a.queue) zero_counter_kernel<<<1, kQueueLanes, 0, stream>>>(a.queue);
   const int res = !a.queue ? 0 : D == 128 ? resident_workgroups<bsa_bwd_dkdv_kernel<128>>(512)
                                           : resident_workgroups<bsa_bwd_dkdv_kernel<64>>(512);
   const unsigned blocks = (unsigned)(a.queue && res < a.total ? res : a.total);
@@ -629,7 +631,7 @@ int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do
   a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
   a.total = (int)((int64_t)BH * a.npairs);
   a.queue = work_counter;
-  if (a.queue) zero_counter_kernel<<<1, 1, 0, stream>>>(a.queue);
+  if (a.queue) zero_counter_kernel<<<1, kQueueLanes, 0, stream>>>(a.queue);
   const int res = !a.queue ? 0 : D == 128 ? resident_workgroups<bsa_bwd_dq_kernel<128>>(256)
                                           : resident_workgroups<bsa_bwd_dq_kernel<64>>(256);
   const unsigned blocks = (unsigned)(a.queue && res < a.total ? res : a.total);

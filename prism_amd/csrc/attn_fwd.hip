@@ -263,17 +263,18 @@ __device__ __forceinline__ void bsa_fwd_pair(const FwdArgs& a, uint8_t* smem, in
 }
 
 // One workgroup per pair (no work counter), or persistent workgroups that
-// take pairs from the work queue (work_queue_next).  The pair body re-reads
+// take pairs from the work queue (work_queue_take).  The pair body re-reads
 // the arguments (kernel_args) and recomputes its lane offsets
 // (opaque_thread_id), so nothing stays in registers across pairs.
 template <int D>
 __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   __shared__ __align__(16) uint8_t smem[kStages * FwdTiles<D>::STAGE];
-  __shared__ int next_id;
-  for (int pid = (int)blockIdx.x;;) {
+  __shared__ WorkQueueState wq;
+  work_queue_init(&wq);
+  for (int pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : (int)blockIdx.x; pid >= 0;
+       pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : -1) {
     const FwdArgs ap = kernel_args<FwdArgs>();
     bsa_fwd_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<64>(pid, a.total));
-    if (!work_queue_next(a.queue, a.total, &next_id, &pid)) return;
   }
 }
 
@@ -300,7 +301,7 @@ int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S
   a.o = (uint16_t*)o; a.lse = lse;
   a.total = (int)((int64_t)BH * a.npairs);
   a.queue = work_counter;
-  if (a.queue) zero_counter_kernel<<<1, 1, 0, stream>>>(a.queue);
+  if (a.queue) zero_counter_kernel<<<1, kQueueLanes, 0, stream>>>(a.queue);
   const int res = !a.queue ? 0 : D == 128 ? resident_workgroups<bsa_fwd_kernel<128>>(256)
                                           : resident_workgroups<bsa_fwd_kernel<64>>(256);
   const unsigned blocks = (unsigned)(a.queue && res < a.total ? res : a.total);

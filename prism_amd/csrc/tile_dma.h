@@ -147,19 +147,52 @@ __device__ __forceinline__ int stage_ahead(int st) {
 }
 
 // ------------------------------------------------------------ work queue
-// Persistent launches (queue != null): workgroup b first takes pair id b,
-// then the ids gridDim.x + atomicAdd(queue, 1) until they run past total.
-// The id is published through LDS between two barriers (the first also keeps
-// the next pair's tile copies off the LDS that slower waves still read), so
-// all waves of the workgroup take the same ids and leave the loop together.
-// Returns false when the workgroup is done (always, without a queue).
-__device__ __forceinline__ bool work_queue_next(int* queue, int total, int* slot, int* pid) {
-  if (queue == nullptr) return false;
+// Persistent launches (queue != null): the queue holds kQueueLanes counters,
+// one per XCD.  Launch position b belongs to lane b mod 8: the XCD to which
+// the hardware's round-robin dispatch sends workgroup b of a launch with one
+// workgroup per pair, so each XCD walks the same runs of neighbouring pairs
+// as there (their lists overlap in its L2).  A workgroup starts on the lane of
+// its own XCD (blockIdx mod 8) and takes b = 8 atomicAdd(counter, 1) + lane;
+// when its lane runs out it moves to the next lane, taking the remaining work
+// of a slower XCD, until all eight are exhausted.  Each position is taken
+// exactly once whichever XCD a workgroup runs on.  The position is published
+// through LDS between two barriers (the first also keeps the next pair's tile
+// copies off the LDS that slower waves still read), so all waves of the
+// workgroup take the same positions and leave the loop together.
+constexpr int kQueueLanes = 8;
+
+// the queue state of a workgroup, in LDS (so no register stays live across
+// the pairs): the published position, the current lane and the number of
+// lanes not yet found exhausted (both used by thread 0 only)
+struct WorkQueueState {
+  int slot, lane, left;
+};
+
+__device__ __forceinline__ void work_queue_init(WorkQueueState* st) {
+  if (threadIdx.x == 0) {
+    st->lane = (int)(blockIdx.x % kQueueLanes);
+    st->left = kQueueLanes;
+  }
+}
+
+// next launch position, or -1 when every lane is exhausted
+__device__ __forceinline__ int work_queue_take(int* queue, int total, WorkQueueState* st) {
   __syncthreads();
-  if (threadIdx.x == 0) *slot = (int)gridDim.x + atomicAdd(queue, 1);
+  if (threadIdx.x == 0) {
+    int r = -1;
+    while (st->left > 0) {
+      const int b = kQueueLanes * atomicAdd(queue + st->lane, 1) + st->lane;
+      if (b < total) {
+        r = b;
+        break;
+      }
+      st->lane = (st->lane + 1) % kQueueLanes;
+      --st->left;
+    }
+    st->slot = r;
+  }
   __syncthreads();
-  *pid = (int)uniform_u32((uint32_t)*slot);
-  return *pid < total;
+  return (int)uniform_u32((uint32_t)st->slot);
 }
 
 // Workgroups of Kernel (threads each, static LDS only) that the current
@@ -179,9 +212,10 @@ int resident_workgroups(int threads) {
   return n;
 }
 
-// zeroes the work-queue counter of a persistent launch on its stream (a
-// kernel, not a memset, so the launch pair can be captured in a graph)
-static __global__ void zero_counter_kernel(int* counter) { *counter = 0; }
+// zeroes the kQueueLanes work-queue counters of a persistent launch on its
+// stream (a kernel, not a memset, so the launch pair can be captured in a
+// graph)
+static __global__ void zero_counter_kernel(int* counter) { counter[threadIdx.x] = 0; }
 
 // The kernel's argument struct, re-read from the kernarg segment through a
 // pointer the compiler cannot see through: a persistent kernel then reloads

@@ -513,10 +513,11 @@ AttnShape attn_shape(const Tensor& q, const Tensor& k, const Tensor& v) {
 }
 void check_union(const Tensor& us, const Tensor& ul, const Tensor& uc) { check_lists(us, ul, uc); }
 
-// a work-queue counter for one attention launch (persistent workgroups; the
-// entry point zeroes it on the stream), from the caching allocator: each call
-// has its own, and the temporary lives until the launch call returns
-Tensor work_counter(const Tensor& like) { return at::empty({1}, opts(like, at::kInt)); }
+// the work-queue counters of one attention launch (persistent workgroups; 8
+// int32, one per XCD, zeroed by the entry point on the stream), from the
+// caching allocator: each call has its own, and the temporary lives until the
+// launch call returns
+Tensor work_counter(const Tensor& like) { return at::empty({8}, opts(like, at::kInt)); }
 
 std::tuple<Tensor, Tensor> bsa_fwd(const Tensor& q_, const Tensor& k_, const Tensor& v_, const OptT& masks_,
                                    const Tensor& us_, const Tensor& ul_, const Tensor& uc_, const OptT& pairmap_,

@@ -465,7 +465,7 @@ def test_work_queue_bit_identical(case):
     stream = torch.cuda.current_stream().cuda_stream
     qorder = ops.pair_order(plan.qunion[1], 64)
     o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, qorder)
-    counter = torch.full((1,), 12345, dtype=torch.int32, device="cuda")
+    counter = torch.full((8,), 12345, dtype=torch.int32, device="cuda")
     for ctr in (None, counter, counter):
         say("work queue: forward, counter", ctr is not None)
         o2, lse2 = torch.empty_like(o), torch.empty_like(lse)
