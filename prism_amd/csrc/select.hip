@@ -219,9 +219,14 @@ __device__ __forceinline__ void radix_pick(const unsigned long long* hb, unsigne
   for (int i = 0; i < 4; ++i) hn[4 * lane + i] = 0ull;
 }
 
+// The cdf weight of a key: floor(w 2^60) of the softmax weight w whose fp32
+// bits the key is (recomputed where used instead of held beside the key: the
+// row kernel then needs 48 fewer VGPRs and keeps more workgroups resident)
+__device__ __forceinline__ uint64_t weight_of(uint32_t key) { return fixp(__uint_as_float(key), 60); }
+
 // Radix search over the 32-bit keys of one row (4 digits of 8 bits, most
 // significant first): the largest v with S(v) >= thr, where S(v) is the sum
-// of wt over present elements with key >= v (wt = W[e], or 1 to count), for
+// of wt over present elements with key >= v (wt = weight_of(key[e]), or 1 to count), for
 // 0 < thr <= S(0).  *above = S(v + 1), the weight strictly above v.  The
 // sums are exact integers, so v is the same as a bisection on S would find.
 // Per digit: an LDS histogram of wt over the elements that match the digits
@@ -231,7 +236,7 @@ __device__ __forceinline__ void radix_pick(const unsigned long long* hb, unsigne
 // costs two workgroup barriers.  hist: [2][256], buffer 0 zero on entry (and
 // again on return).
 template <int EPT, bool WEIGHTED>
-__device__ __forceinline__ uint32_t radix_search(const uint32_t* key, const uint64_t* W, uint64_t present, uint64_t thr,
+__device__ __forceinline__ uint32_t radix_search(const uint32_t* key, uint64_t present, uint64_t thr,
                                                  uint64_t* above, SelShared& sh, unsigned long long* hist) {
   const int tid = threadIdx.x, lane = tid & 63;
   uint32_t prefix = 0;
@@ -252,7 +257,7 @@ __device__ __forceinline__ uint32_t radix_search(const uint32_t* key, const uint
     for (int e = 0; e < EPT; ++e)
       if (((present >> e) & 1) && (key[e] & hmask) == prefix) {
         const uint32_t b = (key[e] >> shift) & 255u;
-        const uint64_t w = WEIGHTED ? W[e] : 1ull;
+        const uint64_t w = WEIGHTED ? weight_of(key[e]) : 1ull;
         if (b != run_bin) {
           if (run_bin != 0xffffffffu) atomicAdd(&hb[run_bin], (unsigned long long)run_w);
           run_bin = b;
@@ -290,7 +295,7 @@ struct SelArgs {
 
 // One workgroup per row; element j lives in thread j / EPT, slot j % EPT.
 template <int EPT>
-__global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
+__global__ __launch_bounds__(kSelThreads, EPT <= 24 ? 4 : 1) void select_kernel(SelArgs a) {
   static_assert(kSelThreads == 256, "one radix bin per thread");
   __shared__ SelShared sh;
   __shared__ unsigned long long hist[2 * 256];
@@ -304,7 +309,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   const int64_t j0 = (int64_t)tid * EPT;
 
   uint32_t key[EPT];
-  uint64_t W[EPT];
   uint64_t present = 0;  // bit e: slot e holds a real element
   int64_t eff = 0;
   uint32_t v_e = 0;
@@ -315,7 +319,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     for (int e = 0; e < EPT; ++e) {
       const int64_t j = (int64_t)tid * EPT + e;
       key[e] = 0;
-      W[e] = 0;
       if (j < N) {
         const uint32_t u = __float_as_uint(s[j]);
         key[e] = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -352,13 +355,12 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
       for (int e = 0; e < EPT; ++e) {
         const float w = ((present >> e) & 1) ? x[e] / sum : 0.0f;
         key[e] = __float_as_uint(w);
-        W[e] = fixp(w, 60);
       }
       // G(v) = sum of W over present elements with key >= v
       auto G = [&](uint32_t v) {
         uint64_t t = 0;
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) t += (((present >> e) & 1) && key[e] >= v) ? W[e] : 0ull;
+        for (int e = 0; e < EPT; ++e) t += (((present >> e) & 1) && key[e] >= v) ? weight_of(key[e]) : 0ull;
         return block_sum_u64(t, sh);
       };
       auto Nge = [&](uint32_t v) {
@@ -374,7 +376,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
       if (G(0) >= a.thr) {
         // crossing value vc: G(vc) >= thr > G(vc + 1) = A
         uint64_t A;
-        vc = radix_search<EPT, true>(key, W, present, a.thr, &A, sh, hist);
+        vc = radix_search<EPT, true>(key, present, a.thr, &A, sh, hist);
         const uint32_t ngt = Nge(vc + 1);
         const uint64_t Wv = fixp(__uint_as_float(vc), 60);
         jt = (a.thr - A - 1) / Wv;  // smallest j with A + (j+1) Wv >= thr
@@ -395,7 +397,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
 
   if (eff > 0) {  // count search: largest v with #(key >= v) >= eff (eff <= #present)
     uint64_t above;
-    v_e = radix_search<EPT, false>(key, W, present, (uint64_t)eff, &above, sh, hist);
+    v_e = radix_search<EPT, false>(key, present, (uint64_t)eff, &above, sh, hist);
     need = (uint64_t)eff - above;
   } else {
     eff = -eff;
@@ -422,8 +424,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   }
   // tiles of the selected blocks: all first-tile entries are read at once,
   // then the tile counts of the selected blocks' tiles (two round trips, not
-  // two per selected block); tinfo[e] = first / second tile listed, or
-  // bit 2 for a block of more than two tiles (counted by a loop)
+  // two per selected block); bit e of ok0m / ok1m: the first / second tile
+  // of block e is listed, of bigm: block e has more than two tiles (counted
+  // by a loop)
   int32_t fb[EPT + 1];
 #pragma unroll
   for (int e = 0; e <= EPT; ++e) {
@@ -431,21 +434,21 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     const bool need = (e < EPT && ((selm >> e) & 1)) || (e > 0 && ((selm >> (e - 1)) & 1));
     fb[e] = need ? a.block_first_tile[j0 + e] : 0;
   }
-  uint32_t tinfo[EPT];
+  uint64_t ok0m = 0, ok1m = 0, bigm = 0;
   uint32_t packed = 0;  // tiles | blocks << 16 of this thread
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
-    tinfo[e] = 0;
     if ((selm >> e) & 1) {
       const int32_t t0 = fb[e], nt = fb[e + 1] - t0;
       uint32_t cnt;
       if (nt <= 2) {
         const bool ok0 = nt >= 1 && (a.tile_count == nullptr || a.tile_count[t0] > 0);
         const bool ok1 = nt >= 2 && (a.tile_count == nullptr || a.tile_count[t0 + 1] > 0);
-        tinfo[e] = (ok0 ? 1u : 0u) | (ok1 ? 2u : 0u);
+        ok0m |= ok0 ? 1ull << e : 0ull;
+        ok1m |= ok1 ? 1ull << e : 0ull;
         cnt = (ok0 ? 1u : 0u) + (ok1 ? 1u : 0u);
       } else {
-        tinfo[e] = 4u;
+        bigm |= 1ull << e;
         cnt = 0;
         for (int32_t t = t0; t < t0 + nt; ++t) cnt += (a.tile_count == nullptr || a.tile_count[t] > 0) ? 1u : 0u;
       }
@@ -458,12 +461,12 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
   for (int e = 0; e < EPT; ++e) {
     if ((selm >> e) & 1) {
       const int32_t t0 = fb[e];
-      if (tinfo[e] < 4u) {
-        if (tinfo[e] & 1u) {
+      if (!((bigm >> e) & 1)) {
+        if ((ok0m >> e) & 1) {
           if (p < a.tcap) trow[p] = t0;
           ++p;
         }
-        if (tinfo[e] & 2u) {
+        if ((ok1m >> e) & 1) {
           if (p < a.tcap) trow[p] = t0 + 1;
           ++p;
         }
