@@ -496,6 +496,53 @@ def test_work_queue_bit_identical(case):
             assert bits_equal(host(g), host(g2))
 
 
+def test_attention_graph_capture_replays(case):
+    """Forward and backward over a prebuilt plan, captured in one HIP graph
+    (persistent launches with their counter-zeroing kernels, the operators'
+    outputs and counters from the graph's memory pool): three replays, with
+    eager work and synchronisations between them, each give the eager bits."""
+    from prism_amd import ops, plan_dynamic
+    valid = case["valid"] if case["pad"] else None
+    B, H, S, D = case["q"].shape
+    sm = 1 / math.sqrt(D)
+    plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
+                        sparsity=0.6, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
+    rng = np.random.default_rng(97)
+    do_t = dev(bf16(rng.standard_normal((B, H, S, D)).astype(np.float32)))
+    qorder = ops.pair_order(plan.qunion[1], 64)
+    klists = ops.transpose_lists(plan.qstart, plan.qlen, plan.qcols, B * H, plan.lay.Nt)
+    kpair = ops.pair_tiles(*klists, plan.lay.Nt)
+    kunion = ops.pair_union(*klists, plan.lay.Nt, pairmap=kpair)
+    korder = ops.pair_order(kunion[1], 32)
+
+    def step():
+        o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, qorder)
+        delta = ops.bwd_preprocess(o, do_t)
+        dq, dk, dv = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_t, ops.lse_to_m2(lse), delta, plan.kv_valid,
+                                 plan.tmasks, plan.qunion, kunion, sm, plan.qpair, kpair, qorder, korder)
+        return o, lse, dq, dk, dv
+
+    ref = [host(t) for t in step()]
+    warm = torch.cuda.Stream()
+    warm.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm):
+        step()
+    torch.cuda.current_stream().wait_stream(warm)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for rep in range(3):
+        say("graph replay", rep)
+        junk = torch.full((1 << 20,), float(rep), device="cuda").cumsum(0)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, t, r in zip(("O", "LSE", "dQ", "dK", "dV"), outs, ref):
+            assert bits_equal(host(t), r), (rep, name)
+        del junk
+
+
 @pytest.mark.parametrize("compute_padded", [False, True, None])
 def test_end_to_end_autograd(case, compute_padded):
     """flash_attn_bsa_3d_dynamic forward + backward through autograd in THW
