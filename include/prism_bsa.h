@@ -297,8 +297,10 @@ int prism_lse_to_m2(const float* lse, int64_t n, float* m2, hipStream_t stream);
  * one-workgroup-per-pair launch would run there, since the hardware hands
  * workgroup ids to the XCDs round-robin), then the remaining positions of
  * slower XCDs.  The work spreads over the XCDs as they free up.  Calls that
- * may overlap need counters of their own.  NULL: one workgroup per pair.  The
- * results are bit-identical either way.  No counterpart in the reference (a
+ * may overlap need counters of their own.  NULL: one workgroup per pair.
+ * Without an `order`, position b runs the pair the same fixed XCD grouping
+ * gives workgroup id b (runs of neighbouring pairs per XCD) in both launch
+ * forms.  The results are bit-identical either way.  No counterpart in the reference (a
  * Triton launch of one program per tile). */
 
 /* attn_fwd_bsa_varlen_triton (bsa_interface.py:328-385) with
@@ -345,6 +347,44 @@ int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do
                      int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks, const int64_t* ustart,
                      const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap, const int32_t* order,
                      float sm_scale, void* dq, int32_t* work_counter, hipStream_t stream);
+
+/* ------------------------------------------------------------------ measured ceilings */
+
+/* Measurement aids of the benchmark's roofline (no counterpart in the
+ * reference).  prism_mfma_peak: two 4-wave workgroups per CU, each wave
+ * running iters x 4 independent v_mfma_f32_32x32x16_bf16 on register operands
+ * (no memory traffic): the bf16 MFMA rate the chip sustains at full load.
+ * *flops (host) = the launch's FLOPs; sink: >= 512 x CUs floats; clocks[0],
+ * clocks[1] (device) = shader-clock and 100 MHz constant-clock ticks of one
+ * wave over the launch (their ratio x 100 MHz is the engine clock it ran at).
+ * prism_copy_peak: dst = src over `bytes` (a multiple of 16) with 16-byte
+ * lanes, the HBM rate of a read + write stream. */
+int prism_mfma_peak(int64_t iters, float* sink, int64_t sink_len, uint64_t* clocks, int64_t* flops,
+                    hipStream_t stream);
+int prism_copy_peak(const void* src, void* dst, int64_t bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------ list checks (debug) */
+
+/* Work-list validation on HOST memory (no counterpart in the reference, whose
+ * Triton kernels read the lists unchecked).  rows lists (start[r], len[r]) into
+ * cols[0, ncols): each len in [0, ntiles], each row inside cols, entries
+ * strictly ascending in [0, ntiles); with unions != 0 the entries are
+ * prism_pair_union entries (tile = entry >> 3): flagged for at least one tile
+ * of the pair, and flagged partial exactly where tile_masks[tile] is not all
+ * ones (never when tile_masks is NULL).  Returns 1 (invalid argument) naming
+ * the first violation.  With PRISM_DEBUG=1 in the environment, prism_bsa_fwd,
+ * prism_bsa_bwd_dkdv, prism_bsa_bwd_dq and prism_pair_union run these checks
+ * on host copies of their lists (synchronising their stream) before launching
+ * anything, and return 1 without a launch when one fails. */
+int prism_check_lists(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t ncols,
+                      int64_t ntiles, int unions, const uint64_t* tile_masks);
+
+/* Launch maps on HOST memory: pairmap [heads, tiles_per_head] (if not NULL)
+ * a permutation of each head's tiles (prism_pair_tiles), order [n_order] (if
+ * not NULL) a permutation of [0, n_order) (prism_pair_order).  No counterpart
+ * in the reference. */
+int prism_check_launch_maps(const int32_t* pairmap, int64_t heads, int64_t tiles_per_head, const int32_t* order,
+                            int64_t n_order);
 
 #ifdef __cplusplus
 }

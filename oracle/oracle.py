@@ -43,7 +43,9 @@ def build() -> str:
 def lib():
     global _LIB
     if _LIB is None:
-        path = os.path.join(_HERE, "liboracle.so")
+        # PRISM_ORACLE_LIB: another build of the same source (the sanitizer
+        # variant of the Makefile)
+        path = os.environ.get("PRISM_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
         if not os.path.exists(path):
             build()
         _LIB = ctypes.CDLL(path)

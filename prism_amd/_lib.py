@@ -50,6 +50,10 @@ SIGNATURES = {
     "prism_bwd_preprocess": [P, P, I64, I32, P, P],
     "prism_bsa_bwd_dkdv": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P, P],
     "prism_bsa_bwd_dq": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P],
+    "prism_check_lists": [P, P, P, I64, I64, I64, I32, P],
+    "prism_mfma_peak": [I64, P, I64, P, P, P],
+    "prism_copy_peak": [P, P, I64, P],
+    "prism_check_launch_maps": [P, I64, I64, P, I64],
 }
 
 _lib = None
@@ -68,11 +72,14 @@ def load() -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
-        if not os.path.exists(LIB_PATH):
+        # PRISM_BSA_LIB: another build of the same sources (the host-sanitized
+        # variant of build.py --sanitize, for CPU test runs)
+        path = os.environ.get("PRISM_BSA_LIB") or LIB_PATH
+        if not os.path.exists(path):
             raise ImportError(
-                f"{LIB_PATH} not found: build the HIP library first (python prism_amd/build.py); "
+                f"{path} not found: build the HIP library first (python prism_amd/build.py); "
                 "prism_amd has no fallback path")
-        lib = ctypes.CDLL(LIB_PATH)
+        lib = ctypes.CDLL(path)
         lib.prism_last_error.restype = ctypes.c_char_p
         lib.prism_last_error.argtypes = []
         lib.prism_abi_version.restype = ctypes.c_int

@@ -2,6 +2,10 @@
 
     python prism_amd/build.py          # run as a file: importing the package
                                        # would load the library it builds
+    PRISM_DEBUG=1 python prism_amd/build.py   # debug build: work lists checked
+                                              # on the host before every launch
+    python prism_amd/build.py --sanitize      # host code under ASan + UBSan
+                                              # (_build_san/, CPU test runs only)
 
 Each csrc/*.hip file is compiled by hipcc for gfx950 only and linked into one
 shared library exporting the C-ABI declared in include/prism_bsa.h;
@@ -27,7 +31,7 @@ TORCH_OPS_SRC = "torch_ops.cpp"
 TORCH_OPS_PATH = os.path.join(HERE, "libprism_torch.so")
 
 SOURCES = ["errors.hip", "stats.hip", "layout.hip", "select.hip", "lists.hip", "attn_fwd.hip", "attn_bwd.hip",
-           "oproj.hip"]
+           "oproj.hip", "validate.hip", "peak.hip"]
 CANONICAL = {"stats.hip", "layout.hip", "select.hip"}
 
 COMMON_FLAGS = [
@@ -46,11 +50,24 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: the prism_bsa HIP library cannot be built")
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    flags = list(COMMON_FLAGS)
+# AddressSanitizer + UBSan on the host code only (device code is built as
+# usual): the argument checks and host-side list checks of the C-ABI, run on
+# the CPU under clang's ASan runtime (tests/run_sanitizers.sh)
+SANITIZE_DIR = os.path.join(HERE, "_build_san")
+SANITIZE_LIB = os.path.join(SANITIZE_DIR, "libprism_bsa_san.so")
+HOST_SANITIZE_FLAGS = ["-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                       "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def _compile(src: str, sanitize: bool = False) -> str:
+    obj = os.path.join(SANITIZE_DIR if sanitize else BUILD_DIR, os.path.splitext(src)[0] + ".o")
+    flags = list(COMMON_FLAGS) + (HOST_SANITIZE_FLAGS if sanitize else [])
     if src in CANONICAL:
         flags.append("-ffp-contract=off")
+    if src == "validate.hip" and os.environ.get("PRISM_DEBUG", "0") not in ("", "0"):
+        # debug build: the attention entry points check their work lists on
+        # the host before every launch unless PRISM_DEBUG=0 at run time
+        flags.append("-DPRISM_DEBUG_DEFAULT=1")
     cmd = [_hipcc(), *flags, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -105,6 +122,26 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+def build_sanitized(verbose: bool = False) -> str:
+    """The host-sanitized variant of libprism_bsa.so (_build_san/, never
+    loaded unless PRISM_BSA_LIB names it; not shipped)."""
+    os.makedirs(SANITIZE_DIR, exist_ok=True)
+    jobs = min(len(SOURCES), max(1, int(os.environ.get("MAX_JOBS", "8"))))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, sanitize=True), SOURCES))
+    cmd = [_hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address", "-Xarch_host",
+           "-fsanitize=undefined", "-Xarch_host", "-shared-libsan", *objs, "-o", SANITIZE_LIB]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{r.stderr[-4000:]}")
+    if verbose:
+        print(f"built {SANITIZE_LIB}")
+    return SANITIZE_LIB
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--sanitize" in sys.argv[1:]:
+        build_sanitized(verbose=True)
+    else:
+        build(verbose=True)
     sys.exit(0)

@@ -49,6 +49,7 @@
 #include "common.h"
 #include "mfma.h"
 #include "tile_dma.h"
+#include "validate.h"
 
 namespace {
 
@@ -360,7 +361,7 @@ __global__ __launch_bounds__(512, 1) void bsa_bwd_dkdv_kernel(BwdArgs a) {
   for (int pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : (int)blockIdx.x; pid >= 0;
        pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : -1) {
     const BwdArgs ap = kernel_args<BwdArgs>();
-    bsa_bwd_dkdv_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<32>(pid, a.total));
+    bsa_bwd_dkdv_pair<D>(ap, smem, a.order ? a.order[pid] : xcd_group_remap<32>(pid, a.total));
   }
 }
 
@@ -548,7 +549,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   for (int pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : (int)blockIdx.x; pid >= 0;
        pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : -1) {
     const BwdArgs ap = kernel_args<BwdArgs>();
-    bsa_bwd_dq_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<64>(pid, a.total));
+    bsa_bwd_dq_pair<D>(ap, smem, a.order ? a.order[pid] : xcd_group_remap<64>(pid, a.total));
   }
 }
 
@@ -598,6 +599,13 @@ int prism_bsa_bwd_dkdv(const void* q, const void* k, const void* v, const void* 
   int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dkdv");
   if (rc) return rc;
   PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dk && dv, "prism_bsa_bwd_dkdv: null pointer");
+  if (prism_debug_enabled()) {
+    // per-key-tile query lists: entries are query tiles, built without tile masks
+    PRISM_DEBUG_CHECK(prism_debug_check_lists("prism_bsa_bwd_dkdv", ustart, ulen, ucols, (int64_t)BH * (Sk / 128),
+                                              Sq / 64, 1, nullptr, stream));
+    PRISM_DEBUG_CHECK(prism_debug_check_maps("prism_bsa_bwd_dkdv", pairmap, BH, Sk / 64, order,
+                                             (int64_t)BH * (Sk / 128), stream));
+  }
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
   a.m2 = m2; a.delta = delta; a.kv_valid = kv_valid;
@@ -623,6 +631,12 @@ int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do
   int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dq");
   if (rc) return rc;
   PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq: null pointer");
+  if (prism_debug_enabled()) {
+    PRISM_DEBUG_CHECK(prism_debug_check_lists("prism_bsa_bwd_dq", ustart, ulen, ucols, (int64_t)BH * (Sq / 128),
+                                              Sk / 64, 1, tile_masks, stream));
+    PRISM_DEBUG_CHECK(prism_debug_check_maps("prism_bsa_bwd_dq", pairmap, BH, Sq / 64, order,
+                                             (int64_t)BH * (Sq / 128), stream));
+  }
   BwdArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
   a.m2 = m2; a.delta = delta; a.tmask = tile_masks;

@@ -40,6 +40,7 @@
 #include "common.h"
 #include "mfma.h"
 #include "tile_dma.h"
+#include "validate.h"
 
 namespace {
 
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   for (int pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : (int)blockIdx.x; pid >= 0;
        pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : -1) {
     const FwdArgs ap = kernel_args<FwdArgs>();
-    bsa_fwd_pair<D>(ap, smem, a.order ? a.order[pid] : a.queue ? pid : xcd_group_remap<64>(pid, a.total));
+    bsa_fwd_pair<D>(ap, smem, a.order ? a.order[pid] : xcd_group_remap<64>(pid, a.total));
   }
 }
 
@@ -293,6 +294,12 @@ int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S
                 "prism_bsa_fwd: Sq and Sk must be positive multiples of 128");
   PRISM_REQUIRE(BH >= 1, "prism_bsa_fwd: BH must be >= 1");
   PRISM_REQUIRE((int64_t)BH * (Sq / 128) < (1ll << 31), "prism_bsa_fwd: grid too large");
+  if (prism_debug_enabled()) {
+    PRISM_DEBUG_CHECK(prism_debug_check_lists("prism_bsa_fwd", ustart, ulen, ucols, (int64_t)BH * (Sq / 128), Sk / 64,
+                                              1, tile_masks, stream));
+    PRISM_DEBUG_CHECK(prism_debug_check_maps("prism_bsa_fwd", pairmap, BH, Sq / 64, order, (int64_t)BH * (Sq / 128),
+                                             stream));
+  }
   FwdArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.tmask = tile_masks;
   a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = pairmap; a.order = order; a.Sq = Sq; a.Sk = Sk;

@@ -19,6 +19,6 @@ extern "C" {
 const char* prism_last_error(void) { return g_err; }
 
 // ABI version of this library; bumped on any signature change.
-int prism_abi_version(void) { return 9; }
+int prism_abi_version(void) { return 10; }
 
 }  // extern "C"

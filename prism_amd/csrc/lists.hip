@@ -17,6 +17,7 @@
 // prism_lists_csr_offsets / prism_lists_csr_fill turn any (start, len, cols)
 // lists into compact CSR (int32 offsets, entries stored once, O(nnz) memory).
 #include "common.h"
+#include "validate.h"
 
 namespace {
 
@@ -337,6 +338,12 @@ int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* co
   const int64_t pairs = rows / 2;
   if (pairs == 0) return PRISM_OK;
   PRISM_REQUIRE(pairs < (1ll << 31), "prism_pair_union: too many pairs");
+  if (prism_debug_enabled()) {
+    PRISM_DEBUG_CHECK(prism_debug_check_lists("prism_pair_union", start, len, cols, rows, col_tiles, 0, nullptr,
+                                              stream));
+    PRISM_DEBUG_CHECK(prism_debug_check_maps("prism_pair_union", pairmap, rows / row_tiles, row_tiles, nullptr, 0,
+                                             stream));
+  }
   pair_union_kernel<<<(unsigned)pairs, 256, 0, stream>>>(start, len, cols, row_tiles, col_tiles, pairmap, tile_masks, ucap, ustart, ulen, ucols);
   PRISM_LAUNCH_CHECK("prism_pair_union");
   return PRISM_OK;

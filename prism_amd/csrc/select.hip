@@ -435,7 +435,7 @@ __global__ __launch_bounds__(kSelThreads, EPT <= 24 ? 4 : 1) void select_kernel(
     fb[e] = need ? a.block_first_tile[j0 + e] : 0;
   }
   uint64_t ok0m = 0, ok1m = 0, bigm = 0;
-  uint32_t packed = 0;  // tiles | blocks << 16 of this thread
+  uint64_t packed = 0;  // tiles | blocks << 32 of this thread (32-bit fields: a row may hold any tile count)
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     if ((selm >> e) & 1) {
@@ -452,11 +452,12 @@ __global__ __launch_bounds__(kSelThreads, EPT <= 24 ? 4 : 1) void select_kernel(
         cnt = 0;
         for (int32_t t = t0; t < t0 + nt; ++t) cnt += (a.tile_count == nullptr || a.tile_count[t] > 0) ? 1u : 0u;
       }
-      packed += cnt | (1u << 16);
+      packed += (uint64_t)cnt | (1ull << 32);
     }
   }
-  const uint32_t pos = block_excl_scan_u32(packed, sh, &tot);
-  uint32_t p = pos & 0xffffu, q = pos >> 16;
+  uint64_t tot64;
+  const uint64_t pos = block_excl_scan_u64(packed, sh, &tot64);
+  int64_t p = (int64_t)(pos & 0xffffffffu), q = (int64_t)(pos >> 32);
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     if ((selm >> e) & 1) {
@@ -477,13 +478,13 @@ __global__ __launch_bounds__(kSelThreads, EPT <= 24 ? 4 : 1) void select_kernel(
             ++p;
           }
       }
-      if (brow) brow[q] = (int32_t)(j0 + e);
+      if (brow && q < a.bcap) brow[q] = (int32_t)(j0 + e);
       ++q;
     }
   }
   if (tid == 0) {
-    a.ntiles[row] = (int32_t)(tot & 0xffffu);
-    if (a.nsel) a.nsel[row] = (int32_t)(tot >> 16);
+    a.ntiles[row] = (int32_t)(tot64 & 0xffffffffu);
+    if (a.nsel) a.nsel[row] = (int32_t)(tot64 >> 32);
   }
 }
 
@@ -688,7 +689,7 @@ __global__ __launch_bounds__(kWideThreads) void select_wide_kernel(SelArgs a) {
           if (p < a.tcap) trow[p] = t;
           ++p;
         }
-      if (brow) brow[pos >> 32] = (int32_t)j;
+      if (brow && (int64_t)(pos >> 32) < a.bcap) brow[pos >> 32] = (int32_t)j;
     }
   }
   if (tid == 0) {
@@ -876,8 +877,8 @@ int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, i
   a.block_first_tile = block_first_tile; a.tile_count = tile_count; a.tcap = tcap; a.tiles = tiles;
   a.ntiles = ntiles; a.sel_blocks = sel_blocks; a.bcap = bcap; a.nsel = nsel;
   const int64_t need = (N + kSelThreads - 1) / kSelThreads;
-  // rows of up to 64 kSelThreads blocks in registers (the per-thread packed
-  // scan then holds 2 N < 65536 tiles and blocks); wider rows pass by pass
+  // rows of up to 64 kSelThreads blocks in registers, wider rows pass by
+  // pass (both place tiles and blocks with 32-bit scan fields)
   if (need > 64) select_wide_kernel<<<(unsigned)rows, kWideThreads, 0, stream>>>(a);
   else if (need <= 8) select_kernel<8><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   else if (need <= 16) select_kernel<16><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);

@@ -120,12 +120,18 @@ class _Plan:
             self.qcols.device, self.build_key_lists, reads=(self.qstart, self.qlen, self.qcols),
             produces=lambda _: (*self.klists, self.kpair, *self.kunion, self.korder))
 
-    def build_key_lists(self):
-        """Per-key-tile query lists, their pairing, unions and launch order
-        (the dK/dV side), built on first use."""
+    def join_side(self):
+        """Make the current stream wait for a side-stream key-list build (the
+        stream fork is joined where it was opened, so a captured or
+        backward-less forward leaves no dangling dependency)."""
         if self.keys_ready is not None:
             torch.cuda.current_stream().wait_event(self.keys_ready)
             self.keys_ready = None
+
+    def build_key_lists(self):
+        """Per-key-tile query lists, their pairing, unions and launch order
+        (the dK/dV side), built on first use."""
+        self.join_side()
         if self.kunion is not None:
             return
         Nt = self.lay.Nt
@@ -154,6 +160,7 @@ class _DynBSA(torch.autograd.Function):
             plan.build_key_lists_side()  # the backward's lists, beside the forward kernel
         o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
                                 plan.qorder)
+        plan.join_side()  # queued after the forward kernel: the key lists still run beside it
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)

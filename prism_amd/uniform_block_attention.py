@@ -104,10 +104,15 @@ class _ChunkPlan:
             self.qcols.device, self.key_lists, reads=(self.qstart, self.qlen, self.qcols),
             produces=lambda _: (*self.klists, self.kpair, *self.kunion, self.korder))
 
-    def key_lists(self):
+    def join_side(self):
+        """Make the current stream wait for a side-stream key-list build (the
+        fork is joined in the forward that opened it)."""
         if getattr(self, "keys_ready", None) is not None:
             torch.cuda.current_stream().wait_event(self.keys_ready)
             self.keys_ready = None
+
+    def key_lists(self):
+        self.join_side()
         if self.kunion is None:
             self.klists = ops.transpose_lists(self.qstart, self.qlen, self.qcols, self.B * self.H, self.lq.Nt,
                                               self.lk.Nt)
@@ -136,6 +141,7 @@ class _ChunkBSA(torch.autograd.Function):
             plan.key_lists_side()  # the backward's lists, beside the forward kernel
         o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
                                 plan.qorder)
+        plan.join_side()  # queued after the forward kernel: the key lists still run beside it
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)

@@ -99,4 +99,4 @@ def test_invalid_arguments_raise_without_gpu():
                   None, None, None, None, None, None, None, None)
     with pytest.raises(ValueError, match="multiple of the chunk|multiples of the chunk"):
         _lib.call("prism_chunk_scatter_rows", 1, 1, 1, 64, 4, 4, 4, 4, 4, 6, 4, 4, 4, 128, 1, 1, None)
-    assert _lib.load().prism_abi_version() == 9
+    assert _lib.load().prism_abi_version() == 10

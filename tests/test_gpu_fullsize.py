@@ -19,8 +19,9 @@ oracle checks what it finishes in seconds:
     the float64 oracle;
   * dK and dV of sampled key tiles sum over every query tile that lists
     them; they are checked against float64 sums over those query tiles with
-    each query row's LSE and delta taken from the kernels (the LSE itself is
-    checked on the sampled query rows);
+    each query row's LSE taken from the kernels (the LSE itself is checked on
+    the sampled query rows) and delta = rowsum(O dO) recomputed in float64
+    from the stored O and dO (the kernels' delta is compared with it);
   * two forward launches give bit-identical O and LSE, two backward
     launches bit-identical dQ, dK and dV.
 """
@@ -146,7 +147,14 @@ def _attention(rng, q_re, k_re, v_re, kv_valid, o, lse, do_re, delta, dq, dk, dv
         Qs = q_re.view(BH, -1, D)[bh][qi].double().cpu().numpy()
         dOs = do_re.view(BH, -1, D)[bh][qi].double().cpu().numpy()
         Ls = lse_h[bh][qi].double().cpu().numpy()
-        dls = delta_h[bh][qi].double().cpu().numpy()
+        # delta = rowsum(O dO) in float64 from the stored bf16 O and dO rows
+        # (not the kernels' delta, which is only compared with it)
+        Os = o.view(BH, -1, D)[bh][qi].double().cpu().numpy()
+        prod = Os * dOs
+        dls = prod.sum(1)
+        dk_delta = delta_h[bh][qi].double().cpu().numpy()
+        # float32 sum of D products: |error| <= D 2^-24 sum |o do|
+        assert (np.abs(dk_delta - dls) <= D * 2.0 ** -24 * np.abs(prod).sum(1) + 1e-30).all(), "delta"
         Kj = _rows(k_re, bh, j * TILE, TILE).astype(np.float64)
         Vj = _rows(v_re, bh, j * TILE, TILE).astype(np.float64)
         s = Qs @ Kj.T * sm

@@ -229,6 +229,29 @@ def test_select_tile_expansion_any_tile_count(N):
             assert np.array_equal(tiles[r, : nt[r]], want), (N, sp, p, r)
 
 
+def test_select_row_of_65536_tiles():
+    """The widest register-held rows (16,384 blocks) with 4 tiles per block
+    and every block selected: 65,536 tiles in one row, more than a 16-bit
+    count holds.  Tiles, blocks and both counts are exact."""
+    from prism_amd import ops
+    rng = np.random.default_rng(17)
+    N, rows = 16384, 3
+    s = _random_scores(rng, rows, N, "plain")
+    first = (4 * np.arange(N + 1)).astype(np.int32)
+    for sp, p in ((0.0, None), (0.0, 0.999999)):
+        say("select 65536 tiles", sp, p)
+        ref_sel, ref_n = O.select(s, sp, p, 0.125)
+        assert (ref_n == N).all()
+        res = ops.select_tiles(dev(s), sp, p, 0.125, dev(first), None, want_blocks=True, tiles_per_block=4)
+        assert res["tcap"] == 4 * N
+        n, nt = host(res["nsel"]), host(res["ntiles"])
+        assert (n == N).all() and (nt == 4 * N).all(), (n, nt)
+        got, tiles = host(res["sel_blocks"]), host(res["tiles"])
+        for r in range(rows):
+            assert np.array_equal(got[r], np.arange(N))
+            assert np.array_equal(tiles[r], np.arange(4 * N))
+
+
 @pytest.mark.parametrize("kind", ["plain", "ties", "neginf", "peaked"])
 def test_select_bitexact_wide_rows(kind):
     """Rows of more than 16384 blocks (the pass-by-pass workgroup kernel):
@@ -447,6 +470,50 @@ def test_attention_fwd_bwd_tolerance(case):
     dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, og, dof, lse_ref, *lists, kv, sm)
     for name, g, r in (("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
         _tol(O.bf16_bits_to_f32(host(g)).reshape(B * H, S, D), r, name)
+
+
+def test_debug_mode_checks_lists(case, monkeypatch):
+    """PRISM_DEBUG=1: the attention entry points copy their work lists to the
+    host and check them before launching.  Valid lists give the same bits as
+    without the checks; corrupted ones (kept inside the operands' bounds,
+    so a launch could not fault) raise ValueError naming the defect."""
+    from prism_amd import ops, plan_dynamic
+    valid = case["valid"] if case["pad"] else None
+    B, H, S, D = case["q"].shape
+    sm = 1 / math.sqrt(D)
+    plan = plan_dynamic(dev(case["qh"]), dev(case["kh"]), dev(case["vh"]), case["grid"], method="ivpq",
+                        sparsity=0.6, cdf_threshold=0.9, valid_mask=None if valid is None else dev(valid).bool())
+    o, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, plan.qorder)
+    plan.build_key_lists()
+    monkeypatch.setenv("PRISM_DEBUG", "1")
+    say("debug: valid lists")
+    o2, lse2 = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, plan.qorder)
+    assert bits_equal(host(o), host(o2)) and bits_equal(host(lse), host(lse2))
+    us, ul, uc = plan.qunion
+    r = int(torch.nonzero(ul >= 2)[0, 0])
+    s = int(us[r])
+    bad = uc.clone()
+    bad[s], bad[s + 1] = uc[s + 1], uc[s]
+    say("debug: descending union entries")
+    with pytest.raises(ValueError, match="not above"):
+        ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, (us, ul, bad), sm, plan.qpair, plan.qorder)
+    bad_order = plan.qorder.clone()
+    bad_order[1] = bad_order[0]
+    say("debug: launch order with a repeated pair")
+    with pytest.raises(ValueError, match="twice"):
+        ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, bad_order)
+    ks, kl, kc = plan.kunion
+    bad_k = kc.clone()
+    bad_k[int(ks[int(torch.nonzero(kl >= 1)[0, 0])])] |= 4  # a partial flag on a query-tile list
+    rng = np.random.default_rng(5)
+    do_t = dev(bf16(rng.standard_normal((B, H, S, D)).astype(np.float32)))
+    delta = ops.bwd_preprocess(o, do_t)
+    m2 = ops.lse_to_m2(lse)
+    say("debug: partial flag in a dK/dV list")
+    with pytest.raises(ValueError, match="flagged partial"):
+        ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_t, m2, delta, plan.kv_valid, plan.tmasks, plan.qunion,
+                    (ks, kl, bad_k), sm, plan.qpair, plan.kpair, plan.qorder, plan.korder)
+    torch.cuda.synchronize()
 
 
 def test_work_queue_bit_identical(case):
