@@ -394,6 +394,80 @@ def measured_traffic(kernel: str):
         return None
 
 
+# ------------------------------------------------------------------ measured ceilings
+WALL_CLOCK_HZ = 100e6   # s_memrealtime (wall_clock64) counts at a constant 100 MHz
+MFMA_FLOPS_PER_CU_CYCLE = 4 * 2 * 32 * 32 * 16 / 32  # one 32x32x16 bf16 MFMA per 32 cycles per SIMD
+
+
+def measured_ceilings():
+    """The device's measured bf16 MFMA, GEMM and HBM rates, beside the
+    datasheet's 2.5 PFLOP/s and 8 TB/s:
+      mfma_loop  prism_mfma_peak: four chains of v_mfma_f32_32x32x16_bf16 per
+                 wave on register operands, two waves per SIMD on every CU,
+                 ~0.25 s per launch (no memory traffic): the MFMA rate at the
+                 clock the chip holds under full matrix load; best of 3;
+      gemm       torch.matmul bf16 8192^3 (hipBLASLt), median of 20;
+      copy       prism_copy_peak over 4 GiB (read + write bytes), best of 10."""
+    import ctypes
+    import statistics
+    import torch
+    from prism_amd import _lib
+    stream = torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(512 * cus, device="cuda", dtype=torch.float32)
+    clocks = torch.zeros(2, device="cuda", dtype=torch.int64)
+    flops = ctypes.c_int64(0)
+
+    def timed(fn, reps):
+        out = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            out.append(a.elapsed_time(b))
+        return out
+
+    def mfma(iters):
+        _lib.call("prism_mfma_peak", iters, sink.data_ptr(), sink.numel(), clocks.data_ptr(),
+                  ctypes.addressof(flops), stream)
+
+    t_probe = timed(lambda: mfma(20000), 2)[-1]
+    iters = max(20000, int(20000 * 250.0 / max(t_probe, 1e-3)))
+    best = None
+    for t in timed(lambda: mfma(iters), 3):
+        rate = flops.value / (t * 1e-3) / 1e12
+        if best is None or rate > best[0]:
+            c = clocks.cpu().tolist()
+            best = (rate, t, c[0] / max(c[1], 1) * WALL_CLOCK_HZ / 1e9)
+    mfma_tflops, mfma_ms, clk = best
+    a = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    timed(lambda: torch.matmul(a, b), 3)
+    g_ms = statistics.median(timed(lambda: torch.matmul(a, b), 20))
+    del a, b
+    nbytes = 4 << 30
+    src = torch.ones(nbytes // 4, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+
+    def copy():
+        _lib.call("prism_copy_peak", src.data_ptr(), dst.data_ptr(), nbytes, stream)
+
+    c_ms = min(timed(copy, 12)[2:])
+    assert bool((dst[:: 1 << 20] == 1).all())
+    del src, dst
+    torch.cuda.empty_cache()
+    return {
+        "mfma_loop_tflops": round(mfma_tflops, 1), "mfma_loop_ms": round(mfma_ms, 1),
+        "mfma_loop_clock_ghz": round(clk, 3),
+        "mfma_loop_issue_clock_ghz": round(mfma_tflops * 1e12 / (cus * MFMA_FLOPS_PER_CU_CYCLE) / 1e9, 3),
+        "gemm_tflops": round(2 * 8192 ** 3 / (g_ms * 1e-3) / 1e12, 1), "gemm": "torch.matmul bf16 8192^3 (hipBLASLt)",
+        "copy_GBps": round(2 * nbytes / (c_ms * 1e-3) / 1e9, 1), "copy": "prism_copy_peak, 4 GiB read + 4 GiB written",
+        "cus": cus,
+    }
+
+
 # ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser()
@@ -417,6 +491,7 @@ def main():
                          "line of its own, not the headline")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the measured MFMA / GEMM / copy ceilings")
     ap.add_argument("--cpu-budget", type=float, default=8.0,
                     help="seconds of sampled masked-SDPA work in the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -515,7 +590,7 @@ def main():
     with torch.no_grad():
         plan = plan_dynamic(q.detach(), k.detach(), v.detach(), gp, method="ivpq", sparsity=sparsity,
                             cdf_threshold=cdf, audio_token_norms=norms0, input_grid=grid,
-                            compact_lists=bool(args.compact_lists))
+                            compact_lists=bool(args.compact_lists), keep_scores=True)
         plan.build_key_lists()
     # bytes of the work lists a step keeps until its backward (per-query-tile
     # lists and their pair unions, per-key-tile lists and theirs)
@@ -565,6 +640,21 @@ def main():
             "traffic": measured_traffic(dom) if args.config == "c4" else None}
     att_ms = sum(kt[n][1] for n in attn if n in kt)
 
+    ceil = None
+    if not args.no_ceilings:
+        log("[bench] measured ceilings (MFMA loop, hipBLASLt GEMM, copy)")
+        ceil = measured_ceilings()
+        pm, pg, ph = ceil["mfma_loop_tflops"], ceil["gemm_tflops"], ceil["copy_GBps"]
+        roof.update(peak_measured=pm, frac_measured=round(roof["achieved"] / pm, 4),
+                    peak_measured_kind="MFMA loop at the sustained clock (prism_mfma_peak)",
+                    gemm_peak_measured=pg, frac_gemm=round(roof["achieved"] / pg, 4),
+                    clock_ghz_mfma_loop=ceil["mfma_loop_clock_ghz"])
+        for name, e in breakdown.items():
+            if "mfma_frac" in e:
+                e["mfma_frac_measured"] = round(e["tflops"] / pm, 4)
+            if "hbm_frac" in e:
+                e["hbm_frac_measured"] = round(e["GBps"] / ph, 4)
+
     dense = None
     if not args.no_dense:
         log("[bench] dense SDPA comparison")
@@ -591,11 +681,18 @@ def main():
         except Exception as e:  # report, do not fail the bench
             dense = {"error": repr(e)[:200]}
         del qd, kd, vd
+        if not fwd_only:
+            log("[bench] own kernels at 100% density (every tile listed)")
+            dense.update(own_dense_point(inp, grid, gp, ms_median, q, k, v, do))
 
     cpu = None
+    sel_agree = None
     if not args.no_cpu and not fwd_only:
         log("[bench] CPU baseline (the reference's torch path, float32, host cores)")
         cpu = cpu_baseline(inp, sparsity, cdf, args.cpu_budget, step_pairs=sum_lens)
+        log("[bench] selection vs the reference's torch sequence (GPU and CPU kernels, same scores)")
+        sel_agree = selection_vs_torch(plan, sparsity, cdf, 1 / math.sqrt(D))
+    plan.scores = None
 
     value = kept_flops / (ms * 1e-3) / 1e12
     rec = {
@@ -612,10 +709,63 @@ def main():
                    "ms_per_step_median": round(ms_median, 3),
                    "compact_lists": bool(args.compact_lists), "list_bytes": list_bytes,
                    "attention_ms": round(att_ms, 3),
-                   "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
+                   "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                   "selection_vs_reference_torch": sel_agree},
         "roofline": roof, "cpu_baseline": cpu, "dense": dense, "breakdown": breakdown,
     }
+    if ceil is not None:
+        rec["config"]["mfma_util_step_measured"] = round(value / ceil["mfma_loop_tflops"], 4)
+        rec["hbm_peak_measured"] = {"GBps": ceil["copy_GBps"], "kernel": ceil["copy"],
+                                    "frac_of_nominal": round(ceil["copy_GBps"] / PEAK_HBM_GBS, 4)}
+        rec["ceilings"] = ceil
     print(json.dumps(rec), flush=True)
+
+
+def own_dense_point(inp, grid, gp, sparse_ms, q, k, v, do):
+    """The same step with every block selected (sparsity 0: every query tile
+    lists every key tile that holds a valid token, i.e. dense attention
+    through these kernels), median of 3 after 1 warm-up."""
+    import torch
+    from prism_amd import DynamicBlockSparseAttention, a2v_token_norms, plan_dynamic
+    B, H, D, S = inp["B"], inp["H"], inp["D"], inp["S"]
+    full = DynamicBlockSparseAttention("ivpq", {"dynamic_block_tau_128": 0.15})
+    full.bsa_params.update({"sparsity": 0.0, "cdf_threshold": None})
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = full(q, k, v, grid, a2v_token_norms(inp["res"]))
+        out.backward(do)
+
+    _, oms, _ = time_region(step, 3, 1)
+    with torch.no_grad():
+        plan = plan_dynamic(q.detach(), k.detach(), v.detach(), gp, method="ivpq", sparsity=0.0,
+                            cdf_threshold=None, audio_token_norms=a2v_token_norms(inp["res"]), input_grid=grid)
+        pairs = plan.sum_lens()
+        Nt = plan.lay.Nt
+    del plan
+    torch.cuda.empty_cache()
+    return {"own_kernel_impl": "this path with sparsity 0 (every key tile with a valid token listed), fwd+bwd",
+            "own_kernel_ms": round(oms, 2), "own_kernel_density": round(pairs / (B * H * Nt * Nt), 4),
+            "own_kernel_kept_block_tflops": round(14 * 64 * 64 * D * pairs / (oms * 1e-3) / 1e12, 1),
+            "own_kernel_dense_equivalent_tflops": round(14 * S * S * D * B * H / (oms * 1e-3) / 1e12, 1),
+            "speedup_sparse_vs_own_dense": round(oms / sparse_ms, 2),
+            "crossover_note": "vs torch SDPA the sparse step wins at every density including 100% (bench.py "
+                              "--sweep); vs the own dense point it wins below 100%, where it is the same "
+                              "computation"}
+
+
+def selection_vs_torch(plan, sparsity, cdf, sm):
+    """Rows whose selected block set differs from the reference's torch op
+    sequence (bsa_interface.py:235-304) in float32 on the same scores, with
+    torch's GPU and CPU kernels (the checker of oracle/torch_path.py)."""
+    from oracle import torch_path as TP
+    from prism_amd import ops
+    N_b = plan.lay.N_b
+    scores = plan.scores.view(-1, N_b)
+    ours = ops.select_tiles(scores, sparsity, cdf, sm, plan.lay.block_first_tile, plan.tile_count, want_blocks=True)
+    out = TP.selection_agreement(scores, ours["sel_blocks"], ours["nsel"], sparsity, cdf, sm)
+    out["rows"] = int(scores.shape[0])
+    return out
 
 
 SWEEP_DENSITIES = (0.05, 0.10, 0.25, 0.50, 1.00)
@@ -681,11 +831,20 @@ def run_sweep(args, inp):
     _, dms, _ = time_region(dstep, DENSE_STEPS, DENSE_WARMUP)
     # the sparse step's time grows with density; first density where it is no
     # longer faster than dense, linearly interpolated (None: faster everywhere)
-    cross = None
-    for a_, b_ in zip(rows, rows[1:]):
-        if a_["ms_per_step"] < dms <= b_["ms_per_step"]:
-            t = (dms - a_["ms_per_step"]) / (b_["ms_per_step"] - a_["ms_per_step"])
-            cross = round(a_["density"] + t * (b_["density"] - a_["density"]), 4)
+    def crossover(dense_ms):
+        for a_, b_ in zip(rows, rows[1:]):
+            if a_["ms_per_step"] < dense_ms <= b_["ms_per_step"]:
+                t = (dense_ms - a_["ms_per_step"]) / (b_["ms_per_step"] - a_["ms_per_step"])
+                return round(a_["density"] + t * (b_["density"] - a_["density"]), 4)
+        return None
+
+    cross = crossover(dms)
+    # k = N_b: every tile with a valid token listed, the same kernels run dense;
+    # against it the sparse step is faster at every lower density (the times
+    # rise monotonically) and equal at that density
+    own = rows[-1]
+    monotonic = all(a_["ms_per_step"] < b_["ms_per_step"] for a_, b_ in zip(rows, rows[1:]))
+    cross_own = own["density"] if monotonic else crossover(own["ms_per_step"])
     print(json.dumps({
         "metric": "C5 density sweep: sparse fwd+bwd ms per step vs dense SDPA fwd+bwd",
         "config": {"workload": "c5: C4 shapes, seeded uniform shape ids, top-k only", "B": B, "H": H, "D": D,
@@ -693,8 +852,16 @@ def run_sweep(args, inp):
         "steps": args.steps, "warmup": args.warmup, "dtype": "bf16", "data": "synthetic",
         "sweep": rows,
         "dense": {"impl": "torch SDPA (ROCm) fwd+bwd, same shape, unpadded", "ms": round(dms, 2),
-                  "tflops": round(14 * S * S * D * B * H / (dms * 1e-3) / 1e12, 1)},
-        "crossover_density": cross}))
+                  "tflops": round(14 * S * S * D * B * H / (dms * 1e-3) / 1e12, 1),
+                  "own_kernel_ms": own["ms_per_step"], "own_kernel_density": own["density"],
+                  "own_kernel_dense_equivalent_tflops": round(14 * S * S * D * B * H / (own["ms_per_step"] * 1e-3)
+                                                              / 1e12, 1)},
+        "crossover_density": cross,
+        "crossover_note": ("vs torch SDPA: " + ("sparse wins at every density, including 100%" if cross is None
+                                                 else f"crossover at density {cross}")
+                           + f"; vs the own dense point (k = N_b, density {own['density']}): crossover at "
+                           f"{cross_own}, i.e. sparse wins at every lower density"),
+        "crossover_density_vs_own_dense": cross_own}))
 
 
 def run_bridge(args, inp):

@@ -3,7 +3,9 @@ in torch float32 for the CPU.
 
 TEST INFRASTRUCTURE ONLY: this is the timed CPU baseline of ``bench.py``
 (``cpu_baseline``) and a cross-check in ``tests/``; the product package
-``prism_amd`` never imports it.  Nothing here is run on the GPU.
+``prism_amd`` never imports it.  Only the selection checker
+(selection_rows_with_margins, selection_agreement) also runs torch's GPU
+kernels, as the second float32 evaluation of the reference's sequence.
 
 It restates, with torch operations in the reference's order of steps (paths
 relative to hymm/models/modules/block_sparse_attention/):
@@ -191,6 +193,75 @@ def select_blocks(score: torch.Tensor, sparsity: Optional[float], p: Optional[fl
     n = ((torch.cumsum(vals, dim=-1) < p).sum(dim=-1, keepdim=True) + 1).clamp(min=lo, max=N)
     idx = idx.masked_fill(torch.arange(ub)[None, :] >= n, N)
     return torch.sort(idx, dim=-1).values
+
+
+def selection_rows_with_margins(scores: torch.Tensor, sparsity, p, sm: float):
+    """The reference's selection (bsa_interface.py:235-304) as the same torch
+    op sequence in float32 on the device that holds `scores` (the GPU, or the
+    host for torch's CPU kernels).  scores: [R, N].  Returns the selected
+    sets as a [R, N] bool mask, the decision margin |exact cumsum - p| at the
+    crossing (float64 cumsum of the float32 weights; inf for top-k rows) and
+    the boundary-tie flags (the weight or score at the cut equals the next)."""
+    R, N = scores.shape
+    dev = scores.device
+    if p is None:
+        k = int((1 - sparsity) * N)
+        _, idx = torch.topk(scores, k, dim=-1)
+        mask = torch.zeros((R, N), dtype=torch.bool, device=dev).scatter_(1, idx, True)
+        srt = torch.sort(scores, dim=-1, descending=True).values
+        tie = (srt[:, k - 1] == srt[:, k]) if k < N else torch.zeros(R, dtype=torch.bool, device=dev)
+        return mask, torch.full((R,), float("inf"), device=dev, dtype=torch.float64), tie
+    w = torch.softmax(scores * sm, dim=-1)
+    lo = 1 if sparsity is None else max(1, int((1 - sparsity) * N))
+    ub = min(N, max(lo, int(p * N) + 1))
+    vals, idx = torch.topk(w, k=ub, dim=-1, largest=True, sorted=True)
+    cdf = torch.cumsum(vals, dim=-1)
+    n = ((cdf < p).to(torch.int32).sum(dim=-1, keepdim=True) + 1).clamp(min=lo, max=N)
+    pos = torch.arange(ub, device=dev)
+    idx = idx.masked_fill(pos >= n, N)
+    mask = torch.zeros((R, N + 1), dtype=torch.bool, device=dev).scatter_(1, idx, True)[:, :N]
+    c = (cdf < p).to(torch.int64).sum(dim=-1)
+    cdf64 = torch.cumsum(vals.double(), dim=-1)
+    near = torch.stack([(cdf64.gather(1, (c - d).clamp(0, ub - 1)[:, None])[:, 0] - p).abs() for d in (0, 1)])
+    margin = near.min(dim=0).values
+    e = torch.clamp(n.squeeze(-1), max=ub).long()
+    srt = torch.sort(w, dim=-1, descending=True).values
+    nxt = torch.clamp(e, max=N - 1)
+    tie = (e < N) & (srt.gather(1, (e - 1)[:, None])[:, 0] == srt.gather(1, nxt[:, None])[:, 0])
+    return mask, margin, tie
+
+
+def selection_agreement(scores: torch.Tensor, sel_blocks: torch.Tensor, nsel: torch.Tensor, sparsity, p,
+                        sm: float, chunk: int = 2048):
+    """Rows whose selected block set (sel_blocks [R, width] ascending, nsel
+    [R] live entries) differs from the reference's torch sequence in float32,
+    run on the scores' device and with torch's CPU kernels.  Returns
+    {"gpu" | "cpu": {"rows_differing", "of_them_tied", "max_untied_margin"}}
+    (margins and ties from the device run; a row is tied if either run finds a
+    tie at its cut)."""
+    R, N = scores.shape
+    dev = scores.device
+    width = sel_blocks.shape[1]
+    out = {"gpu": [0, 0, 0.0], "cpu": [0, 0, 0.0]}
+    for r0 in range(0, R, chunk):
+        s = scores[r0:r0 + chunk]
+        sel = sel_blocks[r0:r0 + chunk].long()
+        live = torch.arange(width, device=dev)[None, :] < nsel[r0:r0 + chunk, None]
+        sel = torch.where(live, sel, torch.full_like(sel, N))
+        mine = torch.zeros((len(s), N + 1), dtype=torch.bool, device=dev).scatter_(1, sel, True)[:, :N]
+        ref_dev = selection_rows_with_margins(s, sparsity, p, sm)
+        ref_cpu = selection_rows_with_margins(s.cpu(), sparsity, p, sm)
+        margin, tie = ref_dev[1], ref_dev[2] | ref_cpu[2].to(dev)
+        for name, ref_mask in (("gpu", ref_dev[0]), ("cpu", ref_cpu[0].to(dev))):
+            diff = (mine != ref_mask).any(dim=1)
+            if bool(diff.any()):
+                dm, dt = margin[diff], tie[diff]
+                out[name][0] += int(diff.sum())
+                out[name][1] += int(dt.sum())
+                untied = dm[~dt]
+                if untied.numel():
+                    out[name][2] = max(out[name][2], float(untied.max()))
+    return {k: {"rows_differing": v[0], "of_them_tied": v[1], "max_untied_margin": v[2]} for k, v in out.items()}
 
 
 def tile_lists(sel: torch.Tensor, kbt: torch.Tensor, tcount: Optional[torch.Tensor], Nt: int):

@@ -4,11 +4,12 @@
 // Reference (hymm/models/modules/block_sparse_attention/):
 //   block_scores_kernel  cal_score (bsa_interface.py:203-207) + invalid-key fill
 //                        (dynamic_block_attention.py:276-279), fp32 out
-//   select_kernel        get_select_indices_topk_from_score (bsa_interface.py:235-248),
-//                        get_select_indices_cdf_from_score (:257-275),
-//                        get_select_indices_cdf_topk_from_score (:284-304),
+//   select_rows_kernel   get_select_indices_topk_from_score (bsa_interface.py:235-248),
+//   (select_kernel,      get_select_indices_cdf_from_score (:257-275),
+//    select_wide_kernel) get_select_indices_cdf_topk_from_score (:284-304),
 //                        fused with the block -> tile expansion
-//                        (dynamic_block_attention.py:297-319)
+//                        (dynamic_block_attention.py:297-319); one wave per
+//                        row up to 6,144 blocks, one workgroup per row beyond
 //   tile_rows_kernel     q-tile rows share their q-block's list (:315-318)
 //   transpose kernels    create_indices_k_from_indices_q_varlen (bsa_interface.py:147-161)
 //                        as a bitmap transpose instead of a dense N_tiles^2 mask + sort
@@ -488,6 +489,395 @@ __global__ __launch_bounds__(kSelThreads, EPT <= 24 ? 4 : 1) void select_kernel(
   }
 }
 
+// ------------------------------------------------------------ one wave per row
+// Rows of up to kWaveMaxN blocks: one wave per row, kWaveRows rows per
+// workgroup.  Element j lives in lane j % 64, slot j / 64 (coalesced loads;
+// slot order is ascending block order, so ballots rank the ties and place the
+// outputs).  After the workgroup's set-up there is no workgroup barrier: each
+// wave runs its row's chain on its own, and the waves of other rows hide its
+// latency (the 256-thread row kernel waits at about twenty barriers per row).
+// The arithmetic is select_kernel's (same canonical exp, division and exact
+// integer sums), so the selection is identical.  LDS per workgroup: the tile
+// flags of every block, built once for the workgroup's rows, and a pair of
+// 256-bin histograms per wave.
+constexpr int kWaveRows = 4;
+constexpr int kWaveMaxN = 6144;
+
+// tile flags of block j: first tile << 3 | second tile listed << 1 | first
+// tile listed for blocks of at most two tiles; kBigBlock for others (their
+// tiles are counted from block_first_tile in the emit)
+constexpr int32_t kBigBlock = 4;
+
+__device__ __forceinline__ int32_t block_tile_flags(const int32_t* first, const int32_t* tile_count, int64_t j) {
+  const int32_t f0 = first[j], nt = first[j + 1] - f0;
+  if (nt > 2 || nt < 0 || f0 < 0 || f0 >= (1 << 28)) return kBigBlock;
+  const bool ok0 = nt >= 1 && (tile_count == nullptr || tile_count[f0] > 0);
+  const bool ok1 = nt >= 2 && (tile_count == nullptr || tile_count[f0 + 1] > 0);
+  return (f0 << 3) | (ok1 ? 2 : 0) | (ok0 ? 1 : 0);
+}
+
+// canon_exp and fixp without branches: the same operations for every input
+// in range, the special cases selected at the end (per-slot branch nests
+// otherwise serialise the unrolled slots of a lane)
+__device__ __forceinline__ float canon_exp_nb(float x) {
+#pragma clang fp contract(off)
+  const float xc = fminf(fmaxf(x, -87.0f), 88.0f);  // == x wherever the result is computed
+  const float t = xc * 1.44269504f;
+  const float n = floorf(t + 0.5f);
+  float r = __builtin_fmaf(-n, 0.693359375f, xc);
+  r = __builtin_fmaf(-n, -2.12194440e-4f, r);
+  float p = 1.98412698e-4f;
+  p = __builtin_fmaf(p, r, 1.38888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const float v = p * __uint_as_float((uint32_t)((int)n + 127) << 23);
+  return x != x ? x : x > 88.0f ? __uint_as_float(0x7f800000u) : x < -87.0f ? 0.0f : v;
+}
+__device__ __forceinline__ uint64_t fixp_nb(float w, int F) {
+  const uint32_t u = __float_as_uint(w);
+  const int e8 = (int)((u >> 23) & 0xffu);
+  const uint64_t m = (u & 0x7fffffu) | (e8 != 0 ? 0x800000u : 0u);
+  const int sh = (e8 != 0 ? e8 : 1) - 150 + F;
+  const uint64_t left = m << (sh > 0 ? (sh < 63 ? sh : 63) : 0);
+  const uint64_t right = sh <= -64 ? 0ull : m >> (-sh > 0 ? -sh : 0);
+  return sh >= 0 ? left : right;
+}
+__device__ __forceinline__ uint64_t weight_of_nb(uint32_t key) { return fixp_nb(__uint_as_float(key), 60); }
+
+// 64-lane reductions and scans through DPP row operations (VALU latency, no
+// LDS round trips): rows of 16 lanes by row_shr 1, 2, 4, 8, then the rows
+// joined by row_bcast15 (rows 1, 3) and row_bcast31 (rows 2, 3)
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_zero(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xf, true);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint64_t dpp_add_u64(uint64_t v) {
+  const uint32_t lo = dpp_zero<CTRL, ROWS>((uint32_t)v), hi = dpp_zero<CTRL, ROWS>((uint32_t)(v >> 32));
+  return v + (((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ uint64_t wave_incl_scan_u64_dpp(uint64_t v) {
+  v = dpp_add_u64<0x111, 0xf>(v);
+  v = dpp_add_u64<0x112, 0xf>(v);
+  v = dpp_add_u64<0x114, 0xf>(v);
+  v = dpp_add_u64<0x118, 0xf>(v);
+  v = dpp_add_u64<0x142, 0xa>(v);
+  v = dpp_add_u64<0x143, 0xc>(v);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_incl_scan_u32_dpp(uint32_t v) {
+  v += dpp_zero<0x111, 0xf>(v);
+  v += dpp_zero<0x112, 0xf>(v);
+  v += dpp_zero<0x114, 0xf>(v);
+  v += dpp_zero<0x118, 0xf>(v);
+  v += dpp_zero<0x142, 0xa>(v);
+  v += dpp_zero<0x143, 0xc>(v);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_sum_u64_dpp(uint64_t v) {
+  const uint64_t s = wave_incl_scan_u64_dpp(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)s, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(s >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32_dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan_u32_dpp(v), 63);
+}
+// max over the 64 lanes (lanes whose DPP source is out of range keep their own value)
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_max(float v) {
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf,
+                                                            false)));
+}
+__device__ __forceinline__ float wave_max_f32_dpp(float v) {
+  v = dpp_max<0x111, 0xf>(v);
+  v = dpp_max<0x112, 0xf>(v);
+  v = dpp_max<0x114, 0xf>(v);
+  v = dpp_max<0x118, 0xf>(v);
+  v = dpp_max<0x142, 0xa>(v);
+  v = dpp_max<0x143, 0xc>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// LDS accesses of one wave complete in issue order; this keeps the compiler
+// from moving them across the point
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// radix_search for one wave: the largest v with S(v) >= thr (S(v) = sum of wt
+// over present elements with key >= v, wt = weight_of(key) or 1); *above =
+// S(v + 1).  Returns false, with no search, when S(0) < thr (S(0) is the
+// total of the first level's histogram).  hist: this wave's two 256-bin
+// buffers, buffer 0 zero on entry and on return.
+template <int EPL, bool WEIGHTED>
+__device__ __forceinline__ bool wave_radix_search(uint32_t* key, int64_t N, int lane, uint64_t thr, uint32_t* value,
+                                                  uint64_t* above, unsigned long long (*hist)[256]) {
+  uint32_t prefix = 0;
+  uint64_t acc = 0;
+#pragma unroll 1
+  for (int level = 0; level < 4; ++level) {
+    // the keys are opaque to the compiler at each level, so the per-element
+    // weights are recomputed where used instead of held across the levels
+    // (2 EPL more registers)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) asm volatile("" : "+v"(key[e]));
+    const int shift = 24 - 8 * level;
+    const uint32_t hmask = level == 0 ? 0u : (0xffffffffu << (shift + 8));
+    unsigned long long* hb = hist[level & 1];
+    unsigned long long* hn = hist[(level + 1) & 1];
+    int64_t lim = N - lane;  // slot e present: 64 e < lim (opaque: no predicate held across loops)
+    asm volatile("" : "+v"(lim));
+    // a lane's weights mostly share a digit (at the first level, all of a
+    // row's weights share one or two exponent bytes): runs of one digit over
+    // a lane's slots are summed in registers and added with one LDS atomic
+    uint32_t run_bin = 0xffffffffu;
+    uint64_t run_w = 0;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const bool hit = 64 * e < lim && (key[e] & hmask) == prefix;
+      const uint32_t b = hit ? (key[e] >> shift) & 255u : run_bin;
+      if (b != run_bin) {
+        if (run_bin != 0xffffffffu) atomicAdd(&hb[run_bin], (unsigned long long)run_w);
+        run_bin = b;
+        run_w = 0;
+      }
+      run_w += hit ? (WEIGHTED ? weight_of_nb(key[e]) : 1ull) : 0ull;
+    }
+    if (run_bin != 0xffffffffu) atomicAdd(&hb[run_bin], (unsigned long long)run_w);
+    wave_lds_order();
+    // lane l takes digits 255 - 4 l - i: inclusive sums over the descending
+    // digits; the first t = 4 l + i with acc + incl >= thr is d* = 255 - t
+    uint64_t h[4], p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = hb[255 - 4 * lane - i];
+    p[0] = h[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) p[i] = p[i - 1] + h[i];
+    const uint64_t incl = wave_incl_scan_u64_dpp(p[3]);
+    const uint64_t base = incl - p[3];
+    if (level == 0) {
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)incl, 63);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(incl >> 32), 63);
+      if ((((uint64_t)hi << 32) | lo) < thr) {  // S(0) < thr: no crossing
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hb[4 * lane + i] = 0ull;
+        wave_lds_order();
+        return false;
+      }
+    }
+    uint32_t below = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) below += acc + base + p[i] >= thr ? 0u : 1u;
+    const int tstar = (int)min(wave_sum_u32_dpp(below), 255u);
+    const int slot = tstar & 3;
+    const uint64_t mine = base + (slot == 0 ? 0ull : slot == 1 ? p[0] : slot == 2 ? p[1] : p[2]);
+    acc += readlane_u64(mine, tstar >> 2);  // weight of the digits above d*
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hn[4 * lane + i] = 0ull;
+    wave_lds_order();
+    prefix |= (255u - (uint32_t)tstar) << shift;
+  }
+  *above = acc;
+  *value = prefix;
+  return true;
+}
+
+template <int EPL>
+__global__ __launch_bounds__(64 * kWaveRows) void select_rows_kernel(SelArgs a) {
+  static_assert(64 * EPL <= kWaveMaxN, "row too wide for the wave kernel");
+  __shared__ int32_t flags[kWaveMaxN];
+  __shared__ unsigned long long hist_all[kWaveRows][2][256];
+  __shared__ uint64_t selm_all[kWaveRows][kWaveMaxN / 64];
+  // the wave index in a scalar register: the row and its score pointer are
+  // then scalar, and the score loads take a scalar base + 32-bit lane offset
+  // (a 64-bit address per load and slot otherwise: 2 EPL registers)
+  const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t N = a.N;
+  for (int64_t j = tid; j < N; j += 64 * kWaveRows) flags[j] = block_tile_flags(a.block_first_tile, a.tile_count, j);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hist_all[wid][0][4 * lane + i] = 0ull;
+  __syncthreads();
+  const int64_t row = (int64_t)blockIdx.x * kWaveRows + wid;
+  if (row >= a.rows) return;  // wave-uniform; no barrier follows
+  unsigned long long(*hist)[256] = hist_all[wid];
+  const float* s = a.scores + row * N;
+  const float NINF = -__uint_as_float(0x7f800000u);
+
+  uint32_t key[EPL];
+  int64_t eff = 0;
+  uint32_t v_e = 0;
+  uint64_t need = 0;
+  // slot e of this lane is present iff 64 e < lim; lim is made opaque in
+  // each loop, so the compiler does not keep EPL predicate masks across loops
+  int64_t lim = N - lane;
+  if (a.mode == 0) {
+    asm volatile("" : "+v"(lim));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      // unconditional loads (absent slots read the row's last score): the
+      // loads of all slots are in flight together, not one branch each
+      const uint32_t u = __float_as_uint(s[min(64 * e + lane, (int)N - 1)]);
+      key[e] = 64 * e < lim ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
+    }
+    eff = a.k_lo < N ? a.k_lo : N;
+  } else {
+    float x[EPL];
+    float m = NINF;
+    asm volatile("" : "+v"(lim));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const float v = s[min(64 * e + lane, (int)N - 1)] * a.scale;  // unconditional load, as above
+      x[e] = 64 * e < lim ? v : NINF;
+      m = fmaxf(m, x[e]);
+    }
+    m = wave_max_f32_dpp(m);
+    if (m == NINF) {
+      eff = 0;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) key[e] = 0;
+    } else {
+      // (the running sums are opaque at each step: integer adds would
+      // otherwise be reassociated into a tree over all EPL terms at once, 2 EPL
+      // registers more)
+      uint64_t E = 0;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        x[e] = canon_exp_nb(x[e] - m);  // absent slots hold -inf: 0
+        E += fixp_nb(x[e], 40);
+        asm volatile("" : "+v"(E));
+      }
+      E = wave_sum_u64_dpp(E);
+      const float sum = (float)E * 9.094947017729282e-13f;  // 2^-40
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        key[e] = __float_as_uint(x[e] / sum);  // absent slots: 0 / sum = 0
+        asm volatile("" : "+v"(key[e]));       // one division at a time (their temporaries otherwise pile up)
+      }
+      int64_t c = a.ub;
+      bool crossed = false;
+      uint32_t vc = 0;
+      uint64_t jt = 0;
+      uint64_t A;
+      // crossing value vc: G(vc) >= thr > G(vc + 1) = A (none when G(0) < thr)
+      if (wave_radix_search<EPL, true>(key, N, lane, a.thr, &vc, &A, hist)) {
+        uint32_t ngt = 0;
+        asm volatile("" : "+v"(lim));
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) ngt += (64 * e < lim && key[e] > vc) ? 1u : 0u;
+        ngt = wave_sum_u32_dpp(ngt);
+        const uint64_t Wv = fixp(__uint_as_float(vc), 60);
+        jt = (a.thr - A - 1) / Wv;  // smallest j with A + (j+1) Wv >= thr
+        const int64_t k = (int64_t)ngt + (int64_t)jt;
+        if (k < a.ub) { c = k; crossed = true; }
+      }
+      int64_t n = c + 1;
+      if (n < a.k_lo) n = a.k_lo;
+      if (n > N) n = N;
+      eff = n < a.ub ? n : a.ub;
+      if (crossed && eff == c + 1) {
+        v_e = vc;
+        need = jt + 1;
+        eff = -eff;  // marks "v_e already known"
+      }
+    }
+  }
+  if (eff > 0) {  // count search: largest v with #(key >= v) >= eff
+    uint64_t above;
+    (void)wave_radix_search<EPL, false>(key, N, lane, (uint64_t)eff, &v_e, &above, hist);  // (eff <= the count)
+    need = (uint64_t)eff - above;
+  } else {
+    eff = -eff;
+  }
+
+  // emit in ascending block order.  Pass 1 (unrolled over the keys): rank
+  // the ties and record each slot's selection as a ballot in LDS.  Pass 2 (a
+  // plain loop, no key access): place the tiles and blocks slot by slot from
+  // the ballots and the tile flags.
+  const uint64_t lt = (1ull << lane) - 1ull;
+  uint64_t* selm = selm_all[wid];
+  {
+    int64_t lim = eff > 0 ? N - lane : 0;  // slot e present: 64 e < lim
+    asm volatile("" : "+v"(lim));
+    uint64_t ties_before = 0;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const bool pres = 64 * e < lim;
+      const bool tie = pres && key[e] == v_e;
+      const uint64_t tb = __builtin_amdgcn_ballot_w64(tie);
+      const uint64_t rank = ties_before + (uint64_t)__popcll(tb & lt);
+      ties_before += (uint64_t)__popcll(tb);
+      // every lane stores the same value (no branch per slot)
+      selm[e] = __builtin_amdgcn_ballot_w64(pres && (key[e] > v_e || (tie && rank < need)));
+    }
+  }
+  wave_lds_order();
+  int32_t* trow = a.tiles + row * a.tcap;
+  int32_t* brow = a.sel_blocks ? a.sel_blocks + row * a.bcap : nullptr;
+  uint64_t tiles_before = 0, blocks_before = 0;
+  const int nslots = (int)((N + 63) >> 6);
+#pragma unroll 4
+  for (int e = 0; e < nslots; ++e) {
+    const uint64_t bs = selm[e];
+    if (bs == 0) continue;
+    const int64_t j = 64 * e + lane;
+    const bool sel = (bs >> lane) & 1ull;
+    const int32_t f = sel ? flags[j] : 0;
+    const bool big = sel && (f & kBigBlock);
+    const bool ok0 = f & 1, ok1 = f & 2;  // (neither for a block of more than two tiles)
+    const uint64_t b0 = __builtin_amdgcn_ballot_w64(ok0), b1 = __builtin_amdgcn_ballot_w64(ok1);
+    if (__builtin_amdgcn_ballot_w64(big) == 0) {
+      const int64_t p = (int64_t)(tiles_before + __popcll(b0 & lt) + __popcll(b1 & lt));
+      const int32_t t0 = f >> 3;
+      if (ok0 && p < a.tcap) trow[p] = t0;
+      if (ok1 && p + (ok0 ? 1 : 0) < a.tcap) trow[p + (ok0 ? 1 : 0)] = t0 + 1;
+      tiles_before += (uint64_t)(__popcll(b0) + __popcll(b1));
+    } else {
+      // a block of more than two tiles in this slot: counts by loop, one scan
+      int32_t t0 = 0, t1 = 0;
+      uint32_t cnt = (ok0 ? 1u : 0u) + (ok1 ? 1u : 0u);
+      if (big) {
+        t0 = a.block_first_tile[j];
+        t1 = a.block_first_tile[j + 1];
+        for (int32_t t = t0; t < t1; ++t) cnt += (a.tile_count == nullptr || a.tile_count[t] > 0) ? 1u : 0u;
+      }
+      const uint32_t incl = wave_incl_scan_u32(cnt, lane);
+      int64_t p = (int64_t)tiles_before + (int64_t)(incl - cnt);
+      if (big) {
+        for (int32_t t = t0; t < t1; ++t)
+          if (a.tile_count == nullptr || a.tile_count[t] > 0) {
+            if (p < a.tcap) trow[p] = t;
+            ++p;
+          }
+      } else {
+        if (ok0) { if (p < a.tcap) trow[p] = f >> 3; ++p; }
+        if (ok1 && p < a.tcap) trow[p] = (f >> 3) + 1;
+      }
+      tiles_before += (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    }
+    if (brow && sel) {
+      const int64_t q = (int64_t)(blocks_before + __popcll(bs & lt));
+      if (q < a.bcap) brow[q] = (int32_t)j;
+    }
+    blocks_before += (uint64_t)__popcll(bs);
+  }
+  if (lane == 0) {
+    a.ntiles[row] = (int32_t)tiles_before;
+    if (a.nsel) a.nsel[row] = (int32_t)blocks_before;
+  }
+}
+
 // ------------------------------------------------------------ wide rows
 // Rows of more than 64 kSelThreads blocks: one 1024-thread workgroup per row;
 // element j is taken by thread j mod 1024 in pass j / 1024 (coalesced reads),
@@ -877,12 +1267,18 @@ int prism_select_tiles(const float* scores, int64_t rows, int64_t N, int mode, i
   a.block_first_tile = block_first_tile; a.tile_count = tile_count; a.tcap = tcap; a.tiles = tiles;
   a.ntiles = ntiles; a.sel_blocks = sel_blocks; a.bcap = bcap; a.nsel = nsel;
   const int64_t need = (N + kSelThreads - 1) / kSelThreads;
-  // rows of up to 64 kSelThreads blocks in registers, wider rows pass by
-  // pass (both place tiles and blocks with 32-bit scan fields)
-  if (need > 64) select_wide_kernel<<<(unsigned)rows, kWideThreads, 0, stream>>>(a);
-  else if (need <= 8) select_kernel<8><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
-  else if (need <= 16) select_kernel<16><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
-  else if (need <= 24) select_kernel<24><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
+  const unsigned wave_grid = (unsigned)((rows + kWaveRows - 1) / kWaveRows);
+  // rows of up to 6,144 blocks: one wave per row; up to 16,384: one
+  // 256-thread workgroup per row, in registers; wider rows pass by pass (all
+  // place tiles and blocks with 32-bit fields)
+  if (N <= 1024) select_rows_kernel<16><<<wave_grid, 64 * kWaveRows, 0, stream>>>(a);
+  else if (N <= 2048) select_rows_kernel<32><<<wave_grid, 64 * kWaveRows, 0, stream>>>(a);
+  else if (N <= 3072) select_rows_kernel<48><<<wave_grid, 64 * kWaveRows, 0, stream>>>(a);
+  else if (N <= 4096) select_rows_kernel<64><<<wave_grid, 64 * kWaveRows, 0, stream>>>(a);
+  else if (N <= 5120) select_rows_kernel<80><<<wave_grid, 64 * kWaveRows, 0, stream>>>(a);
+  else if (N <= 5632) select_rows_kernel<88><<<wave_grid, 64 * kWaveRows, 0, stream>>>(a);
+  else if (N <= kWaveMaxN) select_rows_kernel<96><<<wave_grid, 64 * kWaveRows, 0, stream>>>(a);
+  else if (need > 64) select_wide_kernel<<<(unsigned)rows, kWideThreads, 0, stream>>>(a);
   else if (need <= 32) select_kernel<32><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   else select_kernel<64><<<(unsigned)rows, kSelThreads, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_select_tiles");

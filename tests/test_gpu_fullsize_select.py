@@ -32,6 +32,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
+from oracle.torch_path import selection_agreement
 from tests.test_gpu_fullsize import _attention, _list_structure, _selection_rows, _tol, say
 
 pytestmark = pytest.mark.gpu
@@ -121,41 +122,6 @@ def test_zone_stats_and_shapes_fullsize_vs_oracle(cfg):
         "< 1e-5:", int((~decided).sum()))
 
 
-def _torch_reference_rows(scores: torch.Tensor, sparsity, p, sm: float):
-    """The reference's selection (bsa_interface.py:235-304) as the same torch
-    op sequence in float32 on the device that holds `scores` (the GPU, or the
-    host for torch's CPU kernels).  scores: [R, N].  Returns the selected
-    sets as a [R, N] bool mask, the decision margin |exact cumsum - p| at the
-    crossing (inf for top-k rows) and the boundary-tie flags."""
-    R, N = scores.shape
-    dev = scores.device
-    if p is None:
-        k = int((1 - sparsity) * N)
-        _, idx = torch.topk(scores, k, dim=-1)
-        mask = torch.zeros((R, N), dtype=torch.bool, device=dev).scatter_(1, idx, True)
-        srt = torch.sort(scores, dim=-1, descending=True).values
-        tie = (srt[:, k - 1] == srt[:, k]) if k < N else torch.zeros(R, dtype=torch.bool, device=dev)
-        return mask, torch.full((R,), float("inf"), device=dev, dtype=torch.float64), tie
-    w = torch.softmax(scores * sm, dim=-1)
-    lo = 1 if sparsity is None else max(1, int((1 - sparsity) * N))
-    ub = min(N, max(lo, int(p * N) + 1))
-    vals, idx = torch.topk(w, k=ub, dim=-1, largest=True, sorted=True)
-    cdf = torch.cumsum(vals, dim=-1)
-    n = ((cdf < p).to(torch.int32).sum(dim=-1, keepdim=True) + 1).clamp(min=lo, max=N)
-    pos = torch.arange(ub, device=dev)
-    idx = idx.masked_fill(pos >= n, N)
-    mask = torch.zeros((R, N + 1), dtype=torch.bool, device=dev).scatter_(1, idx, True)[:, :N]
-    c = (cdf < p).to(torch.int64).sum(dim=-1)
-    cdf64 = torch.cumsum(vals.double(), dim=-1)
-    near = torch.stack([(cdf64.gather(1, (c - d).clamp(0, ub - 1)[:, None])[:, 0] - p).abs() for d in (0, 1)])
-    margin = near.min(dim=0).values
-    e = torch.clamp(n.squeeze(-1), max=ub).long()
-    srt = torch.sort(w, dim=-1, descending=True).values
-    nxt = torch.clamp(e, max=N - 1)
-    tie = (e < N) & (srt.gather(1, (e - 1)[:, None])[:, 0] == srt.gather(1, nxt[:, None])[:, 0])
-    return mask, margin, tie
-
-
 # How far from p a row's exact cumulative sum may lie when torch's float32
 # sequence and the exact fixed-point rule decide it differently.  torch's
 # cumsum adds c float32 weights (c < 1,000 at the crossing of every config
@@ -223,28 +189,9 @@ def test_selection_vs_reference_torch_sequence_fullsize(case):
         scores = plan.scores.view(-1, N_b)
         ours = ops.select_tiles(scores, sp, cdf, sm, plan.lay.block_first_tile, plan.tile_count, want_blocks=True)
     R = scores.shape[0]
-    width = ours["sel_blocks"].shape[1]
-    counts = {"gpu": [0, 0, 0.0], "cpu": [0, 0, 0.0]}  # rows differing, of them tied, largest untied margin
-    chunk = 2048
-    for r0 in range(0, R, chunk):
-        s = scores[r0:r0 + chunk]
-        sel = ours["sel_blocks"][r0:r0 + chunk].long()
-        live = torch.arange(width, device=DEV)[None, :] < ours["nsel"][r0:r0 + chunk, None]
-        sel = torch.where(live, sel, torch.full_like(sel, N_b))
-        mine = torch.zeros((len(s), N_b + 1), dtype=torch.bool, device=DEV).scatter_(1, sel, True)[:, :N_b]
-        ref_gpu = _torch_reference_rows(s, sp, cdf, sm)
-        ref_cpu = _torch_reference_rows(s.cpu(), sp, cdf, sm)
-        margin, tie = ref_gpu[1], ref_gpu[2] | ref_cpu[2].to(DEV)
-        for name, ref_mask in (("gpu", ref_gpu[0]), ("cpu", ref_cpu[0].to(DEV))):
-            diff = (mine != ref_mask).any(dim=1)
-            if bool(diff.any()):
-                dm, dt = margin[diff], tie[diff]
-                counts[name][0] += int(diff.sum())
-                counts[name][1] += int(dt.sum())
-                untied = dm[~dt]
-                if untied.numel():
-                    counts[name][2] = max(counts[name][2], float(untied.max()))
-    for name, (n_diff, n_tie, worst) in counts.items():
+    counts = selection_agreement(scores, ours["sel_blocks"], ours["nsel"], sp, cdf, sm)
+    for name, c in counts.items():
+        n_diff, n_tie, worst = c["rows_differing"], c["of_them_tied"], c["max_untied_margin"]
         say("torch sequence:", case, name, "rows", R, "N_b", N_b, "rows whose set differs", n_diff,
             f"({n_diff / R:.2e})", "of them with a boundary tie", n_tie, "largest |cdf - p| of an untied differing row",
             worst)

@@ -189,8 +189,9 @@ def _random_scores(rng, rows, N, kind):
 def test_select_bitexact(kind):
     from prism_amd import ops
     rng = np.random.default_rng(11)
-    # 8, 16 and 32 elements per thread of the workgroup that takes a row
-    for N in (37, 300, 1440, 2900, 6500):
+    # one wave per row (16 to 96 elements per lane, full and partial last
+    # slots), then one workgroup per row (6,145 to 16,384 blocks)
+    for N in (37, 300, 1024, 1440, 2900, 4097, 5328, 6144, 6145, 6500):
         rows = 24
         s = _random_scores(rng, rows, N, kind)
         first = np.arange(N + 1, dtype=np.int32)
@@ -205,7 +206,7 @@ def test_select_bitexact(kind):
                 assert np.array_equal(got[r, : n[r]], ref_sel[r, : n[r]]), (kind, N, sp, p, r)
 
 
-@pytest.mark.parametrize("N", [300, 5000, 6500])
+@pytest.mark.parametrize("N", [300, 5000, 6144, 6500])
 def test_select_tile_expansion_any_tile_count(N):
     """Blocks of 0..4 tiles (the C-ABI takes any block_first_tile) with padded
     tiles dropped: each row's list is the tiles of its selected blocks, in

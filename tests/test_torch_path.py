@@ -81,3 +81,28 @@ def test_selection_and_attention_match_oracle():
     for name, got, want in (("O", out, o_ref), ("dQ", dq, grads[0]), ("dK", dk, grads[1]), ("dV", dv, grads[2])):
         g = got.numpy().reshape(B * H, S, D)[:, src]
         assert np.abs(g - want).max() < 1e-4, name
+
+
+def test_selection_agreement_counts_only_rounding_differences():
+    """The checker the GPU tests and the benchmark use (selection_agreement):
+    against the C oracle's selection of the same scores it finds no untied
+    row decided away from p, and it counts every row of a planted mistake
+    (the oracle run at p = 0.8 against the sequence at p = 0.9)."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    from oracle.torch_path import selection_agreement
+    rng = np.random.default_rng(4)
+    R, N = 96, 700
+    s = (rng.standard_normal((R, N)) * 3).astype(np.float32)
+    sp = 1 - 20.5 / N
+    for p_ours, planted in ((0.9, False), (0.8, True)):
+        sel, nsel = O.select(s, sp, p_ours, 0.125)
+        sel_t = torch.from_numpy(np.where(sel < 0, 0, sel))
+        out = selection_agreement(torch.from_numpy(s), sel_t, torch.from_numpy(nsel), sp, 0.9, 0.125)
+        for c in out.values():
+            if planted:
+                assert c["rows_differing"] - c["of_them_tied"] >= R // 2
+            else:
+                assert c["max_untied_margin"] <= 4e-6, c
+                assert c["rows_differing"] - c["of_them_tied"] <= R // 20, c
