@@ -406,7 +406,8 @@ def measured_ceilings():
                  wave on register operands, two waves per SIMD on every CU,
                  ~0.25 s per launch (no memory traffic): the MFMA rate at the
                  clock the chip holds under full matrix load; best of 3;
-      gemm       torch.matmul bf16 8192^3 (hipBLASLt), median of 20;
+      gemm       torch.matmul bf16 8192^3 and F.linear at the A2V bridge shape
+                 (302,400 x 5,120 x 5,120) (hipBLASLt), median of 20 and of 5;
       copy       prism_copy_peak over 4 GiB (read + write bytes), best of 10."""
     import ctypes
     import statistics
@@ -447,6 +448,11 @@ def measured_ceilings():
     timed(lambda: torch.matmul(a, b), 3)
     g_ms = statistics.median(timed(lambda: torch.matmul(a, b), 20))
     del a, b
+    x = torch.randn(302400, 5120, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(5120, 5120, device="cuda", dtype=torch.bfloat16)
+    timed(lambda: torch.nn.functional.linear(x, w), 2)
+    l_ms = statistics.median(timed(lambda: torch.nn.functional.linear(x, w), 5))
+    del x, w
     nbytes = 4 << 30
     src = torch.ones(nbytes // 4, device="cuda", dtype=torch.float32)
     dst = torch.empty_like(src)
@@ -462,7 +468,10 @@ def measured_ceilings():
         "mfma_loop_tflops": round(mfma_tflops, 1), "mfma_loop_ms": round(mfma_ms, 1),
         "mfma_loop_clock_ghz": round(clk, 3),
         "mfma_loop_issue_clock_ghz": round(mfma_tflops * 1e12 / (cus * MFMA_FLOPS_PER_CU_CYCLE) / 1e9, 3),
-        "gemm_tflops": round(2 * 8192 ** 3 / (g_ms * 1e-3) / 1e12, 1), "gemm": "torch.matmul bf16 8192^3 (hipBLASLt)",
+        "gemm_tflops": round(max(2 * 8192 ** 3 / (g_ms * 1e-3), 2 * 302400 * 5120 * 5120 / (l_ms * 1e-3)) / 1e12, 1),
+        "gemm_8192_tflops": round(2 * 8192 ** 3 / (g_ms * 1e-3) / 1e12, 1),
+        "gemm_bridge_tflops": round(2 * 302400 * 5120 * 5120 / (l_ms * 1e-3) / 1e12, 1),
+        "gemm": "hipBLASLt bf16 (torch.matmul 8192^3, F.linear 302400x5120x5120): the faster of the two",
         "copy_GBps": round(2 * nbytes / (c_ms * 1e-3) / 1e9, 1), "copy": "prism_copy_peak, 4 GiB read + 4 GiB written",
         "cus": cus,
     }
@@ -483,9 +492,9 @@ def main():
     ap.add_argument("--bridge", action="store_true",
                     help="the a2v bridge o-projection with fused residual norms (prism_linear_rownorm) at the "
                          "config's tokens and C, against torch F.linear + the norm kernel (one JSON line)")
-    ap.add_argument("--compact-lists", action="store_true",
-                    help="keep the work lists in compact CSR form (bsa_params compact_lists); reported in config, "
-                         "not the default headline")
+    ap.add_argument("--dense-lists", action="store_true",
+                    help="keep the pair unions as dense pairs x Nt buffers until the backward (bsa_params "
+                         "compact_lists=False) instead of compact CSR; reported in config")
     ap.add_argument("--forward-only", action="store_true",
                     help="time the forward alone (inference, no autograd), as BASELINE config 2 is quoted; one JSON "
                          "line of its own, not the headline")
@@ -543,7 +552,8 @@ def main():
         sparsity, cdf = inp["sp_only"], None
     else:
         sparsity, cdf = 1.0 - (inp["topk"] + 0.5) / N_b, inp["cdf"]
-    dyn.bsa_params.update({"sparsity": sparsity, "cdf_threshold": cdf, "compact_lists": bool(args.compact_lists)})
+    compact = not args.dense_lists
+    dyn.bsa_params.update({"sparsity": sparsity, "cdf_threshold": cdf, "compact_lists": compact})
     log(f"[bench] N_b={N_b} sparsity={sparsity:.6f} cdf={cdf}")
 
     fwd_only = bool(args.forward_only)
@@ -590,19 +600,18 @@ def main():
     with torch.no_grad():
         plan = plan_dynamic(q.detach(), k.detach(), v.detach(), gp, method="ivpq", sparsity=sparsity,
                             cdf_threshold=cdf, audio_token_norms=norms0, input_grid=grid,
-                            compact_lists=bool(args.compact_lists), keep_scores=True)
+                            compact_lists=compact, keep_scores=True)
         plan.build_key_lists()
-    # bytes of the work lists a step keeps until its backward (per-query-tile
-    # lists and their pair unions, per-key-tile lists and theirs)
-    list_bytes = sum(t.numel() * t.element_size() for t in (plan.qcols, plan.qunion[2], plan.klists[2],
-                                                            plan.kunion[2]))
+    # bytes of work lists at their peak (all lists of the call) and those the
+    # step keeps from its forward to its backward (the two pair unions, after
+    # the forward's settle(), as _DynBSA.forward does)
+    list_bytes_peak = plan.list_bytes()
     sum_lens = plan.sum_lens()
     Nt, Nb, Sp = plan.lay.Nt, plan.lay.N_b, plan.S
     density = sum_lens / (B * H * Nt * Nt)
     n_qvalid = int((plan.tile_count > 0).sum().item()) if plan.tile_count is not None else Nt
     density_valid = sum_lens / (B * H * n_qvalid * Nt)  # over query tiles holding a valid token
-    # fraction of (wave, key tile) slots of the paired-tile kernels that do math
-    union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
+    # fraction of (wave, key tile) slots of the paired-tile kernels that do math (union_eff, below)
     fl = 64 * 64 * D * sum_lens  # one 64x64xD product over all kept tile pairs
     kept_flops = (4 if fwd_only else 14) * fl  # FA convention: fwd 4, bwd 10
 
@@ -612,6 +621,10 @@ def main():
     X = B * H * Sp * D * 2   # one bf16 [B,H,S_p,D] tile-order tensor (zone grid)
     Xin = B * H * S * D * 2  # one bf16 [B,H,S,D] THW tensor (input grid)
     nnz_tiles = int(plan.sel["ntiles"].sum().item())
+    union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
+    with torch.no_grad():
+        plan.settle()
+    list_bytes = plan.list_bytes()
     hbm = {  # algorithmic bytes per launch (average over the step's launches of that entry point)
         "prism_zone_stats": H * S * D * 2 + plan.lay.Nz * 25 * D * 4,
         "prism_a2v_norms": S * inp["res"].shape[-1] * 2 + S * 2,
@@ -707,7 +720,7 @@ def main():
                    "density_valid_q": round(density_valid, 4), "pair_union_efficiency": round(union_eff, 4),
                    "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3),
                    "ms_per_step_median": round(ms_median, 3),
-                   "compact_lists": bool(args.compact_lists), "list_bytes": list_bytes,
+                   "compact_lists": compact, "list_bytes": list_bytes, "list_bytes_peak": list_bytes_peak,
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                    "selection_vs_reference_torch": sel_agree},

@@ -165,6 +165,14 @@ def _register_fakes():
         nnz = torch.library.get_ctx().new_dynamic_size()
         return _empty(start, (start.numel() + 1,), i32), _empty(start, (nnz,), i32)
 
+    @reg("prism::lists_csr_offsets")
+    def _(length):
+        return _empty(length, (length.numel() + 1,), i32), _empty(length, (1,), i64)
+
+    @reg("prism::lists_csr_fill")
+    def _(start, length, cols, offsets, nnz):
+        return _empty(start, (nnz,), i32)
+
     @reg("prism::tile_masks")
     def _(valid):
         return _empty(valid, (valid.numel() // 64,), i64)

@@ -78,8 +78,9 @@ class DynamicBlockSparseAttention:
     """State the reference keeps on SelfAttention for the dynamic path: the
     bsa_params dict, the method switch and the per-pass shape cache
     (wan_video_dit.py:22-33, :401-427).  One key beyond the reference's:
-    bsa_params["compact_lists"] = True keeps the work lists in compact CSR
-    form until the backward (O(nnz) memory; identical results)."""
+    bsa_params["compact_lists"] (default True) keeps the work lists in
+    compact CSR form until the backward (O(nnz) memory; identical results;
+    False: dense buffers)."""
 
     def __init__(self, method: str = "ivpq", bsa_params: Optional[dict] = None):
         if method not in ("ivpq", "penalty"):
@@ -120,7 +121,7 @@ class DynamicBlockSparseAttention:
             lambda_a=p.get("dynamic_block_lambda_a", 0.5), tau_128=p.get("dynamic_block_tau_128", 0.15),
             lambda_128=p.get("dynamic_block_lambda_128", 1.0), shape_ids=cached, return_shape_ids=True,
             input_grid=(T, H, W), compute_padded_queries=False,  # padded rows are sliced away (:429-431)
-            compact_lists=bool(p.get("compact_lists", False)))
+            compact_lists=bool(p.get("compact_lists", True)))
         if self.training:
             self._dyn_shape_cache = (self.pass_id, grid_padded, used)
         return out
@@ -154,5 +155,5 @@ def run_bsa_uniform(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid_size
     lk = ops.ChunkLayout((T, H, W), ck, q.device, pgrid=pgrid)
     return bsa_chunked(q, k, v, lq, lk, sparsity=kw.get("sparsity", 0.875), cdf_threshold=kw.get("cdf_threshold"),
                        sm_scale=1.0 / (D ** 0.5), compute_padded_queries=compute_padded_queries,
-                       compact_lists=bool(kw.get("compact_lists", False)))
+                       compact_lists=bool(kw.get("compact_lists", True)))
 

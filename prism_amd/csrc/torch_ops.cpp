@@ -462,6 +462,39 @@ std::tuple<Tensor, Tensor> lists_to_csr(const Tensor& s_, const Tensor& l_, cons
   return {offsets, out};
 }
 
+// the two halves of lists_to_csr, for callers that batch the host read of
+// several lists' nnz: offsets [rows + 1] and the total [1] stay on the device
+std::tuple<Tensor, Tensor> lists_csr_offsets(const Tensor& l_) {
+  on_gpu(l_, "len");
+  check_dtype(l_, at::kInt, "len");
+  const c10::DeviceGuard guard(l_.device());
+  const Tensor l = l_.contiguous();
+  const int64_t rows = l.numel();
+  Tensor offsets = at::empty({rows + 1}, opts(l, at::kInt));
+  Tensor total = at::empty({1}, opts(l, at::kLong));
+  PRISM_TORCH_CALL(prism_lists_csr_offsets, l.data_ptr<int32_t>(), rows, offsets.data_ptr<int32_t>(),
+                   total.data_ptr<int64_t>(), stream_of(l));
+  return {offsets, total};
+}
+
+// entries [nnz] of (start, len, cols) at the offsets of lists_csr_offsets;
+// nnz is that call's total (read by the caller)
+Tensor lists_csr_fill(const Tensor& s_, const Tensor& l_, const Tensor& c_, const Tensor& offsets_, int64_t nnz) {
+  check_lists(s_, l_, c_);
+  on_gpu(offsets_, "offsets");
+  check_dtype(offsets_, at::kInt, "offsets");
+  TORCH_CHECK_VALUE(s_.numel() == l_.numel() && offsets_.numel() == l_.numel() + 1,
+                    "prism.lists_csr_fill: start, len and offsets disagree in length");
+  TORCH_CHECK_VALUE(nnz >= 0 && nnz <= 2147483647ll, "prism.lists_csr_fill: nnz out of range (int32 offsets)");
+  const c10::DeviceGuard guard(s_.device());
+  const Tensor s = s_.contiguous(), l = l_.contiguous(), c = c_.contiguous(), offsets = offsets_.contiguous();
+  Tensor out = at::empty({nnz}, opts(s, at::kInt));
+  if (nnz > 0)
+    PRISM_TORCH_CALL(prism_lists_csr_fill, s.data_ptr<int64_t>(), l.data_ptr<int32_t>(), c.data_ptr<int32_t>(),
+                     s.numel(), offsets.data_ptr<int32_t>(), out.data_ptr<int32_t>(), stream_of(s));
+  return out;
+}
+
 Tensor pair_order(const Tensor& ulen_, int64_t group, int64_t tail) {
   on_gpu(ulen_, "ulen");
   check_dtype(ulen_, at::kInt, "ulen");
@@ -644,6 +677,8 @@ TORCH_LIBRARY(prism, m) {
         "Tensor? tile_masks) -> (Tensor, Tensor, Tensor)");
   m.def("pair_order(Tensor ulen, int group, int tail) -> Tensor");
   m.def("lists_to_csr(Tensor start, Tensor len, Tensor cols) -> (Tensor, Tensor)");
+  m.def("lists_csr_offsets(Tensor len) -> (Tensor, Tensor)");
+  m.def("lists_csr_fill(Tensor start, Tensor len, Tensor cols, Tensor offsets, int nnz) -> Tensor");
   m.def("tile_masks(Tensor valid) -> Tensor");
   m.def("lse_to_m2(Tensor lse) -> Tensor");
   m.def("bsa_fwd(Tensor q, Tensor k, Tensor v, Tensor? tile_masks, Tensor ustart, Tensor ulen, Tensor ucols, "
@@ -678,6 +713,8 @@ TORCH_LIBRARY_IMPL(prism, CUDA, m) {
   m.impl("pair_union", &pair_union);
   m.impl("pair_order", &pair_order);
   m.impl("lists_to_csr", &lists_to_csr);
+  m.impl("lists_csr_offsets", &lists_csr_offsets);
+  m.impl("lists_csr_fill", &lists_csr_fill);
   m.impl("tile_masks", &tile_masks);
   m.impl("lse_to_m2", &lse_to_m2);
   m.impl("bsa_fwd", &bsa_fwd);

@@ -80,22 +80,21 @@ class _Plan:
         self.qstart, self.qlen = ops.tile_rows(sel["ntiles"], lay.block_id_of_tile, B * H, lay.Nt, lay.N_b,
                                                sel["tcap"], self.tile_count if skip else None)
         self.qcols = sel["tiles"].view(-1)
-        # compact lists: every list the plan keeps (per query tile, pair
-        # unions, and in the backward per key tile and its unions) in CSR
-        # form, O(nnz) memory instead of rows x capacity (one host read of
-        # nnz each); same entries in the same order, so identical results
+        # compact lists: the two pair unions the backward keeps are stored as
+        # CSR, O(nnz) memory instead of pairs x Nt (settle(); one host read of
+        # both nnz, made while the forward kernel runs); same entries in the
+        # same order, so identical results
         self.compact = compact_lists
-        if compact_lists:
-            self.qstart, self.qlen, self.qcols = self._compact(self.qstart, self.qlen, self.qcols)
-            self.sel = {key: val for key, val in sel.items() if key != "tiles"}
+        self._settled = False
         # pair unions of the per-query-tile key lists (forward, dQ) and the key
         # validity words of padded key tiles
         self.tmasks = ops.tile_masks(self.kv_valid) if masked else None
         # pair the query tiles of each zone by list overlap (fewest idle wave slots)
         self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lay.Nt)
         self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks, pairmap=self.qpair)
+        self._csr = ops.DeferredCompaction(2) if compact_lists else None
         if compact_lists:
-            self.qunion = self._compact(*self.qunion)
+            self._csr.add(0, self.qunion)
         # launch order of the forward and dQ kernels (the last workgroups ids
         # take the longest lists first: the launch does not end on a long one)
         self.qorder = ops.pair_order(self.qunion[1], 64)
@@ -105,20 +104,15 @@ class _Plan:
         self.korder = None
         self.keys_ready = None  # event of a key-list build on the side stream
 
-    @staticmethod
-    def _compact(start, length, cols):
-        offsets, entries = ops.lists_to_csr(start, length, cols)
-        return (*ops.csr_lists(offsets), entries)
-
     def build_key_lists_side(self):
         """build_key_lists on the side stream, after the work queued so far on
-        the current stream (compact lists read nnz on the host, so they are
-        built in place on first use instead)."""
-        if self.kunion is not None or self.compact:
+        the current stream."""
+        if self.kunion is not None:
             return
         _, self.keys_ready = ops.side_launch(
             self.qcols.device, self.build_key_lists, reads=(self.qstart, self.qlen, self.qcols),
-            produces=lambda _: (*self.klists, self.kpair, *self.kunion, self.korder))
+            produces=lambda _: (*self.klists, self.kpair, *self.kunion, self.korder,
+                                self._csr.offsets[1] if self._csr is not None else None))
 
     def join_side(self):
         """Make the current stream wait for a side-stream key-list build (the
@@ -136,13 +130,38 @@ class _Plan:
             return
         Nt = self.lay.Nt
         self.klists = ops.transpose_lists(self.qstart, self.qlen, self.qcols, self.B * self.H, Nt)
-        if self.compact:
-            self.klists = self._compact(*self.klists)
         self.kpair = ops.pair_tiles(*self.klists, Nt)
         self.kunion = ops.pair_union(*self.klists, Nt, pairmap=self.kpair)
-        if self.compact:
-            self.kunion = self._compact(*self.kunion)
         self.korder = ops.pair_order(self.kunion[1], 32)
+        if self._csr is not None:
+            self._csr.add(1, self.kunion)
+
+    def settle(self):
+        """Keep only what the backward reads: the query-side and key-side pair
+        unions (compact CSR when the plan is compact, with one batched host
+        read of their nnz), pairings and launch orders.  The per-tile lists
+        (1.0 GB query-side and 0.66 GB key-side at config 4) are released."""
+        if self._settled:
+            return
+        self.build_key_lists()
+        if self._csr is not None:
+            self.qunion, self.kunion = self._csr.finish([self.qunion, self.kunion])
+            self._csr = None
+        self.qcols = None
+        self.klists = None
+        self.sel = {key: val for key, val in self.sel.items() if key != "tiles"}
+        self._settled = True
+
+    def list_bytes(self) -> int:
+        """Bytes of the work lists the plan holds."""
+        ts = [*self.qunion, self.qstart, self.qlen]
+        if self.qcols is not None:
+            ts.append(self.qcols)
+        if self.kunion is not None:
+            ts += list(self.kunion)
+        if self.klists is not None:
+            ts += list(self.klists)
+        return sum(t.numel() * t.element_size() for t in ts)
 
     def sum_lens(self) -> int:
         """Executed (query tile, key tile) pairs (host sync)."""
@@ -156,11 +175,18 @@ class _DynBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _Plan, sm_scale: float):
-        if ops.OVERLAP_SIDE_WORK and any(ctx.needs_input_grad[:3]):
-            plan.build_key_lists_side()  # the backward's lists, beside the forward kernel
+        grads = any(ctx.needs_input_grad[:3])
+        if grads:
+            # the backward's lists, beside the forward kernel (or before it)
+            if ops.OVERLAP_SIDE_WORK:
+                plan.build_key_lists_side()
+            else:
+                plan.build_key_lists()
         o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
                                 plan.qorder)
         plan.join_side()  # queued after the forward kernel: the key lists still run beside it
+        if grads:
+            plan.settle()  # release the per-tile lists; compact the unions while the forward runs
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
@@ -211,9 +237,9 @@ def plan_dynamic(q, k, v, grid_padded, *, method, sparsity=0.9375, cdf_threshold
     kernels, with results identical to padding first.  compute_padded_queries
     defaults to False here, the adapters' setting (flash_attn_bsa_3d_dynamic
     passes True unless told otherwise).  keep_scores keeps the fp32 block
-    scores on the plan (plan.scores) for inspection.  compact_lists keeps every
-    work list in compact CSR form (memory O(nnz): ~0.3 GB instead of ~2.3 GB
-    of list buffers per call at config 4), at one host read per list."""
+    scores on the plan (plan.scores) for inspection.  compact_lists makes
+    plan.settle() keep the two pair unions in compact CSR form (O(nnz)
+    memory, one host read for both); the plan keeps every list until then."""
     B, Hn, S, D = q.shape
     T, H, W = grid_padded
     box = tuple(input_grid) if input_grid is not None else (T, H, W)
@@ -253,7 +279,7 @@ def flash_attn_bsa_3d_dynamic(
     return_shape_ids: bool = False,
     compute_padded_queries: bool = True,
     input_grid: Optional[Tuple[int, int, int]] = None,
-    compact_lists: bool = False,
+    compact_lists: bool = True,
 ):
     """Dynamic-block-shape BSA for video self-attention; returns [B,H,S,D] in
     THW order (dynamic_block_attention.py:194-332).  q, k, v: [B,H,S,D] THW
@@ -276,9 +302,12 @@ def flash_attn_bsa_3d_dynamic(
     unpadding of wan_video_dit.py:342-431 done inside the gather and scatter
     kernels; the result equals padding first and slicing after, bit for bit.
 
-    compact_lists (not in the reference's signature) keeps the work lists in
-    compact CSR form (O(nnz) memory) until the backward; results are
-    identical."""
+    When gradients are needed, the forward releases the per-tile lists once
+    the backward's pair unions exist.  compact_lists (not in the reference's
+    signature; default True) keeps those unions in compact CSR form until
+    the backward (O(nnz) memory, one host read of their sizes made while the
+    forward kernel runs); False keeps them as dense pairs x Nt buffers.
+    Results are identical either way."""
     plan = plan_dynamic(q, k, v, grid_padded, method=method, sparsity=sparsity, cdf_threshold=cdf_threshold,
                         audio_token_norms=audio_token_norms, valid_mask=valid_mask, lambda_a=lambda_a,
                         tau_128=tau_128, lambda_128=lambda_128, shape_ids=shape_ids,

@@ -418,6 +418,49 @@ def lists_to_csr(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor):
     return _op("lists_to_csr", start, length, cols)
 
 
+def csr_offsets(length: torch.Tensor):
+    """First half of lists_to_csr: (offsets int32 [rows + 1], nnz int64 [1]),
+    both on the device (no host read)."""
+    _cuda(length)
+    return _op("lists_csr_offsets", length)
+
+
+def csr_fill(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, offsets: torch.Tensor, nnz: int):
+    """Second half of lists_to_csr: the entries [nnz] at csr_offsets' offsets
+    (nnz read by the caller)."""
+    _cuda(start, length, cols, offsets)
+    return _op("lists_csr_fill", start, length, cols, offsets, int(nnz))
+
+
+class DeferredCompaction:
+    """Compaction of several (start, len, cols) lists into CSR with one host
+    read for all of them.  add() launches a list's offsets on the current
+    stream and copies its nnz into pinned host memory without waiting;
+    finish() waits for those copies (their events, not the streams: work
+    queued after them, such as an attention kernel, is not waited for), then
+    fills every list's CSR entries on the current stream.  The entries and
+    their order are the source lists'."""
+
+    def __init__(self, n: int):
+        self.host = torch.empty(n, dtype=torch.int64, pin_memory=True)
+        self.offsets = [None] * n
+        self.events = [None] * n
+
+    def add(self, i: int, lists):
+        off, total = csr_offsets(lists[1])
+        self.host[i:i + 1].copy_(total, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.offsets[i], self.events[i] = off, ev
+
+    def finish(self, lists_seq):
+        for ev in self.events:
+            ev.synchronize()
+        nnz = self.host.tolist()
+        return [(*csr_lists(self.offsets[i]), csr_fill(*lists, self.offsets[i], nnz[i]))
+                for i, lists in enumerate(lists_seq)]
+
+
 def csr_lists(offsets: torch.Tensor):
     """(start int64 [rows], len int32 [rows]) of CSR offsets: the list form the
     pair, union and attention kernels take (entries unchanged)."""

@@ -38,11 +38,6 @@ import torch
 from . import ops
 
 
-def _compact(start, length, cols):
-    offsets, entries = ops.lists_to_csr(start, length, cols)
-    return (*ops.csr_lists(offsets), entries)
-
-
 class _ChunkPlan:
     """Rearranged rows, selection and work lists of one call (built under no_grad)."""
 
@@ -76,17 +71,17 @@ class _ChunkPlan:
         self.qstart, self.qlen = ops.tile_rows(sel["ntiles"], lq.block_id_of_tile, BH, lq.Nt, lq.N_b, sel["tcap"],
                                                qcount)
         self.qcols = sel["tiles"].view(-1)
-        # compact lists: the kept lists in CSR form, O(nnz) memory (same entries)
+        # compact lists: the pair unions the backward keeps as CSR, O(nnz)
+        # memory (settle(); one host read of both nnz; same entries)
         self.compact = compact_lists
-        if compact_lists:
-            self.qstart, self.qlen, self.qcols = _compact(self.qstart, self.qlen, self.qcols)
-            self.sel = {key: val for key, val in sel.items() if key != "tiles"}
+        self._settled = False
         self.tmasks = ops.tile_masks(self.kv_valid) if k_masked else None
         self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lq.Nt, lk.Nt)
         self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lq.Nt, self.tmasks, col_tiles=lk.Nt,
                                      pairmap=self.qpair)
+        self._csr = ops.DeferredCompaction(2) if compact_lists else None
         if compact_lists:
-            self.qunion = _compact(*self.qunion)
+            self._csr.add(0, self.qunion)
         # launch order of the forward and dQ kernels (longest lists last-dispatched first)
         self.qorder = ops.pair_order(self.qunion[1], 64)
         self.klists = None
@@ -97,12 +92,13 @@ class _ChunkPlan:
 
     def key_lists_side(self):
         """key_lists on the side stream, after the work queued so far on the
-        current stream (not for compact lists, which read nnz on the host)."""
-        if self.kunion is not None or self.compact:
+        current stream."""
+        if self.kunion is not None:
             return
         _, self.keys_ready = ops.side_launch(
             self.qcols.device, self.key_lists, reads=(self.qstart, self.qlen, self.qcols),
-            produces=lambda _: (*self.klists, self.kpair, *self.kunion, self.korder))
+            produces=lambda _: (*self.klists, self.kpair, *self.kunion, self.korder,
+                                self._csr.offsets[1] if self._csr is not None else None))
 
     def join_side(self):
         """Make the current stream wait for a side-stream key-list build (the
@@ -116,14 +112,27 @@ class _ChunkPlan:
         if self.kunion is None:
             self.klists = ops.transpose_lists(self.qstart, self.qlen, self.qcols, self.B * self.H, self.lq.Nt,
                                               self.lk.Nt)
-            if self.compact:
-                self.klists = _compact(*self.klists)
             self.kpair = ops.pair_tiles(*self.klists, self.lk.Nt, self.lq.Nt)
             self.kunion = ops.pair_union(*self.klists, self.lk.Nt, None, col_tiles=self.lq.Nt, pairmap=self.kpair)
-            if self.compact:
-                self.kunion = _compact(*self.kunion)
             self.korder = ops.pair_order(self.kunion[1], 32)
+            if self._csr is not None:
+                self._csr.add(1, self.kunion)
         return self.kunion
+
+    def settle(self):
+        """Keep only what the backward reads: both pair unions (compact CSR
+        when the plan is compact, one batched host read of their nnz),
+        pairings and launch orders; the per-tile lists are released."""
+        if self._settled:
+            return
+        self.key_lists()
+        if self._csr is not None:
+            self.qunion, self.kunion = self._csr.finish([self.qunion, self.kunion])
+            self._csr = None
+        self.qcols = None
+        self.klists = None
+        self.sel = {key: val for key, val in self.sel.items() if key != "tiles"}
+        self._settled = True
 
     def sum_lens(self) -> int:
         """Executed (query tile, key tile) pairs (host sync)."""
@@ -137,11 +146,18 @@ class _ChunkBSA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, plan: _ChunkPlan, sm_scale: float):
-        if ops.OVERLAP_SIDE_WORK and any(ctx.needs_input_grad[:3]):
-            plan.key_lists_side()  # the backward's lists, beside the forward kernel
+        grads = any(ctx.needs_input_grad[:3])
+        if grads:
+            # the backward's lists, beside the forward kernel (or before it)
+            if ops.OVERLAP_SIDE_WORK:
+                plan.key_lists_side()
+            else:
+                plan.key_lists()
         o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
                                 plan.qorder)
         plan.join_side()  # queued after the forward kernel: the key lists still run beside it
+        if grads:
+            plan.settle()  # release the per-tile lists; compact the unions while the forward runs
         ctx.plan = plan
         ctx.sm_scale = sm_scale
         ctx.in_dtypes = (q.dtype, k.dtype, v.dtype)
@@ -195,7 +211,8 @@ def plan_chunked(q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, *, sparsity,
                  compact_lists=False) -> _ChunkPlan:
     """Selection half of the uniform path (no attention).  keep_scores keeps
     the fp32 chunk scores on the plan (plan.scores) for inspection;
-    compact_lists keeps the work lists in compact CSR form (O(nnz) memory)."""
+    compact_lists makes plan.settle() keep the pair unions in compact CSR
+    form (O(nnz) memory)."""
     if sparsity is None and cdf_threshold is None:
         raise ValueError("Either sparsity or cdf_threshold must be provided")
     with torch.no_grad():
@@ -204,7 +221,7 @@ def plan_chunked(q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, *, sparsity,
 
 
 def bsa_chunked(q, k, v, lq: ops.ChunkLayout, lk: ops.ChunkLayout, *, sparsity, cdf_threshold, sm_scale,
-                q_valid=None, k_valid=None, compute_padded_queries=False, compact_lists=False) -> torch.Tensor:
+                q_valid=None, k_valid=None, compute_padded_queries=False, compact_lists=True) -> torch.Tensor:
     """Uniform BSA of q [B,H,Sq,D] (THW of lq.grid) over k, v [B,H,Sk,D] (THW
     of lk.grid); returns [B,H,Sq,D] in q's dtype and order."""
     plan = plan_chunked(q, k, v, lq, lk, sparsity=sparsity, cdf_threshold=cdf_threshold, sm_scale=sm_scale,

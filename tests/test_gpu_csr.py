@@ -6,7 +6,8 @@ Bit-exact: CSR rows equal the source lists (rows anywhere in the source
 buffer, empty rows, a row past the others' capacity); select_csr equals the
 oracle's selection expanded to tiles per query tile; transpose_csr equals the
 oracle's transpose.  A compact plan gives bit-identical attention outputs and
-gradients to the default plan and keeps a fraction of its list memory."""
+gradients to a dense one, and after its forward keeps only the two pair
+unions, in CSR form, with the dense unions' rows."""
 import math
 
 import numpy as np
@@ -100,22 +101,30 @@ def test_compact_plan_identical_and_smaller(plan_case):
         outs.append([host(t) for t in (o, q.grad, k.grad, v.grad)])
     for a, b in zip(*outs):
         assert np.array_equal(a, b)
-    # list memory kept by the plan: dense buffers vs compact CSR
+    # list memory the plan keeps from the forward to the backward (after
+    # settle(), as the forward leaves it): the per-tile lists are released,
+    # the pair unions stay as dense buffers or compact CSR with the same rows
     q, k, v = (dev(bf16(c[n])) for n in ("q", "k", "v"))
-    sizes = []
+    sizes, unions = [], []
     for compact in (False, True):
         p = plan_dynamic(q, k, v, c["grid"], method="ivpq", sparsity=0.75, cdf_threshold=0.9,
                          audio_token_norms=dev(c["norms"]), valid_mask=dev(c["valid"]).bool(), compact_lists=compact)
         p.build_key_lists()
-        lists = [p.qcols, p.qunion[2], p.klists[2], p.kunion[2]]
-        sizes.append(sum(t.numel() * t.element_size() for t in lists))
+        peak = p.list_bytes()
+        p.settle()
+        assert p.qcols is None and p.klists is None and "tiles" not in p.sel
+        sizes.append(p.list_bytes())
+        assert sizes[-1] < peak
+        unions.append([[host(t) for t in u] for u in (p.qunion, p.kunion)])
         if compact:
-            # O(nnz): every kept list buffer holds exactly its entries
-            nnz = int(p.qlen.sum().item())
-            assert p.qcols.numel() == nnz and p.klists[2].numel() == nnz
+            # O(nnz): every kept union buffer holds exactly its entries
             assert p.qunion[2].numel() == int(p.qunion[1].sum().item())
             assert p.kunion[2].numel() == int(p.kunion[1].sum().item())
-    say("list bytes dense", sizes[0], "compact", sizes[1])
+    for (s0, l0, c0), (s1, l1, c1) in zip(*unions):
+        assert np.array_equal(l0, l1)
+        for r in range(l0.size):
+            assert np.array_equal(c0[s0[r]: s0[r] + l0[r]], c1[s1[r]: s1[r] + l1[r]]), r
+    say("list bytes kept: dense", sizes[0], "compact", sizes[1])
     assert sizes[1] < sizes[0]
 
 

@@ -10,7 +10,8 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 OPS = ["zone_stats", "audio_zone_stats", "zone_gradient", "zone_shapes", "assign_shapes", "a2v_norms", "zone_layout",
        "rearrange_index", "gather_pool", "scatter_rows", "chunk_gather_pool", "chunk_scatter_rows", "block_scores",
        "select_tiles", "tile_rows", "transpose_lists", "pair_tiles", "pair_union", "pair_order", "tile_masks",
-       "lse_to_m2", "bsa_fwd", "bwd_preprocess", "bsa_bwd_dkdv", "bsa_bwd_dq", "linear_rownorm", "lists_to_csr"]
+       "lse_to_m2", "bsa_fwd", "bwd_preprocess", "bsa_bwd_dkdv", "bsa_bwd_dq", "linear_rownorm", "lists_to_csr",
+       "lists_csr_offsets", "lists_csr_fill"]
 
 
 @pytest.fixture(scope="module")
@@ -96,3 +97,13 @@ def test_operators_reject_cpu_tensors(prism):
     x = torch.zeros((1, 1, 512, 64), dtype=torch.bfloat16)
     with pytest.raises(Exception):
         prism.zone_stats(x, None, [8, 8, 8], [8, 8, 8])
+
+
+def test_fake_split_csr(prism):
+    """lists_csr_offsets keeps the total on the device; lists_csr_fill takes
+    the caller's nnz (no data-dependent size)."""
+    with FakeTensorMode():
+        off, tot = prism.lists_csr_offsets(_t((100,), torch.int32))
+        assert off.shape == (101,) and off.dtype == torch.int32 and tot.shape == (1,) and tot.dtype == torch.int64
+        ent = prism.lists_csr_fill(_t((100,), torch.int64), _t((100,), torch.int32), _t((5000,), torch.int32), off, 777)
+        assert ent.shape == (777,) and ent.dtype == torch.int32
