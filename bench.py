@@ -633,8 +633,14 @@ def main():
         "prism_block_scores": 2 * B * H * Nb * D * 4 + B * H * Nb * Nb * 4,
         "prism_select_tiles": B * H * Nb * Nb * 4 + 4 * nnz_tiles + 4 * B * H * Nb,
     }
-    breakdown = {}
+    breakdown, side = {}, {}
     for name, (n, t) in sorted(kt.items(), key=lambda x: -x[1][0] * x[1][1]):
+        if name.endswith(" (side stream)"):
+            # launches beside the forward kernel: their events also time the
+            # wait for CUs the forward holds, so they are no kernel durations
+            side[name[: -len(" (side stream)")]] = {"launches_per_step": n // args.steps,
+                                                     "event_ms_incl_wait": round(t, 4)}
+            continue
         e = {"launches_per_step": n // args.steps, "ms": round(t, 4)}
         if name in attn:
             alg, exe = attn[name]
@@ -725,6 +731,9 @@ def main():
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                    "selection_vs_reference_torch": sel_agree},
         "roofline": roof, "cpu_baseline": cpu, "dense": dense, "breakdown": breakdown,
+        "side_stream": {"note": "key-side list builds launched beside the forward kernel on a second stream; "
+                                "event times include waiting for the CUs the forward holds (kernel durations: "
+                                "rocprofv3 kernel trace)", "launches": side},
     }
     if ceil is not None:
         rec["config"]["mfma_util_step_measured"] = round(value / ceil["mfma_loop_tflops"], 4)
@@ -974,6 +983,8 @@ def run_uniform(args, inp):
            "prism_select_tiles": B * H * N_b * N_b * 4 + 4 * int(plan.sel["ntiles"].sum().item()) + 4 * B * H * N_b}
     breakdown = {}
     for name, (n, t) in sorted(kt.items(), key=lambda x: -x[1][0] * x[1][1]):
+        if name.endswith(" (side stream)"):
+            continue  # event times that include waiting beside the forward kernel
         e = {"launches_per_step": n // args.steps, "ms": round(t, 4)}
         if name in attn:
             alg, exe = attn[name]
