@@ -143,3 +143,20 @@ def test_compact_uniform_identical(plan_case):
         outs.append([host(t) for t in (o, q.grad, k.grad, v.grad)])
     for a, b in zip(*outs):
         assert np.array_equal(a, b)
+
+
+def test_autograd_forward_keeps_only_compact_unions(plan_case):
+    """Through autograd (flash_attn_bsa_3d_dynamic with gradients), the plan
+    the backward holds has released its per-tile lists and keeps the two pair
+    unions as CSR (each entry buffer exactly the union sizes), by default."""
+    from prism_amd import flash_attn_bsa_3d_dynamic
+    c = plan_case
+    q, k, v = (dev(bf16(c[n])).requires_grad_(True) for n in ("q", "k", "v"))
+    o = flash_attn_bsa_3d_dynamic(q, k, v, c["grid"], method="ivpq", sparsity=0.75, cdf_threshold=0.9,
+                                  audio_token_norms=dev(c["norms"]), valid_mask=dev(c["valid"]).bool())
+    plan = o.grad_fn.plan
+    assert plan.qcols is None and plan.klists is None and "tiles" not in plan.sel
+    for u in (plan.qunion, plan.kunion):
+        assert u[2].numel() == int(u[1].sum().item())
+    o.backward(torch.ones_like(o))
+    assert all(bool(torch.isfinite(t.grad).all()) for t in (q, k, v))
