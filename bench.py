@@ -889,10 +889,10 @@ def run_sweep(args, inp):
 def run_bridge(args, inp):
     """The a2v bridge output projection of the config (residual = x W^T + b,
     interactionv2.py:348; M = video tokens, N = K = C) with the per-token
-    residual norms (wan_video_dit.py:742-752) fused into its epilogue
-    (prism_linear_rownorm), against torch's F.linear (hipBLASLt) followed by
-    prism_a2v_norms: median ms of each, and the fused kernel's bf16 MFMA
-    rate (2 M N K flop)."""
+    residual norms (wan_video_dit.py:742-752): fused into this build's GEMM
+    epilogue (prism_linear_rownorm) and unfused (torch's F.linear, i.e.
+    hipBLASLt, followed by prism_a2v_norms): median ms of each, the GEMM
+    alone, and the fused kernel's bf16 MFMA rate (2 M N K flop)."""
     import torch
     from prism_amd import ops
     S, C = inp["S"], CONFIGS[args.config][5]
@@ -907,6 +907,7 @@ def run_bridge(args, inp):
         fmean, fmed, _ = time_region(lambda: ops.linear_rownorm(x, w, b), steps, warm)
     kt = ops.summarize(tm)
     umean, umed, _ = time_region(lambda: ops.a2v_norms(torch.nn.functional.linear(x, w, b)), steps, warm)
+    gmean, gmed, _ = time_region(lambda: torch.nn.functional.linear(x, w, b), steps, warm)
     flop = 2.0 * S * C * C
     print(json.dumps({
         "metric": "a2v bridge o-projection + residual norms (fused epilogue) ms",
@@ -917,6 +918,7 @@ def run_bridge(args, inp):
         "fused_mfma_frac": round(flop / (fmed * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "unfused_torch_linear_plus_norms_ms": round(umed, 3),
         "speedup_fused_vs_unfused": round(umed / fmed, 3),
+        "torch_linear_alone_ms": round(gmed, 3),
         "breakdown": {k: {"launches": n // steps, "ms": round(t, 4)} for k, (n, t) in kt.items()}}), flush=True)
 
 
