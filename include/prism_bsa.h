@@ -212,9 +212,13 @@ int prism_transpose_lists(const int64_t* qstart, const int32_t* qlen, const int3
  * bitmap lives in a library-owned device workspace of 2^21 uint32 words (8 MiB
  * per GPU, held until the process ends); heads are processed in batches that
  * fit it, and one head's bitmap (Ntk * ceil(Ntq / 32) words) must fit
- * (else PRISM_EINVAL).  The call allocates nothing.  Every call on a GPU uses
- * that GPU's one workspace: calls that overlap on one GPU (different streams
- * or threads) race and must be serialised by the caller.  Outputs as
+ * (else PRISM_EINVAL).  The call allocates nothing (its first call on a GPU
+ * looks up the workspace's address and creates one event there).  Every call
+ * on a GPU uses that GPU's one workspace; the library orders the calls made
+ * outside graph capture, whatever their streams or threads: each call's
+ * stream waits for the event the previous call recorded after its kernels.
+ * Calls captured into a graph neither wait nor record, so a graph replay
+ * that overlaps another call on the same GPU races with it.  Outputs as
  * prism_transpose_lists. */
 int prism_transpose_lists_noalloc(const int64_t* qstart, const int32_t* qlen, const int32_t* qcols, int BH,
                                   int64_t Ntq, int64_t Ntk, int64_t kcap, int64_t* kstart, int32_t* klen,

@@ -1202,16 +1202,27 @@ void launch_transpose(const int64_t* qstart, const int32_t* qlen, const int32_t*
 // fit, in a file-scope device array instead of caller memory.  Each GPU the
 // library runs on holds its own copy (8 MiB) until the process ends; host
 // code reaches it only through the address hipGetSymbolAddress returns for
-// the current device (scratch_device_ptr), never through the name.
+// the current device (ScratchDevice::ptr), never through the name.
 constexpr int64_t kScratchWords = (int64_t)1 << 21;
 static __device__ __align__(256) uint32_t scratch[kScratchWords];
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-uint32_t* g_scratch_ptr[kMaxDevices] = {};
 
-// device address of `scratch` on the current device (looked up once per device)
-int scratch_device_ptr(uint32_t** out) {
+// Per-device state of `scratch`, set up on the first call on the device:
+// its address, and an event recorded on the stream of each call after its
+// kernels.  Every later call's stream waits for that event first, so calls
+// on different streams of one GPU take the array one after the other
+// instead of racing on it (calls under graph capture neither wait nor
+// record: the graph's own launch order applies to them).
+struct ScratchDevice {
+  uint32_t* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  bool recorded = false;
+};
+std::mutex g_scratch_mu;  // held by a call from set-up until its event is recorded
+ScratchDevice g_scratch[kMaxDevices];
+
+int scratch_device(ScratchDevice** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
@@ -1219,17 +1230,24 @@ int scratch_device_ptr(uint32_t** out) {
     return PRISM_EHIP;
   }
   PRISM_REQUIRE(dev >= 0 && dev < kMaxDevices, "prism_transpose_lists_noalloc: device %d out of range", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  ScratchDevice& sd = g_scratch[dev];
+  if (!sd.ptr) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) {
       prism_set_error("prism_transpose_lists_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
       return PRISM_EHIP;
     }
-    g_scratch_ptr[dev] = (uint32_t*)p;
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      prism_set_error("prism_transpose_lists_noalloc: hipEventCreateWithFlags failed: %s", hipGetErrorString(e));
+      return PRISM_EHIP;
+    }
+    sd.done = ev;
+    sd.ptr = (uint32_t*)p;
   }
-  *out = g_scratch_ptr[dev];
+  *out = &sd;
   return PRISM_OK;
 }
 
@@ -1320,16 +1338,35 @@ int prism_transpose_lists_noalloc(const int64_t* qstart, const int32_t* qlen, co
                 "%lld-word workspace; use prism_transpose_lists with a caller workspace",
                 (long long)Ntk, (long long)((Ntq + 31) / 32), (long long)kScratchWords);
   if (BH <= 0) return PRISM_OK;
-  uint32_t* ws = nullptr;
-  const int rc = scratch_device_ptr(&ws);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchDevice* sd = nullptr;
+  const int rc = scratch_device(&sd);
   if (rc != PRISM_OK) return rc;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(stream, &cap);
+  if (e != hipSuccess) {
+    prism_set_error("prism_transpose_lists_noalloc: hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+    return PRISM_EHIP;
+  }
+  const bool ordered = cap == hipStreamCaptureStatusNone;
+  if (ordered && sd->recorded && (e = hipStreamWaitEvent(stream, sd->done, 0)) != hipSuccess) {
+    prism_set_error("prism_transpose_lists_noalloc: hipStreamWaitEvent failed: %s", hipGetErrorString(e));
+    return PRISM_EHIP;
+  }
   // heads in batches that fit the workspace, one after the other on `stream`
   const int per_batch = (int)(kScratchWords / per_head < BH ? kScratchWords / per_head : BH);
   for (int bh0 = 0; bh0 < BH; bh0 += per_batch) {
     const int nbh = BH - bh0 < per_batch ? BH - bh0 : per_batch;
-    launch_transpose(qstart, qlen, qcols, bh0, nbh, Ntq, Ntk, ws, kcap, kstart, klen, kcols, stream);
+    launch_transpose(qstart, qlen, qcols, bh0, nbh, Ntq, Ntk, sd->ptr, kcap, kstart, klen, kcols, stream);
   }
   PRISM_LAUNCH_CHECK("prism_transpose_lists_noalloc");
+  if (ordered) {
+    if ((e = hipEventRecord(sd->done, stream)) != hipSuccess) {
+      prism_set_error("prism_transpose_lists_noalloc: hipEventRecord failed: %s", hipGetErrorString(e));
+      return PRISM_EHIP;
+    }
+    sd->recorded = true;
+  }
   return PRISM_OK;
 }
 
