@@ -1,0 +1,124 @@
+"""Seeded random sweep of the _run_bsa_dynamic contract end to end: the
+adapter (DynamicBlockSparseAttention) on unpadded THW inputs, forward and
+backward through autograd, against the oracle's selection and float64
+attention on the padded inputs (pad to multiples of 8, valid mask, audio
+norms padded with 0, output and gradients sliced back), as
+wan_video_dit.py:342-432 composes them.  Each case draws its own grid
+(padded or not on each axis), batch, heads, head dim, dtype, method, selection
+mode and parameters, and audio norms, so combinations no fixed case names are
+covered.  Shape ids are compared bit for bit, O / dQ / dK / dV within the
+north-star bound."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.cases import bf16
+from tests.test_gpu_parity import _tol, dev, say
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 24
+
+
+def _draw(seed):
+    """Selection modes of bsa_interface.py:235-304 in turn: top-k (sparsity
+    only), hybrid with the nucleus deciding, hybrid with the top-k floor
+    deciding, cdf only (sparsity None)."""
+    rng = np.random.default_rng(1000 + seed)
+    grid = tuple(int(rng.integers(1, 17)) for _ in range(3))
+    if seed % 6 == 5:
+        grid = tuple(-(-x // 8) * 8 for x in grid)  # a grid that needs no padding (no valid mask)
+    mode = ("topk", "hybrid", "hybrid_low_p", "cdf")[seed % 4]
+    sparsity = None if mode == "cdf" else float(rng.uniform(0.3, 0.95))
+    cdf = None if mode == "topk" else float(rng.uniform(0.3, 0.6) if mode == "hybrid_low_p" else rng.uniform(0.7, 0.99))
+    return dict(
+        rng=rng, grid=grid, B=int(rng.integers(1, 3)), H=int(rng.integers(1, 4)), D=(64, 128)[(seed // 4) % 2],
+        dtype=("bf16", "f32")[(seed // 8) % 2], method=("ivpq", "penalty")[(seed // 2) % 2],
+        sparsity=sparsity, cdf=cdf, lambda_a=float(rng.uniform(0.0, 1.0)), tau_128=float(rng.uniform(0.0, 0.5)),
+        lambda_128=float(rng.uniform(0.0, 2.0)), audio=bool(rng.integers(0, 2)))
+
+
+def _pad_thw(x, grid, gp):
+    """[..., S, D] or [S] THW -> the padded grid (zeros outside the input)."""
+    (T, Hg, Wg), (Tp, Hp, Wp) = grid, gp
+    if x.ndim == 1:
+        p = np.zeros((Tp, Hp, Wp), x.dtype)
+        p[:T, :Hg, :Wg] = x.reshape(T, Hg, Wg)
+        return p.reshape(-1)
+    lead, D = x.shape[:-2], x.shape[-1]
+    p = np.zeros(lead + (Tp, Hp, Wp, D), x.dtype)
+    p[..., :T, :Hg, :Wg, :] = x.reshape(lead + (T, Hg, Wg, D))
+    return p.reshape(lead + (Tp * Hp * Wp, D))
+
+
+def _unpad_thw(x, grid, gp):
+    """[BH, S_p, D] padded THW -> [BH, S, D] of the input grid."""
+    (T, Hg, Wg), (Tp, Hp, Wp) = grid, gp
+    return x.reshape(x.shape[0], Tp, Hp, Wp, x.shape[-1])[:, :T, :Hg, :Wg].reshape(x.shape[0], -1, x.shape[-1])
+
+
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_random_adapter_end_to_end(seed):
+    from prism_amd import DynamicBlockSparseAttention
+    from prism_amd.adapter import padded_grid
+    c = _draw(seed)
+    rng, grid, B, H, D = c["rng"], c["grid"], c["B"], c["H"], c["D"]
+    say("random case", seed, {k: v for k, v in c.items() if k != "rng"})
+    gp, _ = padded_grid(grid)
+    S, Sp = int(np.prod(grid)), int(np.prod(gp))
+    sm = 1.0 / math.sqrt(D)
+    xs = [rng.standard_normal((B, H, S, D)).astype(np.float32) for _ in range(3)]
+    norms = (rng.random(S) * 3.0).astype(np.float32) if c["audio"] else None
+    do = rng.standard_normal((B, H, S, D)).astype(np.float32)
+    if c["dtype"] == "bf16":
+        bits = [bf16(x) for x in xs]                      # what the GPU sees, as bf16 bit arrays
+        nbits = None if norms is None else bf16(norms)
+        tdt = torch.bfloat16
+        ins = [dev(b) for b in bits]
+        nt = None if nbits is None else dev(nbits)
+    else:
+        bits, nbits, tdt = xs, norms, torch.float32
+        ins = [torch.from_numpy(x).to("cuda") for x in xs]
+        nt = None if norms is None else torch.from_numpy(norms).to("cuda")
+
+    # the adapter on unpadded inputs, forward + backward
+    att = DynamicBlockSparseAttention(c["method"], {
+        "sparsity": c["sparsity"], "cdf_threshold": c["cdf"], "dynamic_block_lambda_a": c["lambda_a"],
+        "dynamic_block_tau_128": c["tau_128"], "dynamic_block_lambda_128": c["lambda_128"]})
+    att.training = True  # the per-pass shape-id cache then holds the ids the call used
+    att.advance_pass()
+    q, k, v = (t.clone().requires_grad_(True) for t in ins)
+    out = att(q, k, v, grid, nt)
+    sid = att._dyn_shape_cache[2].cpu().numpy()
+    assert out.shape == (B, H, S, D) and out.dtype == tdt
+    do_q = O.bf16_bits_to_f32(bf16(do))
+    out.backward(torch.from_numpy(do_q).to("cuda").to(tdt))
+
+    # the oracle on the padded inputs (the reference's pad + call + slice)
+    valid = _pad_thw(np.ones(S, np.uint8), grid, gp)
+    padded = [_pad_thw(b, grid, gp) for b in bits]
+    npad = None if nbits is None else _pad_thw(nbits, grid, gp)
+    masked = Sp != S
+    ref = O.select_pipeline(*padded, gp, method=c["method"], sparsity=c["sparsity"], cdf_threshold_p=c["cdf"],
+                            audio_norms=npad, valid=valid if masked else None, lambda_a=c["lambda_a"],
+                            tau_128=c["tau_128"], lambda_128=c["lambda_128"], skip_padded_queries=masked)
+    say("shape ids", np.bincount(ref["shape_ids"], minlength=13).tolist(), "N_b", ref["N_b"])
+    assert np.array_equal(sid, ref["shape_ids"])
+    src, inv = O.rearrange_index(ref["shape_ids"], gp)
+    tof = (lambda a: O.bf16_bits_to_f32(a)) if c["dtype"] == "bf16" else (lambda a: O.bf16_bits_to_f32(bf16(a)))
+    qf, kf, vf = (tof(p)[:, :, src].reshape(B * H, Sp, D) for p in padded)
+    kv = valid[src] if masked else None
+    o_ref, lse_ref = O.attn_fwd(qf, kf, vf, ref["qstart"], ref["qlen"], ref["qcols"], kv, sm)
+    o_thw = o_ref[:, inv]
+    og = out.detach().float().cpu().numpy().reshape(B * H, S, D)
+    _tol(og, _unpad_thw(o_thw, grid, gp), "O")
+    # backward: dO of the padded rows is zero (they are sliced away)
+    do_pad = _pad_thw(do_q.reshape(B * H, S, D), grid, gp)
+    o_bf = O.bf16_bits_to_f32(bf16(o_ref.astype(np.float32)))
+    dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, o_bf, do_pad[:, src], lse_ref, ref["qstart"], ref["qlen"],
+                                  ref["qcols"], kv, sm)
+    for name, t, r in (("dQ", q, dq_r), ("dK", k, dk_r), ("dV", v, dv_r)):
+        _tol(t.grad.float().cpu().numpy().reshape(B * H, S, D), _unpad_thw(r[:, inv], grid, gp), name)
