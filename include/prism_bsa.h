@@ -10,7 +10,8 @@
  * Citations name the reference function (file:line under
  * hymm/models/modules/block_sparse_attention/ unless another path is given)
  * whose behaviour the entry point provides.  The reference is Python/Triton;
- * its host layer's calls into these functions are shown in INTEGRATION.md.
+ * its host layer reaches these functions through the torch.ops.prism
+ * operators (prism_amd/csrc/torch_ops.cpp) or through ctypes.
  *
  * dtype codes: PRISM_F32 = 0, PRISM_BF16 = 1.
  * Layouts: "THW order" = the reference's flattened (t, h, w) token order of a

@@ -12,7 +12,7 @@ Pipeline (all HIP kernels of libprism_bsa.so, one host sync for N_b):
   (5) tile lists per query tile        prism_tile_rows
   (6) block-sparse attention           prism_bsa_fwd / prism_bsa_bwd_*
   (7) back to THW order                prism_scatter_rows
-Deliberate differences from the reference (documented in DESIGN.md): block
+Deliberate differences from the reference: block
 means and scores are fp32 (the reference pools and scores in q's dtype) and
 every reduction uses one fixed order, so zone statistics, shape ids and
 selected sets are reproducible bit for bit.
