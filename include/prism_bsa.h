@@ -255,7 +255,9 @@ int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* co
  * device; a total past 2^31 - 1 does not fit the offsets); then
  * prism_lists_csr_fill copies row r's len[r] entries from cols + start[r] to
  * out_cols + offsets[r].  The attention kernels take the result as lists
- * with start = offsets[r], len = offsets[r + 1] - offsets[r]. */
+ * with start = offsets[r], len = offsets[r + 1] - offsets[r]; they reject a
+ * null entry pointer, so a caller allocates at least one entry even when the
+ * total is 0 (the torch operators do). */
 int prism_lists_csr_offsets(const int32_t* len, int64_t rows, int32_t* offsets, int64_t* total,
                             hipStream_t stream);
 int prism_lists_csr_fill(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows,

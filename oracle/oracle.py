@@ -569,9 +569,58 @@ def attn_fwd(q, k, v, qstart, qlen, qcols, kv_valid, sm_scale):
     return o, lse
 
 
-def attn_bwd(q, k, v, o, do, lse, qstart, qlen, qcols, kv_valid, sm_scale):
+def _round_bf16(x: np.ndarray) -> np.ndarray:
+    """float64 -> nearest bf16 value (via float32, ties to even), as float64."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(x.astype(np.float32))).astype(np.float64)
+
+
+def attn_bwd_term_magnitudes(q, k, v, o, do, lse, qstart, qlen, qcols, kv_valid, sm_scale):
+    """Per element of dQ, dK, dV the sum of the magnitudes of the terms that
+    attn_bwd adds up: sum_k |dS_qk| |K_k| sm_scale, sum_q |dS_qk| |Q_q|
+    sm_scale and sum_q P_qk |dO_q| (float64, same lists and masks).  Rounding
+    each dS (P) operand to bf16 moves an element by at most 2^-9 times this
+    sum, the bound of the reference kernels' own arithmetic against float64."""
+    BH, S, D = q.shape
+    Nt = S // TILE
+    q = q.astype(np.float64); k = k.astype(np.float64); v = v.astype(np.float64)
+    o = o.astype(np.float64); do = do.astype(np.float64)
+    delta = (o * do).sum(-1)
+    mq = np.zeros_like(q); mk = np.zeros_like(k); mv = np.zeros_like(v)
+    for bh in range(BH):
+        for t in range(Nt):
+            row = bh * Nt + t
+            n = int(qlen[row])
+            if n == 0:
+                continue
+            sl = slice(t * TILE, (t + 1) * TILE)
+            idx = _row_keys(qcols, int(qstart[row]), n)
+            s = q[bh, sl] @ k[bh, idx].T * sm_scale
+            if kv_valid is not None:
+                s[:, ~kv_valid[idx].astype(bool)] = -np.inf
+            L = lse[bh, sl]
+            p = np.zeros_like(s)
+            ok = np.isfinite(L)
+            p[ok] = np.exp(s[ok] - L[ok, None])
+            ds = np.abs(p * (do[bh, sl] @ v[bh, idx].T - delta[bh, sl][:, None]))
+            mq[bh, sl] += ds @ np.abs(k[bh, idx]) * sm_scale
+            mk[bh, idx] += ds.T @ np.abs(q[bh, sl]) * sm_scale
+            mv[bh, idx] += p.T @ np.abs(do[bh, sl])
+    return mq, mk, mv
+
+
+def attn_bwd(q, k, v, o, do, lse, qstart, qlen, qcols, kv_valid, sm_scale, bf16_operands=False):
     """Backward of attn_fwd (bsa_interface.py:387-523 semantics: delta =
-    rowsum(o * do), dK and dQ scaled by sm_scale).  float64."""
+    rowsum(o * do), dK and dQ scaled by sm_scale).  float64.
+
+    bf16_operands: round the two computed matrix operands to bf16 before
+    their products, as the reference's kernels do: P (from the final LSE) for
+    dV = P^T dO (flash_attn_bsa_varlen_mask.py:382-391), dS = P (dP - delta),
+    formed from the unrounded P, for dK = dS^T Q and dQ = dS K (:395-399,
+    :462-470).  Everything else stays float64.  Where dK / dQ sum terms of
+    mixed sign to a small result, this rounding alone moves them by up to
+    2^-9 of the sum of the terms' magnitudes, more than the result's own bf16
+    rounding."""
+    rb = _round_bf16 if bf16_operands else (lambda x: x)
     BH, S, D = q.shape
     Nt = S // TILE
     q = q.astype(np.float64); k = k.astype(np.float64); v = v.astype(np.float64)
@@ -593,9 +642,9 @@ def attn_bwd(q, k, v, o, do, lse, qstart, qlen, qcols, kv_valid, sm_scale):
             p = np.zeros_like(s)
             ok = np.isfinite(L)
             p[ok] = np.exp(s[ok] - L[ok, None])
-            dv[bh, idx] += p.T @ do[bh, sl]
+            dv[bh, idx] += rb(p).T @ do[bh, sl]
             dp = do[bh, sl] @ v[bh, idx].T
             ds = p * (dp - delta[bh, sl][:, None])
-            dq[bh, sl] += ds @ k[bh, idx] * sm_scale
-            dk[bh, idx] += ds.T @ q[bh, sl] * sm_scale
+            dq[bh, sl] += rb(ds) @ k[bh, idx] * sm_scale
+            dk[bh, idx] += rb(ds).T @ q[bh, sl] * sm_scale
     return dq, dk, dv

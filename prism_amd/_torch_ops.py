@@ -162,7 +162,7 @@ def _register_fakes():
 
     @reg("prism::lists_to_csr")
     def _(start, length, cols):
-        nnz = torch.library.get_ctx().new_dynamic_size()
+        nnz = torch.library.get_ctx().new_dynamic_size(min=1)  # max(entries, 1): never an empty buffer
         return _empty(start, (start.numel() + 1,), i32), _empty(start, (nnz,), i32)
 
     @reg("prism::lists_csr_offsets")
@@ -171,7 +171,7 @@ def _register_fakes():
 
     @reg("prism::lists_csr_fill")
     def _(start, length, cols, offsets, nnz):
-        return _empty(start, (nnz,), i32)
+        return _empty(start, (max(nnz, 1),), i32)
 
     @reg("prism::tile_masks")
     def _(valid):

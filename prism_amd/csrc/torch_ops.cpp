@@ -440,8 +440,17 @@ std::tuple<Tensor, Tensor, Tensor> pair_union(const Tensor& s_, const Tensor& l_
   return {ustart, ulen, ucols};
 }
 
+// CSR entry buffer of nnz entries, with at least one element: lists that
+// hold no entry at all (top-k of int((1 - s) N) = 0 blocks) still get a
+// valid pointer for the attention entry points, which take none as null
+// (torch gives an empty tensor a null data pointer); every length is 0 then,
+// so the spare element is never read
+Tensor csr_entries(const Tensor& like, int64_t nnz) {
+  return at::empty({std::max<int64_t>(nnz, 1)}, opts(like, at::kInt));
+}
+
 // compact CSR of (start, len, cols) lists: offsets int32 [rows + 1], cols
-// int32 [nnz].  One host read of nnz (the allocation size) between the two
+// int32 [max(nnz, 1)].  One host read of nnz (the allocation size) between the two
 // launches.
 std::tuple<Tensor, Tensor> lists_to_csr(const Tensor& s_, const Tensor& l_, const Tensor& c_) {
   check_lists(s_, l_, c_);
@@ -455,7 +464,7 @@ std::tuple<Tensor, Tensor> lists_to_csr(const Tensor& s_, const Tensor& l_, cons
                    total.data_ptr<int64_t>(), stream_of(s));
   const int64_t nnz = total.item<int64_t>();
   TORCH_CHECK_VALUE(nnz <= 2147483647ll, "prism.lists_to_csr: more than 2^31 - 1 list entries (int32 offsets)");
-  Tensor out = at::empty({nnz}, opts(s, at::kInt));
+  Tensor out = csr_entries(s, nnz);
   if (nnz > 0)
     PRISM_TORCH_CALL(prism_lists_csr_fill, s.data_ptr<int64_t>(), l.data_ptr<int32_t>(), c.data_ptr<int32_t>(), rows,
                    offsets.data_ptr<int32_t>(), out.data_ptr<int32_t>(), stream_of(s));
@@ -488,7 +497,7 @@ Tensor lists_csr_fill(const Tensor& s_, const Tensor& l_, const Tensor& c_, cons
   TORCH_CHECK_VALUE(nnz >= 0 && nnz <= 2147483647ll, "prism.lists_csr_fill: nnz out of range (int32 offsets)");
   const c10::DeviceGuard guard(s_.device());
   const Tensor s = s_.contiguous(), l = l_.contiguous(), c = c_.contiguous(), offsets = offsets_.contiguous();
-  Tensor out = at::empty({nnz}, opts(s, at::kInt));
+  Tensor out = csr_entries(s, nnz);
   if (nnz > 0)
     PRISM_TORCH_CALL(prism_lists_csr_fill, s.data_ptr<int64_t>(), l.data_ptr<int32_t>(), c.data_ptr<int32_t>(),
                      s.numel(), offsets.data_ptr<int32_t>(), out.data_ptr<int32_t>(), stream_of(s));

@@ -411,9 +411,11 @@ def lists_to_csr(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor):
     """Compact CSR of per-row lists given as (start int64, len int32, cols
     int32) with rows anywhere in cols (the outputs of tile_rows over
     select_tiles, transpose_lists and pair_union): returns (offsets int32
-    [rows + 1], entries int32 [nnz]), row r's entries at
+    [rows + 1], entries int32 [max(nnz, 1)]), row r's entries at
     [offsets[r], offsets[r + 1]).  Memory O(nnz) instead of the producers'
-    rows x capacity buffers; one host read of nnz."""
+    rows x capacity buffers; one host read of nnz.  Lists with no entry at
+    all still get a one-element buffer (never read), so the attention entry
+    points, which reject null list pointers, take them."""
     _cuda(start, length, cols)
     return _op("lists_to_csr", start, length, cols)
 
@@ -426,8 +428,8 @@ def csr_offsets(length: torch.Tensor):
 
 
 def csr_fill(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, offsets: torch.Tensor, nnz: int):
-    """Second half of lists_to_csr: the entries [nnz] at csr_offsets' offsets
-    (nnz read by the caller)."""
+    """Second half of lists_to_csr: the entries [max(nnz, 1)] at csr_offsets'
+    offsets (nnz read by the caller)."""
     _cuda(start, length, cols, offsets)
     return _op("lists_csr_fill", start, length, cols, offsets, int(nnz))
 

@@ -398,18 +398,39 @@ def _check_order(order, ulen, G, tail):
     assert order[k:].tolist() == want
 
 
-def _tol(got, ref, what, rel_bound=1e-2):
+def _bf16_half_ulp(x):
+    """Half a bf16 ulp at |x| (8 significant bits: 2^(e - 8) for |x| in
+    [2^e, 2^(e + 1))); 0 at 0."""
+    a = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    return np.where(a > 0, np.exp2(e - 8), 0.0)
+
+
+def _tol(got, ref, what, rel_bound=1e-2, slack=None):
     """max-abs 2e-2, mean-abs 2e-3 (bf16 vs float64); plus
     a relative bound ||got - ref|| / ||ref|| <= 1e-2 (Frobenius), which
     catches a scaled result where the values are small (at long lists |O| and
-    |dQ| average ~6e-3, below the absolute bounds)."""
+    |dQ| average ~6e-3, below the absolute bounds).
+
+    The max-abs bound holds for the result before its bf16 storage rounding:
+    element i may differ by 2e-2 plus half a bf16 ulp of ref[i].  A result
+    stored in bf16 differs from the exact value by up to that half ulp even
+    when computed exactly, and at |value| >= 8 the half ulp (0.031) alone
+    exceeds 2e-2 (gradients of queries that keep one key tile reach |dK| ~
+    12).  Below |value| = 1 the slack is at most 2^-9.
+
+    slack: a further per-element allowance (the rounding bound of bf16
+    operands in sums whose terms cancel, from the oracle's term magnitudes)."""
     diff = got.astype(np.float64) - ref
     err = np.abs(diff)
     mx, mean = float(err.max()), float(err.mean())
+    allow = _bf16_half_ulp(ref) + (0.0 if slack is None else slack)
+    excess = float((err - allow).max())
     ref_norm = float(np.linalg.norm(ref))
     rel = float(np.linalg.norm(diff)) / ref_norm if ref_norm > 0 else float(np.linalg.norm(diff))
-    say(what, "max-abs", mx, "mean-abs", mean, "rel", rel, "||ref||", ref_norm)
-    assert mx <= 2e-2 and mean <= 2e-3, (what, mx, mean)
+    say(what, "max-abs", mx, "beyond bf16 rounding", excess, "mean-abs", mean, "rel", rel, "||ref||", ref_norm,
+        "max|ref|", float(np.abs(ref).max()))
+    assert excess <= 2e-2 and mean <= 2e-3, (what, mx, excess, mean)
     assert rel <= rel_bound, (what, "relative error", rel, "||ref||", ref_norm)
 
 

@@ -6,8 +6,17 @@ norms padded with 0, output and gradients sliced back), as
 wan_video_dit.py:342-432 composes them.  Each case draws its own grid
 (padded or not on each axis), batch, heads, head dim, dtype, method, selection
 mode and parameters, and audio norms, so combinations no fixed case names are
-covered.  Shape ids are compared bit for bit, O / dQ / dK / dV within the
-north-star bound."""
+covered.  Shape ids are compared bit for bit, O / dQ / dK / dV with the
+float64 oracle within the north-star bound (mean-abs 2e-3, relative 1e-2),
+the max-abs bound of 2e-2 widened per element by the rounding of the bf16
+operands that the reference's backward kernels multiply
+(flash_attn_bsa_varlen_mask.py:382-399, :462-470: P for dV, dS for dK and
+dQ): 2^-8 times the sum of the magnitudes of the element's terms
+(oracle.attn_bwd_term_magnitudes), twice the 2^-9 by which that rounding
+alone can move it, for the kernels' fp32 P, dS and delta.  Cases whose
+queries keep a single key tile have gradients of |dK| ~ 12 made of terms
+that cancel (sum of magnitudes ~ 34); there the reference's arithmetic
+itself is 0.037 from float64, and so are the kernels."""
 import math
 
 import numpy as np
@@ -21,6 +30,10 @@ from tests.test_gpu_parity import _tol, dev, say
 pytestmark = pytest.mark.gpu
 
 N_CASES = 24
+# seeds past N_CASES that a longer sweep flagged: top-k of int((1 - s) N_b) = 0
+# blocks (no list holds an entry: 224, 312) and queries that keep a single key
+# tile, whose gradients reach |dK| ~ 12 (32, 164, 244)
+REGRESSION_SEEDS = (32, 164, 224, 244, 312)
 
 
 def _draw(seed):
@@ -60,7 +73,7 @@ def _unpad_thw(x, grid, gp):
     return x.reshape(x.shape[0], Tp, Hp, Wp, x.shape[-1])[:, :T, :Hg, :Wg].reshape(x.shape[0], -1, x.shape[-1])
 
 
-@pytest.mark.parametrize("seed", range(N_CASES))
+@pytest.mark.parametrize("seed", list(range(N_CASES)) + list(REGRESSION_SEEDS))
 def test_random_adapter_end_to_end(seed):
     from prism_amd import DynamicBlockSparseAttention
     from prism_amd.adapter import padded_grid
@@ -118,7 +131,9 @@ def test_random_adapter_end_to_end(seed):
     # backward: dO of the padded rows is zero (they are sliced away)
     do_pad = _pad_thw(do_q.reshape(B * H, S, D), grid, gp)
     o_bf = O.bf16_bits_to_f32(bf16(o_ref.astype(np.float32)))
-    dq_r, dk_r, dv_r = O.attn_bwd(qf, kf, vf, o_bf, do_pad[:, src], lse_ref, ref["qstart"], ref["qlen"],
-                                  ref["qcols"], kv, sm)
-    for name, t, r in (("dQ", q, dq_r), ("dK", k, dk_r), ("dV", v, dv_r)):
-        _tol(t.grad.float().cpu().numpy().reshape(B * H, S, D), _unpad_thw(r[:, inv], grid, gp), name)
+    bwd_args = (qf, kf, vf, o_bf, do_pad[:, src], lse_ref, ref["qstart"], ref["qlen"], ref["qcols"], kv, sm)
+    exact = O.attn_bwd(*bwd_args)
+    mags = O.attn_bwd_term_magnitudes(*bwd_args)
+    for name, t, r, m in zip(("dQ", "dK", "dV"), (q, k, v), exact, mags):
+        _tol(t.grad.float().cpu().numpy().reshape(B * H, S, D), _unpad_thw(r[:, inv], grid, gp), name,
+             slack=2.0 ** -8 * _unpad_thw(m[:, inv], grid, gp))

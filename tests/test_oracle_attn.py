@@ -194,3 +194,70 @@ def test_oracle_attention_planted_mistakes_fail():
     # a key mask that is ignored
     o2, _ = O.attn_fwd(q, k, v, qstart, qlen, qcols, None, sm)
     assert _fails(lambda: _close(o2, ro, "O without the key mask"))
+
+
+def test_oracle_bf16_operands_closed_form():
+    """attn_bwd(bf16_operands=True) rounds P before dV = P^T dO and dS =
+    P (dP - delta), formed from the unrounded P, before dK and dQ
+    (flash_attn_bsa_varlen_mask.py:382-399, :462-470).  Inputs with a closed
+    form: keys 0-2 valid (the rest masked), K = 0 except k_0 = 2 e_1, queries
+    with q[:, 1] = 0, so every score is 0 and P = 1/3 over the valid keys
+    (LSE = ln 3); v_0 = 5 e_0, the rest 0; dO rows e_0; O = 0, so delta = 0.
+    Then dP = 5 on key 0 and 0 elsewhere, dS = 5/3 on key 0.  bf16(1/3) =
+    0.333984375 and bf16(5/3) = 1.6640625 (8 significant bits, nearest);
+    rounding P inside dS as well would give bf16(0.333984375 * 5) = 1.671875,
+    and leaving dS unrounded 5/3."""
+    rng = np.random.default_rng(5)
+    S, D = 64, 64
+    sm = 1.0 / 8.0
+    q = rng.standard_normal((1, S, D))
+    q[:, :, 1] = 0.0
+    k = np.zeros((1, S, D)); k[0, 0, 1] = 2.0
+    v = np.zeros((1, S, D)); v[0, 0, 0] = 5.0
+    do = np.zeros((1, S, D)); do[:, :, 0] = 1.0
+    o = np.zeros((1, S, D))
+    lse = np.full((1, S), math.log(3.0))
+    kv = np.zeros(S, np.uint8); kv[:3] = 1
+    qstart, qlen, qcols = np.zeros(1, np.int64), np.ones(1, np.int32), np.zeros(1, np.int32)
+    qsum = q[0].sum(0)
+    for bf, p_bf, ds_bf in ((False, 1.0 / 3.0, 5.0 / 3.0), (True, 0.333984375, 1.6640625)):
+        dq, dk, dv = O.attn_bwd(q, k, v, o, do, lse, qstart, qlen, qcols, kv, sm, bf16_operands=bf)
+        want_dv = np.zeros((S, D)); want_dv[:3, 0] = S * p_bf
+        want_dk = np.zeros((S, D)); want_dk[0] = ds_bf * sm * qsum
+        want_dq = np.zeros((S, D)); want_dq[:, 1] = ds_bf * 2.0 * sm
+        for got, want, what in ((dv[0], want_dv, "dV"), (dk[0], want_dk, "dK"), (dq[0], want_dq, "dQ")):
+            assert np.abs(got - want).max() <= 1e-12 * max(1.0, np.abs(want).max()), (bf, what)
+    # the three roundings are distinguishable at these values
+    r = lambda x: float(O._round_bf16(np.array([x]))[0])
+    assert r(1.0 / 3.0) == 0.333984375 and r(5.0 / 3.0) == 1.6640625 and r(0.333984375 * 5.0) == 1.671875
+
+
+def test_oracle_bf16_operands_within_rounding_bound():
+    """On random lists the bf16-operand backward differs from the float64 one
+    by at most the rounding bound 2^-9 * sum |terms| per element
+    (attn_bwd_term_magnitudes), and by more than nothing.  The magnitudes are
+    at least |float64 result| (triangle inequality) and equal it where every
+    term has one sign (the closed-form case: one nonzero dS per row, q >= 0)."""
+    q, k, v, do, qstart, qlen, qcols, kv = _case(1, 2, 256, 256, 128, (1,), (3,), False)
+    sm = 1.0 / math.sqrt(128)
+    o, lse = O.attn_fwd(q, k, v, qstart, qlen, qcols, kv, sm)
+    args = (q, k, v, o, do, lse, qstart, qlen, qcols, kv, sm)
+    exact = O.attn_bwd(*args)
+    rounded = O.attn_bwd(*args, bf16_operands=True)
+    mags = O.attn_bwd_term_magnitudes(*args)
+    for e, rr, m, what in zip(exact, rounded, mags, ("dQ", "dK", "dV")):
+        diff = np.abs(rr - e)
+        assert (diff <= 2.0 ** -9 * m + 1e-12).all(), what
+        assert diff.max() > 0, what
+        assert (np.abs(e) <= m * (1 + 1e-12) + 1e-12).all(), what
+    # one sign: the closed-form inputs with q >= 0
+    S, D = 64, 64
+    qq = np.abs(np.random.default_rng(5).standard_normal((1, S, D))); qq[:, :, 1] = 0.0
+    kk = np.zeros((1, S, D)); kk[0, 0, 1] = 2.0
+    vv = np.zeros((1, S, D)); vv[0, 0, 0] = 5.0
+    dd = np.zeros((1, S, D)); dd[:, :, 0] = 1.0
+    kv1 = np.zeros(S, np.uint8); kv1[:3] = 1
+    a1 = (qq, kk, vv, np.zeros((1, S, D)), dd, np.full((1, S), math.log(3.0)), np.zeros(1, np.int64),
+          np.ones(1, np.int32), np.zeros(1, np.int32), kv1, 0.125)
+    for e, m in zip(O.attn_bwd(*a1), O.attn_bwd_term_magnitudes(*a1)):
+        assert np.abs(np.abs(e) - m).max() <= 1e-12

@@ -107,3 +107,6 @@ def test_fake_split_csr(prism):
         assert off.shape == (101,) and off.dtype == torch.int32 and tot.shape == (1,) and tot.dtype == torch.int64
         ent = prism.lists_csr_fill(_t((100,), torch.int64), _t((100,), torch.int32), _t((5000,), torch.int32), off, 777)
         assert ent.shape == (777,) and ent.dtype == torch.int32
+        # no entries: still a one-element buffer (a valid pointer for the kernels)
+        ent = prism.lists_csr_fill(_t((100,), torch.int64), _t((100,), torch.int32), _t((5000,), torch.int32), off, 0)
+        assert ent.shape == (1,)
