@@ -107,6 +107,12 @@ def test_random_adapter_end_to_end(seed):
     out = att(q, k, v, grid, nt)
     sid = att._dyn_shape_cache[2].cpu().numpy()
     assert out.shape == (B, H, S, D) and out.dtype == tdt
+    # the inference path (no autograd: no backward lists, no compaction) gives
+    # the same output bits (the shape ids come from the pass cache)
+    with torch.no_grad():
+        out_ng = att(*ins, grid, nt)
+    assert torch.equal(out_ng.view(torch.int16) if tdt == torch.bfloat16 else out_ng.view(torch.int32),
+                       out.detach().view(torch.int16) if tdt == torch.bfloat16 else out.detach().view(torch.int32))
     do_q = O.bf16_bits_to_f32(bf16(do))
     out.backward(torch.from_numpy(do_q).to("cuda").to(tdt))
 

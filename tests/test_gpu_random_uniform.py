@@ -163,6 +163,11 @@ def test_random_uniform_end_to_end(seed):
     q, k, v = (dev(a).requires_grad_(True) for a in ins)
     out = fn(q, k, v)
     assert out.dtype == tdt and out.shape == q.shape
+    # the inference path (no autograd) gives the same output bits
+    with torch.no_grad():
+        out_ng = fn(*(dev(a) for a in ins))
+    iv = torch.int16 if tdt == torch.bfloat16 else torch.int32
+    assert torch.equal(out_ng.view(iv), out.detach().view(iv))
     do = O.bf16_bits_to_f32(bf16(rng.standard_normal((B, H, Sq, D)).astype(np.float32)))
     o_r, grads, mags = _oracle_attention(qh, kh, vh, do, ref, B, H, sm, k_masked)
     _tol(out.detach().float().cpu().numpy().reshape(B * H, -1, D), o_r, "O")
