@@ -382,6 +382,19 @@ def summarize_counters(fetch_csv, write_csv, calib_fetch_csv, calib_write_csv):
     print(json.dumps(out), flush=True)
 
 
+def staged_tile_bytes(plan, D: int) -> dict:
+    """Bytes the attention kernels copy into LDS per launch: one 64 x D bf16
+    tile of each operand per pair-union entry (forward and dQ: K and V over
+    the query-side unions; dK/dV: Q and dO plus the m2 and delta rows over the
+    key-side unions), whether the copy hits in L2 or not."""
+    tile = 64 * D * 2
+    q_entries = int(plan.qunion[1].sum().item())
+    out = {"prism_bsa_fwd": 2 * tile * q_entries, "prism_bsa_bwd_dq": 2 * tile * q_entries}
+    if plan.kunion is not None:
+        out["prism_bsa_bwd_dkdv"] = (2 * tile + 2 * 64 * 4) * int(plan.kunion[1].sum().item())
+    return out
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed counter summary
     (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by the copy calibration),
@@ -622,6 +635,7 @@ def main():
     Xin = B * H * S * D * 2  # one bf16 [B,H,S,D] THW tensor (input grid)
     nnz_tiles = int(plan.sel["ntiles"].sum().item())
     union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
+    staged = staged_tile_bytes(plan, D)
     with torch.no_grad():
         plan.settle()
     list_bytes = plan.list_bytes()
@@ -646,6 +660,9 @@ def main():
             alg, exe = attn[name]
             e.update(tflops=round(alg / (t * 1e-3) / 1e12, 1), executed_tflops=round(exe / (t * 1e-3) / 1e12, 1),
                      mfma_frac=round(alg / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+            if name in staged:
+                e.update(staged_tile_GB=round(staged[name] / 1e9, 2),
+                         staged_tile_TBps=round(staged[name] / (t * 1e-3) / 1e12, 2))
         elif name in hbm:
             e.update(GBps=round(hbm[name] / (t * 1e-3) / 1e9, 1),
                      hbm_frac=round(hbm[name] / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
@@ -974,6 +991,9 @@ def run_uniform(args, inp):
                             sm_scale=1 / math.sqrt(D))
     sum_lens = plan.sum_lens()
     union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
+    with torch.no_grad():
+        plan.key_lists()
+    staged = staged_tile_bytes(plan, D)
     fl = 64 * 64 * D * sum_lens
     kept_flops = 14 * fl
     attn = {"prism_bsa_fwd": (4 * fl, 4 * fl), "prism_bsa_bwd_dkdv": (8 * fl, 8 * fl),
@@ -992,6 +1012,9 @@ def run_uniform(args, inp):
             alg, exe = attn[name]
             e.update(tflops=round(alg / (t * 1e-3) / 1e12, 1), executed_tflops=round(exe / (t * 1e-3) / 1e12, 1),
                      mfma_frac=round(alg / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+            if name in staged:
+                e.update(staged_tile_GB=round(staged[name] / 1e9, 2),
+                         staged_tile_TBps=round(staged[name] / (t * 1e-3) / 1e12, 2))
         elif name in hbm:
             e.update(GBps=round(hbm[name] / (t * 1e-3) / 1e9, 1),
                      hbm_frac=round(hbm[name] / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
