@@ -421,7 +421,11 @@ def measured_ceilings():
                  clock the chip holds under full matrix load; best of 3;
       gemm       torch.matmul bf16 8192^3 and F.linear at the A2V bridge shape
                  (302,400 x 5,120 x 5,120) (hipBLASLt), median of 20 and of 5;
-      copy       prism_copy_peak over 4 GiB (read + write bytes), best of 10."""
+      copy       prism_copy_peak over 4 GiB (read + write bytes), best of 10;
+      tile stream  prism_tile_stream_peak: the attention kernels' LDS tile
+                 copies without their math, over one config-4 head's K and V
+                 (189 MB: the Infinity Cache holds it, the L2s do not) and over
+                 4 GiB (HBM), ~50 ms per launch after a warm-up, best of 3."""
     import ctypes
     import statistics
     import torch
@@ -475,7 +479,23 @@ def measured_ceilings():
 
     c_ms = min(timed(copy, 12)[2:])
     assert bool((dst[:: 1 << 20] == 1).all())
-    del src, dst
+    del dst
+    ssink = torch.empty(2 * cus, device="cuda", dtype=torch.int32)
+    moved = ctypes.c_int64(0)
+
+    def tile_stream(buf, nbytes):
+        def run(steps):
+            _lib.call("prism_tile_stream_peak", buf.data_ptr(), nbytes, steps, ssink.data_ptr(), ssink.numel(),
+                      ctypes.addressof(moved), stream)
+        t_probe = timed(lambda: run(1000), 2)[-1]
+        steps = max(1000, int(1000 * 50.0 / max(t_probe, 1e-3)))
+        t = min(timed(lambda: run(steps), 4)[1:])
+        return moved.value / (t * 1e-3) / 1e12
+    cache_bytes = 11520 * 16384  # 2 x 5,760 tiles of 64 x 128 bf16: one config-4 head's K and V
+    cache_buf = torch.zeros(cache_bytes // 4, device="cuda", dtype=torch.float32)
+    stream_cache = tile_stream(cache_buf, cache_bytes)
+    stream_hbm = tile_stream(src, nbytes)
+    del src, cache_buf
     torch.cuda.empty_cache()
     return {
         "mfma_loop_tflops": round(mfma_tflops, 1), "mfma_loop_ms": round(mfma_ms, 1),
@@ -486,6 +506,9 @@ def measured_ceilings():
         "gemm_bridge_tflops": round(2 * 302400 * 5120 * 5120 / (l_ms * 1e-3) / 1e12, 1),
         "gemm": "hipBLASLt bf16 (torch.matmul 8192^3, F.linear 302400x5120x5120): the faster of the two",
         "copy_GBps": round(2 * nbytes / (c_ms * 1e-3) / 1e9, 1), "copy": "prism_copy_peak, 4 GiB read + 4 GiB written",
+        "tile_stream_TBps": round(stream_cache, 2), "tile_stream_hbm_TBps": round(stream_hbm, 2),
+        "tile_stream": "prism_tile_stream_peak: 32 KB stages of two random 16 KB tiles into LDS, the forward's copy "
+                       "plan, no math; over 189 MB (Infinity Cache) and over 4 GiB (HBM)",
         "cus": cus,
     }
 
@@ -690,6 +713,8 @@ def main():
                 e["mfma_frac_measured"] = round(e["tflops"] / pm, 4)
             if "hbm_frac" in e:
                 e["hbm_frac_measured"] = round(e["GBps"] / ph, 4)
+            if "staged_tile_TBps" in e:
+                e["tile_stream_frac_measured"] = round(e["staged_tile_TBps"] / ceil["tile_stream_TBps"], 4)
 
     dense = None
     if not args.no_dense:

@@ -369,6 +369,15 @@ int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do
 int prism_mfma_peak(int64_t iters, float* sink, int64_t sink_len, uint64_t* clocks, int64_t* flops,
                     hipStream_t stream);
 int prism_copy_peak(const void* src, void* dst, int64_t bytes, hipStream_t stream);
+/* prism_tile_stream_peak: the attention kernels' tile stream without their
+ * math.  Two workgroups per CU each copy `steps` stages of two 16 KB tiles of
+ * src (`bytes`, a multiple of 16384; tiles drawn by a per-workgroup LCG) into
+ * LDS with global_load_lds_dwordx4, one stage in flight, a barrier per stage.
+ * *moved (host) = the bytes copied; sink: >= 2 x CUs words (the first word of
+ * each workgroup's last stage).  Over a buffer that the Infinity Cache holds
+ * but the L2s do not (~190 MB), the rate the forward's K/V stream can reach. */
+int prism_tile_stream_peak(const void* src, int64_t bytes, int64_t steps, uint32_t* sink, int64_t sink_len,
+                           int64_t* moved, hipStream_t stream);
 
 /* ------------------------------------------------------------------ list checks (debug) */
 

@@ -53,6 +53,7 @@ SIGNATURES = {
     "prism_check_lists": [P, P, P, I64, I64, I64, I32, P],
     "prism_mfma_peak": [I64, P, I64, P, P, P],
     "prism_copy_peak": [P, P, I64, P],
+    "prism_tile_stream_peak": [P, I64, I64, P, I64, P, P],
     "prism_check_launch_maps": [P, I64, I64, P, I64],
 }
 
