@@ -243,6 +243,16 @@ int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* co
                      int64_t col_tiles, const int32_t* pairmap, const uint64_t* tile_masks, int64_t ucap,
                      int64_t* ustart, int32_t* ulen, int32_t* ucols, hipStream_t stream);
 
+/* Quad unions for prism_bsa_fwd_quad (no counterpart in the reference; its
+ * forward kernel walks one query tile's list): rows of four tiles, quad q of a
+ * head being pairmap[4 q + k], k < 4 (four consecutive entries of a
+ * prism_pair_tiles map: two pairs of a group), or rows 4 q + k.  Entries
+ * tile << 5 | partial << 4 | member bits (bit k: row k lists the tile); rows %
+ * 4 == 0, row_tiles % 4 == 0; otherwise as prism_pair_union. */
+int prism_quad_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
+                     int64_t col_tiles, const int32_t* pairmap, const uint64_t* tile_masks, int64_t ucap,
+                     int64_t* ustart, int32_t* ulen, int32_t* ucols, hipStream_t stream);
+
 /* Compact CSR of per-row lists (the select and list-transpose output form of
  * the drop-in operators: offsets int32 [rows + 1], entries int32 [nnz]) from the
  * (start, len, cols) lists the other entry points produce, whose rows sit
@@ -326,6 +336,18 @@ int prism_bsa_fwd(const void* q, const void* k, const void* v, int BH, int64_t S
                   const int32_t* pairmap, const int32_t* order, float sm_scale, void* o, float* lse,
                   int32_t* work_counter, hipStream_t stream);
 
+/* prism_bsa_fwd over quad unions (prism_quad_union): one 8-wave workgroup per
+ * four query tiles, so each staged K / V tile serves up to 256 query rows;
+ * quadmap: the pairmap the quad unions were built with (or NULL).  Same
+ * outputs, bit for bit, as prism_bsa_fwd over the pair unions of the same
+ * lists (every query row walks its own list in the same order with the same
+ * arithmetic).  Sq a multiple of 256; order (or NULL) a permutation of the
+ * BH * Sq/256 quads; work_counter as for prism_bsa_fwd. */
+int prism_bsa_fwd_quad(const void* q, const void* k, const void* v, int BH, int64_t Sq, int64_t Sk, int D,
+                       const uint64_t* tile_masks, const int64_t* ustart, const int32_t* ulen, const int32_t* ucols,
+                       const int32_t* quadmap, const int32_t* order, float sm_scale, void* o, float* lse,
+                       int32_t* work_counter, hipStream_t stream);
+
 /* _attn_bwd_preprocess (common.py:110-127): delta[r] = sum_d o[r][d] * do[r][d]
  * over rows of bf16 [rows, D] tensors; fp32 out. */
 int prism_bwd_preprocess(const void* o, const void* do_, int64_t rows, int D, float* delta, hipStream_t stream);
@@ -384,14 +406,17 @@ int prism_tile_stream_peak(const void* src, int64_t bytes, int64_t steps, uint32
 /* Work-list validation on HOST memory (no counterpart in the reference, whose
  * Triton kernels read the lists unchecked).  rows lists (start[r], len[r]) into
  * cols[0, ncols): each len in [0, ntiles], each row inside cols, entries
- * strictly ascending in [0, ntiles); with unions != 0 the entries are
- * prism_pair_union entries (tile = entry >> 3): flagged for at least one tile
- * of the pair, and flagged partial exactly where tile_masks[tile] is not all
- * ones (never when tile_masks is NULL).  Returns 1 (invalid argument) naming
- * the first violation.  With PRISM_DEBUG=1 in the environment, prism_bsa_fwd,
- * prism_bsa_bwd_dkdv, prism_bsa_bwd_dq and prism_pair_union run these checks
- * on host copies of their lists (synchronising their stream) before launching
- * anything, and return 1 without a launch when one fails. */
+ * strictly ascending in [0, ntiles); with unions == 1 the entries are
+ * prism_pair_union entries (tile = entry >> 3, two member bits, partial bit
+ * 4), with unions == 2 prism_quad_union entries (tile = entry >> 5, four
+ * member bits, partial bit 16): flagged for at least one tile of the pair or
+ * quad, and flagged partial exactly where tile_masks[tile] is not all ones
+ * (never when tile_masks is NULL).  Returns 1 (invalid argument) naming the
+ * first violation.  With PRISM_DEBUG=1 in the environment, prism_bsa_fwd,
+ * prism_bsa_fwd_quad, prism_bsa_bwd_dkdv, prism_bsa_bwd_dq, prism_pair_union
+ * and prism_quad_union run these checks on host copies of their lists
+ * (synchronising their stream) before launching anything, and return 1
+ * without a launch when one fails. */
 int prism_check_lists(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t ncols,
                       int64_t ntiles, int unions, const uint64_t* tile_masks);
 

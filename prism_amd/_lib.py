@@ -40,6 +40,7 @@ SIGNATURES = {
     "prism_transpose_lists": [P, P, P, I32, I64, I64, P, I64, P, P, P, P],
     "prism_transpose_lists_noalloc": [P, P, P, I32, I64, I64, I64, P, P, P, P],
     "prism_pair_union": [P, P, P, I64, I64, I64, P, P, I64, P, P, P, P],
+    "prism_quad_union": [P, P, P, I64, I64, I64, P, P, I64, P, P, P, P],
     "prism_pair_tiles": [P, P, P, I64, I64, I64, P, P],
     "prism_pair_order": [P, I64, I32, I64, P, P],
     "prism_lists_csr_offsets": [P, I64, P, P, P],
@@ -47,6 +48,7 @@ SIGNATURES = {
     "prism_tile_masks": [P, I64, P, P],
     "prism_lse_to_m2": [P, I64, P, P],
     "prism_bsa_fwd": [P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P, P],
+    "prism_bsa_fwd_quad": [P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P, P],
     "prism_bwd_preprocess": [P, P, I64, I32, P, P],
     "prism_bsa_bwd_dkdv": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P, P],
     "prism_bsa_bwd_dq": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P],

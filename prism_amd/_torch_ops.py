@@ -156,6 +156,12 @@ def _register_fakes():
         return (_empty(start, (pairs,), i64), _empty(start, (pairs,), i32),
                 _empty(start, (max(pairs * col_tiles, 1),), i32))
 
+    @reg("prism::quad_union")
+    def _(start, length, cols, row_tiles, col_tiles, pairmap, tile_masks):
+        quads = start.numel() // 4
+        return (_empty(start, (quads,), i64), _empty(start, (quads,), i32),
+                _empty(start, (max(quads * col_tiles, 1),), i32))
+
     @reg("prism::pair_order")
     def _(ulen, group, tail):
         return _empty(ulen, (ulen.numel(),), i32)
@@ -183,6 +189,10 @@ def _register_fakes():
 
     @reg("prism::bsa_fwd")
     def _(q, k, v, tile_masks, ustart, ulen, ucols, pairmap, order, sm_scale):
+        return _empty(q, q.shape, q.dtype), _empty(q, q.shape[:3], f32)
+
+    @reg("prism::bsa_fwd_quad")
+    def _(q, k, v, tile_masks, ustart, ulen, ucols, quadmap, order, sm_scale):
         return _empty(q, q.shape, q.dtype), _empty(q, q.shape[:3], f32)
 
     @reg("prism::bwd_preprocess")

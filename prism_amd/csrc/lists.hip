@@ -23,43 +23,51 @@ namespace {
 
 constexpr int kUnionWin = 8192;  // tiles per LDS bitmap window (256 words)
 
-// one 256-thread workgroup per row pair; the pair's rows are 2p, 2p + 1 of
-// the head, or pairmap[2p], pairmap[2p + 1] (row indices inside the head)
+// one 256-thread workgroup per group of R rows (R = 2: a pair, R = 4: a quad);
+// the group's rows are R p .. R p + R - 1 of the head, or pairmap[R p + k]
+// (row indices inside the head).  Entries: tile << (R + 1) | partial << R |
+// member bits (bit k: row k lists the tile).
+template <int R>
 __global__ __launch_bounds__(256) void pair_union_kernel(const int64_t* __restrict__ start,
-                                                         const int32_t* __restrict__ len,
-                                                         const int32_t* __restrict__ cols, int64_t Nr, int64_t Nc,
-                                                         const int32_t* __restrict__ pairmap,
-                                                         const uint64_t* __restrict__ tile_masks, int64_t ucap,
-                                                         int64_t* __restrict__ ustart, int32_t* __restrict__ ulen,
-                                                         int32_t* __restrict__ ucols) {
-  __shared__ uint32_t bmA[kUnionWin / 32], bmB[kUnionWin / 32];
+                                                    const int32_t* __restrict__ len,
+                                                    const int32_t* __restrict__ cols, int64_t Nr, int64_t Nc,
+                                                    const int32_t* __restrict__ pairmap,
+                                                    const uint64_t* __restrict__ tile_masks, int64_t ucap,
+                                                    int64_t* __restrict__ ustart, int32_t* __restrict__ ulen,
+                                                    int32_t* __restrict__ ucols) {
+  __shared__ uint32_t bm[R][kUnionWin / 32];
   __shared__ uint32_t wtot[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t p = blockIdx.x;
-  const int64_t head0 = (2 * p) / Nr * Nr;
-  const int64_t rA = pairmap ? head0 + pairmap[2 * p] : 2 * p;
-  const int64_t rB = pairmap ? head0 + pairmap[2 * p + 1] : 2 * p + 1;
-  const int32_t* A = cols + start[rA];
-  const int32_t* B = cols + start[rB];
-  const int nA = len[rA], nB = len[rB];
+  const int64_t head0 = (R * p) / Nr * Nr;
+  const int32_t* L[R];
+  int nl[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int64_t r = pairmap ? head0 + pairmap[R * p + k] : R * p + k;
+    L[k] = cols + start[r];
+    nl[k] = len[r];
+  }
   // list entries index column tiles inside one head (0 .. Nc-1), as does tile_masks
   int32_t* out = ucols + p * ucap;
   int count = 0;
   for (int64_t w0 = 0; w0 < Nc; w0 += kUnionWin) {
-    bmA[tid] = 0u;
-    bmB[tid] = 0u;
+#pragma unroll
+    for (int k = 0; k < R; ++k) bm[k][tid] = 0u;
     __syncthreads();
-    for (int i = tid; i < nA; i += 256) {
-      const int64_t t = (int64_t)A[i] - w0;
-      if (t >= 0 && t < kUnionWin && A[i] < Nc) atomicOr(&bmA[t >> 5], 1u << (t & 31));
-    }
-    for (int i = tid; i < nB; i += 256) {
-      const int64_t t = (int64_t)B[i] - w0;
-      if (t >= 0 && t < kUnionWin && B[i] < Nc) atomicOr(&bmB[t >> 5], 1u << (t & 31));
-    }
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+      for (int i = tid; i < nl[k]; i += 256) {
+        const int64_t t = (int64_t)L[k][i] - w0;
+        if (t >= 0 && t < kUnionWin && L[k][i] < Nc) atomicOr(&bm[k][t >> 5], 1u << (t & 31));
+      }
     __syncthreads();
-    const uint32_t a = bmA[tid], b = bmB[tid];
-    uint32_t u = a | b;
+    uint32_t mb[R], u = 0u;
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      mb[k] = bm[k][tid];
+      u |= mb[k];
+    }
     const uint32_t c = __popc(u);
     const uint32_t incl = wave_incl_scan_u32(c, lane);
     if (lane == 63) wtot[w] = incl;
@@ -76,8 +84,10 @@ __global__ __launch_bounds__(256) void pair_union_kernel(const int64_t* __restri
       const int bit = __ffs(u) - 1;
       u &= u - 1;
       const int64_t tile = w0 + 32 * tid + bit;
-      int e = (int)(tile << 3) | (int)((a >> bit) & 1u) | (int)(((b >> bit) & 1u) << 1);
-      if (tile_masks && tile_masks[tile] != ~0ull) e |= 4;
+      int e = (int)(tile << (R + 1));
+#pragma unroll
+      for (int k = 0; k < R; ++k) e |= (int)(((mb[k] >> bit) & 1u) << k);
+      if (tile_masks && tile_masks[tile] != ~0ull) e |= 1 << R;
       out[pos++] = e;
     }
     count += (int)total;
@@ -344,8 +354,33 @@ int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* co
     PRISM_DEBUG_CHECK(prism_debug_check_maps("prism_pair_union", pairmap, rows / row_tiles, row_tiles, nullptr, 0,
                                              stream));
   }
-  pair_union_kernel<<<(unsigned)pairs, 256, 0, stream>>>(start, len, cols, row_tiles, col_tiles, pairmap, tile_masks, ucap, ustart, ulen, ucols);
+  pair_union_kernel<2><<<(unsigned)pairs, 256, 0, stream>>>(start, len, cols, row_tiles, col_tiles, pairmap, tile_masks,
+                                                             ucap, ustart, ulen, ucols);
   PRISM_LAUNCH_CHECK("prism_pair_union");
+  return PRISM_OK;
+}
+
+int prism_quad_union(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t row_tiles,
+                     int64_t col_tiles, const int32_t* pairmap, const uint64_t* tile_masks, int64_t ucap,
+                     int64_t* ustart, int32_t* ulen, int32_t* ucols, hipStream_t stream) {
+  PRISM_REQUIRE(start && len && cols && ustart && ulen && ucols, "prism_quad_union: null pointer");
+  PRISM_REQUIRE(rows >= 0 && rows % 4 == 0, "prism_quad_union: rows must be a multiple of 4 (quads of tiles)");
+  PRISM_REQUIRE(row_tiles > 0 && row_tiles % 4 == 0 && rows % row_tiles == 0,
+                "prism_quad_union: rows must be a multiple of row_tiles (tiles per head), itself a multiple of 4");
+  PRISM_REQUIRE(col_tiles > 0 && col_tiles < (1ll << 26), "prism_quad_union: col_tiles out of range");
+  PRISM_REQUIRE(ucap >= col_tiles, "prism_quad_union: ucap must be >= col_tiles");
+  const int64_t quads = rows / 4;
+  if (quads == 0) return PRISM_OK;
+  PRISM_REQUIRE(quads < (1ll << 31), "prism_quad_union: too many quads");
+  if (prism_debug_enabled()) {
+    PRISM_DEBUG_CHECK(prism_debug_check_lists("prism_quad_union", start, len, cols, rows, col_tiles, 0, nullptr,
+                                              stream));
+    PRISM_DEBUG_CHECK(prism_debug_check_maps("prism_quad_union", pairmap, rows / row_tiles, row_tiles, nullptr, 0,
+                                             stream));
+  }
+  pair_union_kernel<4><<<(unsigned)quads, 256, 0, stream>>>(start, len, cols, row_tiles, col_tiles, pairmap, tile_masks,
+                                                              ucap, ustart, ulen, ucols);
+  PRISM_LAUNCH_CHECK("prism_quad_union");
   return PRISM_OK;
 }
 

@@ -440,6 +440,28 @@ std::tuple<Tensor, Tensor, Tensor> pair_union(const Tensor& s_, const Tensor& l_
   return {ustart, ulen, ucols};
 }
 
+// quad unions: rows of four tiles (pairmap[4 q + k]), entries
+// tile << 5 | partial << 4 | member bits
+std::tuple<Tensor, Tensor, Tensor> quad_union(const Tensor& s_, const Tensor& l_, const Tensor& c_, int64_t row_tiles,
+                                              int64_t col_tiles, const OptT& pairmap_, const OptT& masks_) {
+  check_lists(s_, l_, c_);
+  on_gpu(pairmap_, "pairmap");
+  on_gpu(masks_, "tile_masks");
+  check_dtype(pairmap_, at::kInt, "pairmap");
+  check_dtype(masks_, at::kLong, "tile_masks");
+  const c10::DeviceGuard guard(s_.device());
+  const Tensor s = s_.contiguous(), l = l_.contiguous(), c = c_.contiguous();
+  const OptT pairmap = cont(pairmap_), masks = cont(masks_);
+  const int64_t rows = s.numel(), quads = rows / 4;
+  Tensor ustart = at::empty({quads}, opts(s, at::kLong));
+  Tensor ulen = at::empty({quads}, opts(s, at::kInt));
+  Tensor ucols = at::empty({std::max<int64_t>(quads * col_tiles, 1)}, opts(s, at::kInt));
+  PRISM_TORCH_CALL(prism_quad_union, s.data_ptr<int64_t>(), l.data_ptr<int32_t>(), c.data_ptr<int32_t>(), rows,
+                   row_tiles, col_tiles, (const int32_t*)p(pairmap), (const uint64_t*)p(masks), col_tiles,
+                   ustart.data_ptr<int64_t>(), ulen.data_ptr<int32_t>(), ucols.data_ptr<int32_t>(), stream_of(s));
+  return {ustart, ulen, ucols};
+}
+
 // CSR entry buffer of nnz entries, with at least one element: lists that
 // hold no entry at all (top-k of int((1 - s) N) = 0 blocks) still get a
 // valid pointer for the attention entry points, which take none as null
@@ -582,6 +604,27 @@ std::tuple<Tensor, Tensor> bsa_fwd(const Tensor& q_, const Tensor& k_, const Ten
   return {o, lse};
 }
 
+std::tuple<Tensor, Tensor> bsa_fwd_quad(const Tensor& q_, const Tensor& k_, const Tensor& v_, const OptT& masks_,
+                                        const Tensor& us_, const Tensor& ul_, const Tensor& uc_, const OptT& quadmap_,
+                                        const OptT& order_, double sm_scale) {
+  const AttnShape s = attn_shape(q_, k_, v_);
+  check_union(us_, ul_, uc_);
+  on_gpu(masks_, "tile_masks");
+  on_gpu(quadmap_, "quadmap");
+  on_gpu(order_, "order");
+  const c10::DeviceGuard guard(q_.device());
+  const Tensor q = q_.contiguous(), k = k_.contiguous(), v = v_.contiguous();
+  const Tensor us = us_.contiguous(), ul = ul_.contiguous(), uc = uc_.contiguous();
+  const OptT masks = cont(masks_), quadmap = cont(quadmap_), order = cont(order_);
+  Tensor o = at::empty_like(q);
+  Tensor lse = at::empty({s.B, s.H, s.Sq}, opts(q, at::kFloat));
+  PRISM_TORCH_CALL(prism_bsa_fwd_quad, q.data_ptr(), k.data_ptr(), v.data_ptr(), (int)(s.B * s.H), s.Sq, s.Sk,
+                   (int)s.D, (const uint64_t*)p(masks), us.data_ptr<int64_t>(), ul.data_ptr<int32_t>(),
+                   uc.data_ptr<int32_t>(), (const int32_t*)p(quadmap), (const int32_t*)p(order), (float)sm_scale,
+                   o.data_ptr(), lse.data_ptr<float>(), work_counter(q).data_ptr<int32_t>(), stream_of(q));
+  return {o, lse};
+}
+
 Tensor bwd_preprocess(const Tensor& o_, const Tensor& do_) {
   on_gpu(o_, "o");
   on_gpu(do_, "do");
@@ -684,6 +727,8 @@ TORCH_LIBRARY(prism, m) {
   m.def("pair_tiles(Tensor start, Tensor len, Tensor cols, int row_tiles, int col_tiles) -> Tensor");
   m.def("pair_union(Tensor start, Tensor len, Tensor cols, int row_tiles, int col_tiles, Tensor? pairmap, "
         "Tensor? tile_masks) -> (Tensor, Tensor, Tensor)");
+  m.def("quad_union(Tensor start, Tensor len, Tensor cols, int row_tiles, int col_tiles, Tensor? pairmap, "
+        "Tensor? tile_masks) -> (Tensor, Tensor, Tensor)");
   m.def("pair_order(Tensor ulen, int group, int tail) -> Tensor");
   m.def("lists_to_csr(Tensor start, Tensor len, Tensor cols) -> (Tensor, Tensor)");
   m.def("lists_csr_offsets(Tensor len) -> (Tensor, Tensor)");
@@ -692,6 +737,8 @@ TORCH_LIBRARY(prism, m) {
   m.def("lse_to_m2(Tensor lse) -> Tensor");
   m.def("bsa_fwd(Tensor q, Tensor k, Tensor v, Tensor? tile_masks, Tensor ustart, Tensor ulen, Tensor ucols, "
         "Tensor? pairmap, Tensor? order, float sm_scale) -> (Tensor, Tensor)");
+  m.def("bsa_fwd_quad(Tensor q, Tensor k, Tensor v, Tensor? tile_masks, Tensor ustart, Tensor ulen, Tensor ucols, "
+        "Tensor? quadmap, Tensor? order, float sm_scale) -> (Tensor, Tensor)");
   m.def("bwd_preprocess(Tensor o, Tensor do) -> Tensor");
   m.def("bsa_bwd_dkdv(Tensor q, Tensor k, Tensor v, Tensor do, Tensor m2, Tensor delta, Tensor? kv_valid, "
         "Tensor ustart, Tensor ulen, Tensor ucols, Tensor? pairmap, Tensor? order, float sm_scale) -> (Tensor, Tensor)");
@@ -720,6 +767,7 @@ TORCH_LIBRARY_IMPL(prism, CUDA, m) {
   m.impl("transpose_lists", &transpose_lists);
   m.impl("pair_tiles", &pair_tiles);
   m.impl("pair_union", &pair_union);
+  m.impl("quad_union", &quad_union);
   m.impl("pair_order", &pair_order);
   m.impl("lists_to_csr", &lists_to_csr);
   m.impl("lists_csr_offsets", &lists_csr_offsets);
@@ -727,6 +775,7 @@ TORCH_LIBRARY_IMPL(prism, CUDA, m) {
   m.impl("tile_masks", &tile_masks);
   m.impl("lse_to_m2", &lse_to_m2);
   m.impl("bsa_fwd", &bsa_fwd);
+  m.impl("bsa_fwd_quad", &bsa_fwd_quad);
   m.impl("bwd_preprocess", &bwd_preprocess);
   m.impl("bsa_bwd_dkdv", &bsa_bwd_dkdv);
   m.impl("bsa_bwd_dq", &bsa_bwd_dq);

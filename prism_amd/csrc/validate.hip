@@ -67,16 +67,19 @@ int check_lists(const char* who, const int64_t* start, const int32_t* len, const
     int64_t prev = -1;
     for (int64_t i = 0; i < n; ++i) {
       const int32_t e = cols[s + i];
-      const int64_t t = unions ? (int64_t)(e >> 3) : (int64_t)e;
+      // unions: 1 = pair entries (tile << 3 | partial << 2 | 2 member bits),
+      // 2 = quad entries (tile << 5 | partial << 4 | 4 member bits)
+      const int mbits = unions == 2 ? 4 : 2;
+      const int64_t t = unions ? (int64_t)(e >> (mbits + 1)) : (int64_t)e;
       PRISM_REQUIRE(e >= 0 && t < ntiles, "%s: row %lld entry %lld names tile %lld outside [0, %lld)", who,
                     (long long)r, (long long)i, (long long)t, (long long)ntiles);
       PRISM_REQUIRE(t > prev, "%s: row %lld entry %lld (tile %lld) is not above the previous tile %lld", who,
                     (long long)r, (long long)i, (long long)t, (long long)prev);
       prev = t;
       if (unions) {
-        PRISM_REQUIRE((e & 3) != 0, "%s: row %lld entry %lld (tile %lld) belongs to neither tile of the pair", who,
-                      (long long)r, (long long)i, (long long)t);
-        const bool partial = (e & 4) != 0;
+        PRISM_REQUIRE((e & ((1 << mbits) - 1)) != 0, "%s: row %lld entry %lld (tile %lld) belongs to no tile of its %s",
+                      who, (long long)r, (long long)i, (long long)t, unions == 2 ? "quad" : "pair");
+        const bool partial = (e & (1 << mbits)) != 0;
         const bool want = tile_masks != nullptr && tile_masks[t] != ~0ull;
         PRISM_REQUIRE(partial == want, "%s: row %lld entry %lld: tile %lld is flagged %s but its key mask is %s", who,
                       (long long)r, (long long)i, (long long)t, partial ? "partial" : "full",

@@ -98,6 +98,12 @@ class _Plan:
         # launch order of the forward and dQ kernels (the last workgroups ids
         # take the longest lists first: the launch does not end on a long one)
         self.qorder = ops.pair_order(self.qunion[1], 64)
+        # the forward's quad unions (two pairs of a zone per workgroup), used
+        # once by the forward kernel and released after it
+        self.qquad = self.qquad_order = None
+        if ops.FWD_QUAD and lay.Nt % 4 == 0:
+            self.qquad = ops.quad_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks, pairmap=self.qpair)
+            self.qquad_order = ops.pair_order(self.qquad[1], 32)
         self.klists = None
         self.kpair = None
         self.kunion = None
@@ -182,8 +188,13 @@ class _DynBSA(torch.autograd.Function):
                 plan.build_key_lists_side()
             else:
                 plan.build_key_lists()
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
-                                plan.qorder)
+        if plan.qquad is not None:
+            o_re, lse = ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qquad, sm_scale,
+                                         plan.qpair, plan.qquad_order)
+            plan.qquad = plan.qquad_order = None
+        else:
+            o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
+                                    plan.qorder)
         plan.join_side()  # queued after the forward kernel: the key lists still run beside it
         if grads:
             plan.settle()  # release the per-tile lists; compact the unions while the forward runs

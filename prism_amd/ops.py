@@ -9,6 +9,7 @@ where the kernels need it.
 from __future__ import annotations
 
 import contextlib
+import os
 from typing import Dict, List, Optional, Tuple
 
 import torch
@@ -532,6 +533,18 @@ def pair_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt
     return _op("pair_union", start, length, cols, int(Nt), ucap, pairmap, tmasks)
 
 
+def quad_union(start: torch.Tensor, length: torch.Tensor, cols: torch.Tensor, Nt: int,
+               tmasks: Optional[torch.Tensor] = None, col_tiles: Optional[int] = None,
+               pairmap: Optional[torch.Tensor] = None):
+    """Sorted union of the lists of each row quad (4q .. 4q+3, or pairmap[4q + k]:
+    two pairs of a group) with membership flags (entry = tile << 5 |
+    partial << 4 | member bits).  Nt (tiles per head) a multiple of 4.
+    Returns (ustart [rows/4] int64, ulen [rows/4] int32, ucols int32)."""
+    _cuda(start, length, cols, tmasks, pairmap)
+    ucap = int(Nt if col_tiles is None else col_tiles)
+    return _op("quad_union", start, length, cols, int(Nt), ucap, pairmap, tmasks)
+
+
 def tile_masks(valid: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     """[Nt*64] uint8/bool tile-order validity -> [Nt] 64-bit masks (int64 storage)."""
     if valid is None:
@@ -571,6 +584,18 @@ def bsa_fwd(q, k, v, tmasks, qunion, sm_scale: float, qpair: Optional[torch.Tens
     return _op("bsa_fwd", q, k, v, tmasks, ustart, ulen, ucols, qpair, qorder, float(sm_scale))
 
 
+def bsa_fwd_quad(q, k, v, tmasks, quadunion, sm_scale: float, quadmap: Optional[torch.Tensor] = None,
+                 qorder: Optional[torch.Tensor] = None):
+    """bsa_fwd over quad unions (quad_union of the per-query-tile key lists with
+    the pairmap quadmap): the same o and lse, bit for bit, from one 8-wave
+    workgroup per four query tiles.  Sq a multiple of 256."""
+    _cuda(q, k, v, tmasks, quadmap, qorder)
+    q, k, v = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v")
+    _attn_shapes(q, k, v)
+    ustart, ulen, ucols = quadunion
+    return _op("bsa_fwd_quad", q, k, v, tmasks, ustart, ulen, ucols, quadmap, qorder, float(sm_scale))
+
+
 # dK/dV and dQ are independent: with BWD_CONCURRENT the dK/dV kernel runs on a
 # second stream (default priority) so that the dQ kernel's workgroups fill the
 # CUs that the end of the dK/dV launch leaves idle.  Measured 0.7% faster per
@@ -598,6 +623,11 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 # mostly wait for its end and then delay its last workgroups: off by default.
 OVERLAP_SIDE_WORK = True
 OVERLAP_DKDV_SCATTER = False
+
+# The forward over quad unions (bsa_fwd_quad: four query tiles per staged K / V
+# tile, bit-identical to bsa_fwd) when the query tiles per head are a multiple
+# of 4.
+FWD_QUAD = os.environ.get("PRISM_FWD_QUAD", "0") not in ("", "0")
 
 
 def side_launch(device: torch.device, fn, reads=(), produces=None):

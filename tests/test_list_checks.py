@@ -119,7 +119,7 @@ def test_corrupt_unions_raise(lists, kind):
     if kind == "no_member_flag":
         p, i = full[0]
         ucols[ustart[p] + i] &= ~3
-        match = "neither tile"
+        match = "belongs to no tile"
     elif kind == "partial_flag_missing":
         p, i = hits[0]
         ucols[ustart[p] + i] &= ~4
@@ -156,3 +156,49 @@ def test_corrupt_launch_maps_raise(lists, kind):
         match = "twice"
     with pytest.raises(ValueError, match=match):
         check_maps(pairmap, HEADS, NT, order)
+
+
+def _quad_lists(L, masks):
+    """Quad unions (entry = tile << 5 | partial << 4 | four member bits) of
+    the four tiles each group of four pairmap slots names."""
+    full = np.uint64(0xFFFFFFFFFFFFFFFF)
+    ents = []
+    for h in range(HEADS):
+        for q in range(NT // 4):
+            want = {}
+            for k in range(4):
+                r = h * NT + int(L["pairmap"][h * NT + 4 * q + k])
+                for t in L["cols"][L["start"][r]: L["start"][r] + L["length"][r]]:
+                    want[int(t)] = want.get(int(t), 0) | (1 << k)
+            ents.append([t << 5 | (16 if masks is not None and masks[t] != full else 0) | b
+                         for t, b in sorted(want.items())])
+    qs = np.cumsum([0] + [len(e) for e in ents])[:-1]
+    return qs, np.array([len(e) for e in ents], np.int32), np.array(sum(ents, []), np.int32)
+
+
+@pytest.mark.parametrize("kind", ["valid", "valid_no_masks", "no_member_flag", "partial_flag_missing",
+                                  "partial_flag_spurious", "tile_out_of_range"])
+def test_quad_unions(lists, kind):
+    L = lists
+    masks = None if kind == "valid_no_masks" else L["masks"]
+    qs, ql, qc = _quad_lists(L, masks)
+    if kind.startswith("valid"):
+        check_lists(qs, ql, qc, NT, 2, masks)
+        return
+    last = NT - 1
+    hit = next(i for i in range(qc.size) if qc[i] >> 5 == last)
+    other = next(i for i in range(qc.size) if qc[i] >> 5 != last)
+    if kind == "no_member_flag":
+        qc[other] &= ~15
+        match = "belongs to no tile of its quad"
+    elif kind == "partial_flag_missing":
+        qc[hit] &= ~16
+        match = "flagged full but its key mask is partial"
+    elif kind == "partial_flag_spurious":
+        qc[other] |= 16
+        match = "flagged partial but its key mask is full"
+    else:
+        qc[hit] = (NT << 5) | 1
+        match = "outside \\[0"
+    with pytest.raises(ValueError, match=match):
+        check_lists(qs, ql, qc, NT, 2, masks)
