@@ -268,13 +268,16 @@ __device__ __forceinline__ void bsa_fwd_pair(const FwdArgs& a, uint8_t* smem, in
 // workgroup per CU, over the quad's union list (prism_quad_union: entries
 // tile << 5 | partial << 4 | member bits), so each staged K / V tile serves up
 // to 256 query rows.  Wave w owns 32 queries of quad tile w >> 1; waves w and
-// w + 4 share a SIMD.  Group 0 (waves 0-3) takes entry j as the pair kernel
-// does (S, row max, exponentials with P V) and issues the copies of entry
-// j + 2 (four stages).  Group 1 (waves 4-7) runs half an entry behind: after
-// the barrier it first finishes entry j - 1 (rescale, exponentials with P V,
-// from the S accumulators and V operands it carried across the barrier),
-// then S and the row max of entry j, so on each SIMD one wave's exponentials
-// run beside the other's MFMAs.  Every wave walks its own tile's entries in
+// w + 4 share a SIMD.  Every wave issues an eighth of the copies of entry
+// j + 2 (four stages).  Group 0 (waves 0-3) issues them right after the
+// barrier of entry j and takes entry j as the pair kernel does (S, row max,
+// exponentials with P V).  Group 1 (waves 4-7) runs half an entry behind:
+// after the barrier it first finishes entry j - 1 (rescale, exponentials with
+// P V, from the S accumulators and V operands it carried across the barrier),
+// then issues its copies, then S and the row max of entry j, so on each SIMD
+// one wave's exponentials run beside the other's MFMAs (group 1 issuing
+// right after the barrier too measured 4% slower, group 0 issuing all
+// copies 1% slower).  Every wave walks its own tile's entries in
 // ascending order with the pair kernel's arithmetic: results are bit-identical.
 constexpr int kStagesQuad = 4, kAheadQuad = 2;
 
@@ -284,7 +287,7 @@ __device__ __forceinline__ void bsa_fwd_quad(const FwdArgs& a, uint8_t* smem, in
   using RT = typename T::RT;
   constexpr int NS = D / 16;   // MFMA k-steps over d
   constexpr int NDT = D / 32;  // 32-row d blocks of O^T
-  constexpr int NOFF = RT::KB / 4, PERW = T::STAGE_KB / 4;
+  constexpr int NOFF = RT::KB / 4, PERW = T::STAGE_KB / 8;
 
   const int tid = opaque_thread_id(), lane = tid & 63, g = lane >> 5, l32 = lane & 31;
   const int w = (int)uniform_u32((uint32_t)tid >> 6);
@@ -299,20 +302,19 @@ __device__ __forceinline__ void bsa_fwd_quad(const FwdArgs& a, uint8_t* smem, in
   const uint16_t* Vh = a.v + (int64_t)bh * a.Sk * D;
   const float NINF = -__builtin_inff();
 
-  // DMA plan: waves 0-3 (one per SIMD) issue KB-instructions w, w + 4, ... of
-  // each stage (K then V); instruction i + 4m of a tile reads 4096 m bytes
-  // past instruction i, so one lane offset serves all
-  static_assert(RT::KB % 4 == 0, "tile splits into fours");
+  // DMA plan: every wave issues KB-instructions w, w + 8, ... of each stage
+  // (K then V); instruction i + 4m of a tile reads 4096 m bytes past
+  // instruction i, so one lane offset serves all
+  static_assert(RT::KB % 4 == 0 && T::STAGE_KB % 8 == 0, "tile splits into fours");
   const uint32_t soff = RT::src_offset(w & 3, lane);
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int kt, int st) {
-    if (w >= 4) return;
     const char* kb = (const char*)uniform_ptr(Kh + (int64_t)kt * 64 * D);
     const char* vb = (const char*)uniform_ptr(Vh + (int64_t)kt * 64 * D);
     const uint32_t base = lds0 + (uint32_t)(st * T::STAGE);
 #pragma unroll
     for (int s = 0; s < PERW; ++s) {
-      const int i = w + 4 * s;
+      const int i = w + 8 * s;
       const int t = i < RT::KB ? i : i - RT::KB;
       dma_b128(soff, (i < RT::KB ? kb : vb) + 4096 * ((t >> 2) % NOFF), base + (uint32_t)i * 1024u);
     }
@@ -457,9 +459,11 @@ __device__ __forceinline__ void bsa_fwd_quad(const FwdArgs& a, uint8_t* smem, in
     float m_new = NINF, alpha = 1.0f, mb = 0.0f;
     bool move = false;
     for (int j = 0; j < n; ++j) {
-      const int e = ring.e[0];
+      const int e = ring.e[0], enext = ring.e[kAheadQuad];
       ring.advance(U, n, j);
+      stage_wait<kAheadQuad + 1, PERW>(n - 1 - j);
       __syncthreads();
+      const int snext = (st + kAheadQuad) % kStagesQuad;
       const uint8_t* sK = smem + st * T::STAGE;
       st = st + 1 == kStagesQuad ? 0 : st + 1;
       if (pend) {
@@ -467,6 +471,7 @@ __device__ __forceinline__ void bsa_fwd_quad(const FwdArgs& a, uint8_t* smem, in
         pv_phase(sacc, vfr, m_new, alpha, mb, move);
         __builtin_amdgcn_s_setprio(0);
       }
+      if (j + kAheadQuad < n) issue(enext >> 5, snext);
       pend = (e & mybit) != 0;
       if (pend) {
         s_phase(sK, sacc);
