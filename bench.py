@@ -357,7 +357,8 @@ def summarize_counters(fetch_csv, write_csv, calib_fetch_csv, calib_write_csv):
     FETCH_SIZE and WRITE_SIZE runs, each scaled so that the calibration copy of
     COPY_BYTES reads and writes exactly COPY_BYTES."""
     names = {"bsa_fwd_kernel": "prism_bsa_fwd", "bsa_bwd_dkdv_kernel": "prism_bsa_bwd_dkdv",
-             "bsa_bwd_dq_kernel": "prism_bsa_bwd_dq", "select_kernel": "prism_select_tiles",
+             "bsa_bwd_dq_kernel": "prism_bsa_bwd_dq", "bsa_fwd_quad_kernel": "prism_bsa_fwd_quad",
+             "bsa_bwd_dq_quad_kernel": "prism_bsa_bwd_dq_quad", "select_kernel": "prism_select_tiles",
              "gather_pool_kernel": "prism_gather_pool", "scatter_rows_kernel": "prism_scatter_rows",
              "block_scores_kernel": "prism_block_scores", "a2v_norms_kernel": "prism_a2v_norms",
              "zone_stats_kernel": "prism_zone_stats", "pair_union_kernel": "prism_pair_union"}
@@ -382,14 +383,23 @@ def summarize_counters(fetch_csv, write_csv, calib_fetch_csv, calib_write_csv):
     print(json.dumps(out), flush=True)
 
 
+def query_side_unions(plan):
+    """(union lists, tiles per union) the forward and dQ kernels walk: the
+    plan's quad unions when it has them, else its pair unions."""
+    quad = getattr(plan, "qquad", None)
+    return (quad, 4) if quad is not None else (plan.qunion, 2)
+
+
 def staged_tile_bytes(plan, D: int) -> dict:
     """Bytes the attention kernels copy into LDS per launch: one 64 x D bf16
-    tile of each operand per pair-union entry (forward and dQ: K and V over
-    the query-side unions; dK/dV: Q and dO plus the m2 and delta rows over the
-    key-side unions), whether the copy hits in L2 or not."""
+    tile of each operand per union entry (forward and dQ: K and V over the
+    query-side pair or quad unions; dK/dV: Q and dO plus the m2 and delta rows
+    over the key-side unions), whether the copy hits in L2 or not."""
     tile = 64 * D * 2
-    q_entries = int(plan.qunion[1].sum().item())
-    out = {"prism_bsa_fwd": 2 * tile * q_entries, "prism_bsa_bwd_dq": 2 * tile * q_entries}
+    qu, r = query_side_unions(plan)
+    q_entries = int(qu[1].sum().item())
+    sfx = "_quad" if r == 4 else ""
+    out = {"prism_bsa_fwd" + sfx: 2 * tile * q_entries, "prism_bsa_bwd_dq" + sfx: 2 * tile * q_entries}
     if plan.kunion is not None:
         out["prism_bsa_bwd_dkdv"] = (2 * tile + 2 * 64 * 4) * int(plan.kunion[1].sum().item())
     return out
@@ -654,10 +664,12 @@ def main():
     # attention kernels: algorithmic FLOPs per launch (executed in parentheses)
     attn = {"prism_bsa_fwd": (4 * fl, 4 * fl), "prism_bsa_bwd_dkdv": (8 * fl, 8 * fl),
             "prism_bsa_bwd_dq": (2 * fl, 6 * fl)}
+    attn.update({n + "_quad": attn[n] for n in ("prism_bsa_fwd", "prism_bsa_bwd_dq")})
     X = B * H * Sp * D * 2   # one bf16 [B,H,S_p,D] tile-order tensor (zone grid)
     Xin = B * H * S * D * 2  # one bf16 [B,H,S,D] THW tensor (input grid)
     nnz_tiles = int(plan.sel["ntiles"].sum().item())
-    union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
+    qu, per_union = query_side_unions(plan)
+    union_eff = sum_lens / max(1, per_union * int(qu[1].sum().item()))
     staged = staged_tile_bytes(plan, D)
     with torch.no_grad():
         plan.settle()
@@ -765,7 +777,8 @@ def main():
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(gp),
                    "audio_tokens": CONFIGS[args.config][4], "topk": inp["topk"], "cdf_threshold": cdf,
                    "sparsity": sparsity, "N_b": Nb, "sum_lens": sum_lens, "density": round(density, 4),
-                   "density_valid_q": round(density_valid, 4), "pair_union_efficiency": round(union_eff, 4),
+                   "density_valid_q": round(density_valid, 4), "union_slot_efficiency": round(union_eff, 4),
+                   "query_unions": "quad" if per_union == 4 else "pair",
                    "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3),
                    "ms_per_step_median": round(ms_median, 3),
                    "compact_lists": compact, "list_bytes": list_bytes, "list_bytes_peak": list_bytes_peak,
@@ -1015,7 +1028,8 @@ def run_uniform(args, inp):
         plan = plan_chunked(q.detach(), k.detach(), v.detach(), lq, lq, sparsity=sparsity, cdf_threshold=cdf,
                             sm_scale=1 / math.sqrt(D))
     sum_lens = plan.sum_lens()
-    union_eff = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
+    qu, per_union = query_side_unions(plan)
+    union_eff = sum_lens / max(1, per_union * int(qu[1].sum().item()))
     with torch.no_grad():
         plan.key_lists()
     staged = staged_tile_bytes(plan, D)
@@ -1023,6 +1037,7 @@ def run_uniform(args, inp):
     kept_flops = 14 * fl
     attn = {"prism_bsa_fwd": (4 * fl, 4 * fl), "prism_bsa_bwd_dkdv": (8 * fl, 8 * fl),
             "prism_bsa_bwd_dq": (2 * fl, 6 * fl)}
+    attn.update({n + "_quad": attn[n] for n in ("prism_bsa_fwd", "prism_bsa_bwd_dq")})
     X_in, X_rows = B * H * S * D * 2, B * H * lq.rows * D * 2
     hbm = {"prism_chunk_gather_pool": (4 * (X_in + X_rows) + X_rows) / 4,  # q, k, v, dO (+ O for delta)
            "prism_chunk_scatter_rows": X_rows + X_in,
@@ -1056,7 +1071,8 @@ def run_uniform(args, inp):
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(lq.pgrid), "chunk": list(chunk),
                    "topk": inp["topk"], "cdf_threshold": cdf, "sparsity": sparsity, "N_b": N_b,
                    "cpu_path_kept_tile_pairs": sum_lens,  # includes the padded query tiles the reference attends for "density": round(sum_lens / (B * H * lq.Nt * lq.Nt), 4),
-                   "pair_union_efficiency": round(union_eff, 4), "wall_ms_per_step": round(wall_ms, 3),
+                   "union_slot_efficiency": round(union_eff, 4),
+                   "query_unions": "quad" if per_union == 4 else "pair", "wall_ms_per_step": round(wall_ms, 3),
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12, 2),

@@ -243,8 +243,9 @@ int prism_pair_union(const int64_t* start, const int32_t* len, const int32_t* co
                      int64_t col_tiles, const int32_t* pairmap, const uint64_t* tile_masks, int64_t ucap,
                      int64_t* ustart, int32_t* ulen, int32_t* ucols, hipStream_t stream);
 
-/* Quad unions for prism_bsa_fwd_quad (no counterpart in the reference; its
- * forward kernel walks one query tile's list): rows of four tiles, quad q of a
+/* Quad unions for prism_bsa_fwd_quad and prism_bsa_bwd_dq_quad (no
+ * counterpart in the reference; its forward and dQ kernels walk one query
+ * tile's list): rows of four tiles, quad q of a
  * head being pairmap[4 q + k], k < 4 (four consecutive entries of a
  * prism_pair_tiles map: two pairs of a group), or rows 4 q + k.  Entries
  * tile << 5 | partial << 4 | member bits (bit k: row k lists the tile); rows %
@@ -377,6 +378,19 @@ int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do
                      const int32_t* ulen, const int32_t* ucols, const int32_t* pairmap, const int32_t* order,
                      float sm_scale, void* dq, int32_t* work_counter, hipStream_t stream);
 
+/* prism_bsa_bwd_dq over quad unions (prism_quad_union of the per-query-tile
+ * key lists; no counterpart in the reference, whose dQ kernel walks one query
+ * tile's list): one 8-wave workgroup per four query tiles, so each staged K /
+ * V tile serves up to 256 query rows.  quadmap: the pairmap the quad unions
+ * were built with (or NULL).  The same dq, bit for bit, as prism_bsa_bwd_dq
+ * over the pair unions of the same lists.  Sq a multiple of 256; order (or
+ * NULL) a permutation of the BH * Sq/256 quads; work_counter as for
+ * prism_bsa_bwd_dq. */
+int prism_bsa_bwd_dq_quad(const void* q, const void* k, const void* v, const void* do_, const float* m2,
+                          const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks,
+                          const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* quadmap,
+                          const int32_t* order, float sm_scale, void* dq, int32_t* work_counter, hipStream_t stream);
+
 /* ------------------------------------------------------------------ measured ceilings */
 
 /* Measurement aids of the benchmark's roofline (no counterpart in the
@@ -413,8 +427,8 @@ int prism_tile_stream_peak(const void* src, int64_t bytes, int64_t steps, uint32
  * quad, and flagged partial exactly where tile_masks[tile] is not all ones
  * (never when tile_masks is NULL).  Returns 1 (invalid argument) naming the
  * first violation.  With PRISM_DEBUG=1 in the environment, prism_bsa_fwd,
- * prism_bsa_fwd_quad, prism_bsa_bwd_dkdv, prism_bsa_bwd_dq, prism_pair_union
- * and prism_quad_union run these checks on host copies of their lists
+ * prism_bsa_fwd_quad, prism_bsa_bwd_dkdv, prism_bsa_bwd_dq,
+ * prism_bsa_bwd_dq_quad, prism_pair_union and prism_quad_union run these checks on host copies of their lists
  * (synchronising their stream) before launching anything, and return 1
  * without a launch when one fails. */
 int prism_check_lists(const int64_t* start, const int32_t* len, const int32_t* cols, int64_t rows, int64_t ncols,

@@ -52,6 +52,7 @@ SIGNATURES = {
     "prism_bwd_preprocess": [P, P, I64, I32, P, P],
     "prism_bsa_bwd_dkdv": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P, P],
     "prism_bsa_bwd_dq": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P],
+    "prism_bsa_bwd_dq_quad": [P, P, P, P, P, P, I32, I64, I64, I32, P, P, P, P, P, P, F32, P, P, P],
     "prism_check_lists": [P, P, P, I64, I64, I64, I32, P],
     "prism_mfma_peak": [I64, P, I64, P, P, P],
     "prism_copy_peak": [P, P, I64, P],

@@ -206,3 +206,7 @@ def _register_fakes():
     @reg("prism::bsa_bwd_dq")
     def _(q, k, v, do, m2, delta, tile_masks, ustart, ulen, ucols, pairmap, order, sm_scale):
         return _empty(q, q.shape, q.dtype)
+
+    @reg("prism::bsa_bwd_dq_quad")
+    def _(q, k, v, do, m2, delta, tile_masks, ustart, ulen, ucols, quadmap, order, sm_scale):
+        return _empty(q, q.shape, q.dtype)

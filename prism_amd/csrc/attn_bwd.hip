@@ -553,6 +553,228 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_kernel(BwdArgs a) {
   }
 }
 
+// ------------------------------------------------------------ dQ over quads
+// A QUAD of query tiles (two pairs of a zone) per 8-wave workgroup, one
+// workgroup per CU, over the quad's union list (prism_quad_union: entries
+// tile << 5 | partial << 4 | member bits), so each staged K / V tile serves up
+// to 256 query rows.  Wave w owns query rows [32 qh, 32 qh + 32) of quad tile
+// tq (qh = w & 1, tq = w >> 1) with the pair kernel's per-entry arithmetic;
+// waves w and w + 4 share a SIMD.  Four stages, the copies of entry j + 2
+// issued while entry j is multiplied, an eighth by every wave.  Group 0
+// (waves 0-3) takes entry j whole after its barrier (S^T and dP^T, then the
+// exponentials, dS and dQ).  Group 1 (waves 4-7) runs half an entry behind:
+// after the barrier it first finishes entry j - 1 (exponentials, dS and dQ
+// from the accumulators it carried across the barrier and the K tile still in
+// entry j - 1's stage), then issues its copies, then S^T and dP^T of entry j,
+// so on each SIMD one wave's exponentials run beside the other's MFMAs.
+// Every wave walks its own tile's entries in ascending order: dQ is
+// bit-identical to the pair kernel's.
+constexpr int kStagesDqQuad = 4, kAheadDqQuad = 2;
+
+template <int D>
+__device__ __forceinline__ void bsa_bwd_dq_quad(const BwdArgs& a, uint8_t* smem, int logical) {
+  using T = BwdTiles<D>;
+  using RT = typename T::RT;
+  constexpr int NS = D / 16, NDT = D / 32;
+  constexpr int SB = T::DQ_STAGE;
+  constexpr int PERW = T::SLOTS;  // KB-instructions per wave and stage (8 waves)
+  constexpr int NOFF = RT::KB / 4;
+
+  const int tid = opaque_thread_id(), lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int w = (int)uniform_u32((uint32_t)tid >> 6);
+  const int qh = w & 1, tq = w >> 1;
+  const int bh = logical / a.npairs, quad = logical - bh * a.npairs;  // npairs: quads per head
+  const int32_t* U = a.ucols + a.ustart[logical];
+  const int n = a.ulen[logical];
+  const int mybit = 1 << tq;
+  const int64_t qoff = (int64_t)bh * a.Sq * D, koff = (int64_t)bh * a.Sk * D;
+
+  // DMA plan: wave w issues KB-instructions w, w + 8, ... of each stage (K
+  // then V); instruction i + 4m of a tile reads 4096 m bytes past
+  // instruction i, so one lane offset serves all
+  const uint32_t soff = RT::src_offset(w & 3, lane);
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int ktile, int st) {
+    const int64_t toff = koff + (int64_t)ktile * 64 * D;
+    const char* kb = (const char*)uniform_ptr(a.k + toff);
+    const char* vb = (const char*)uniform_ptr(a.v + toff);
+    const uint32_t base = lds0 + (uint32_t)(st * SB);
+#pragma unroll
+    for (int s = 0; s < PERW; ++s) {
+      const int i = w + 8 * s;
+      const int t = i < RT::KB ? i : i - RT::KB;
+      dma_b128(soff, (i < RT::KB ? kb : vb) + 4096 * ((t >> 2) % NOFF), base + (uint32_t)i * 1024u);
+    }
+  };
+  RowOperand rop;  // K / V rows l32 (+ 32 kh as an immediate)
+  rop.init<RT>(0, l32, g);
+  TrOperand top;   // K^T over key rows 0 .. 63
+  top.init<RT>(0, lane);
+
+  EntryRing<kAheadDqQuad + 1> ring;
+  ring.init(U, n);
+#pragma unroll
+  for (int k = 0; k < kAheadDqQuad; ++k)
+    if (k < n) issue(ring.e[k] >> 5, k);
+
+  const int qslot = 4 * quad + tq;
+  const int qtile = a.pairmap ? a.pairmap[(int64_t)bh * 4 * a.npairs + qslot] : qslot;
+  const int64_t qrow = (int64_t)qtile * 64 + 32 * qh + l32;
+  bf16x8 qf[NS], df[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    qf[s] = ld_bf16x8(a.q + qoff + qrow * D + 16 * s + 8 * g);
+    df[s] = ld_bf16x8(a.do_ + qoff + qrow * D + 16 * s + 8 * g);
+  }
+  const float mq = a.m2[(int64_t)bh * a.Sq + qrow];
+  const float dlt = a.delta[(int64_t)bh * a.Sq + qrow];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    consume_regs(qf[s]);
+    consume_regs(df[s]);
+  }
+  consume_regs(mq);
+  consume_regs(dlt);
+  f32x16 ndl;  // -delta: the dP^T chains start from it (dP - delta)
+#pragma unroll
+  for (int r = 0; r < 16; ++r) ndl[r] = -dlt;
+  f32x16 dq[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) dq[dt] = f32x16_zero();
+
+  // S^T = K Q^T and dP^T - delta = V dO^T - delta (the pair kernel's ring of
+  // four row operands)
+  auto sdp_phase = [&](const uint8_t* sK, f32x16 (&sacc)[2], f32x16 (&pacc)[2]) {
+    const uint8_t* sV = sK + RT::BYTES;
+    sacc[0] = f32x16_zero();
+    sacc[1] = f32x16_zero();
+    pacc[0] = ndl;
+    pacc[1] = ndl;
+    constexpr int NO = 4 * NS, RING = 4;
+    bf16x8 op[RING];
+    auto rd = [&](int i) { return rop.load(((i & 1) ? sV : sK) + RT::rows(32 * ((i >> 1) & 1)), i >> 2); };
+#pragma unroll
+    for (int i = 0; i + 1 < RING; ++i) op[i] = rd(i);
+#pragma unroll
+    for (int i = 0; i < NO; ++i) {
+      if (i + RING - 1 < NO) op[(i + RING - 1) % RING] = rd(i + RING - 1);
+      const int kh = (i >> 1) & 1;
+      if (i & 1) pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[i % RING], df[i >> 2], pacc[kh], 0, 0, 0);
+      else sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[i % RING], qf[i >> 2], sacc[kh], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, RING - 1, 0);
+#pragma unroll
+    for (int i = 0; i + RING - 1 < NO; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, RING - 1, 0);
+  };
+  // key mask of a partial tile, P, dS = P (dP - delta) and dQ^T += K^T dS^T
+  // (the pair kernel's arithmetic and K^T operand ring)
+  auto ds_phase = [&](int e, const uint8_t* sK, f32x16 (&sacc)[2], f32x16 (&pacc)[2]) {
+    constexpr int NQ = 4 * NDT, RQ = 4;
+    bf16x8 kt[RQ];
+    auto rdk = [&](int i) { return top.load<RT>(sK, i / NDT, i % NDT); };
+#pragma unroll
+    for (int i = 0; i + 1 < RQ; ++i) kt[i] = rdk(i);
+    __builtin_amdgcn_s_setprio(1);
+    if (e & 16) {
+      const uint64_t mm = sload_u64(a.tmask + (e >> 5)) >> (4 * g);
+      const uint32_t lo = (uint32_t)mm, hi = (uint32_t)(mm >> 32);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int b = 8 * (r >> 2) + (r & 3);
+        sacc[0][r] = keep_or_ninf(sacc[0][r], lo, b);
+        sacc[1][r] = keep_or_ninf(sacc[1][r], hi, b);
+      }
+    }
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(__builtin_fmaf(sacc[kh][r], a.scale_log2, -mq));
+        pacc[kh][r] = p * pacc[kh][r];
+      }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const bf16x8 sb = b_from_acc(pacc, tt);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int i = tt * NDT + dt;
+        if (i + RQ - 1 < NQ) kt[(i + RQ - 1) % RQ] = rdk(i + RQ - 1);
+        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kt[i % RQ], sb, dq[dt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + RQ - 1 < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  if (w < 4) {
+    int st = 0;  // stage of entry j
+    for (int j = 0; j < n; ++j) {
+      const int e = ring.e[0], enext = ring.e[kAheadDqQuad];
+      ring.advance(U, n, j);
+      stage_wait<kAheadDqQuad + 1, PERW>(n - 1 - j);
+      __syncthreads();
+      if (j + kAheadDqQuad < n) issue(enext >> 5, (st + kAheadDqQuad) % kStagesDqQuad);
+      const uint8_t* sK = smem + st * SB;
+      st = st + 1 == kStagesDqQuad ? 0 : st + 1;
+      if (!(e & mybit)) continue;
+      f32x16 sacc[2], pacc[2];
+      sdp_phase(sK, sacc, pacc);
+      ds_phase(e, sK, sacc, pacc);
+    }
+  } else {
+    int st = 0;
+    int epend = 0;  // entry j - 1 if it waits for its dS and dQ, else 0
+    const uint8_t* spend = smem;
+    f32x16 sacc[2], pacc[2];
+    for (int j = 0; j < n; ++j) {
+      const int e = ring.e[0], enext = ring.e[kAheadDqQuad];
+      ring.advance(U, n, j);
+      stage_wait<kAheadDqQuad + 1, PERW>(n - 1 - j);
+      __syncthreads();
+      const int snext = (st + kAheadDqQuad) % kStagesDqQuad;
+      const uint8_t* sK = smem + st * SB;
+      st = st + 1 == kStagesDqQuad ? 0 : st + 1;
+      if (epend) ds_phase(epend, spend, sacc, pacc);
+      if (j + kAheadDqQuad < n) issue(enext >> 5, snext);
+      epend = (e & mybit) ? e : 0;
+      spend = sK;
+      if (epend) sdp_phase(sK, sacc, pacc);
+    }
+    if (epend) ds_phase(epend, spend, sacc, pacc);
+  }
+
+  uint16_t* dqr = a.dq + qoff + qrow * D;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      uint2 o;
+      o.x = pack_bf16(dq[dt][4 * jj + 0] * a.sm_scale, dq[dt][4 * jj + 1] * a.sm_scale);
+      o.y = pack_bf16(dq[dt][4 * jj + 2] * a.sm_scale, dq[dt][4 * jj + 3] * a.sm_scale);
+      *reinterpret_cast<uint2*>(dqr + 32 * dt + 8 * jj + 4 * g) = o;
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(512, 1) void bsa_bwd_dq_quad_kernel(BwdArgs a) {
+  __shared__ __align__(16) uint8_t smem[kStagesDqQuad * BwdTiles<D>::DQ_STAGE];
+  __shared__ WorkQueueState wq;
+  work_queue_init(&wq);
+  for (int pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : (int)blockIdx.x; pid >= 0;
+       pid = a.queue ? work_queue_take(a.queue, a.total, &wq) : -1) {
+    const BwdArgs ap = kernel_args<BwdArgs>();
+    bsa_bwd_dq_quad<D>(ap, smem, a.order ? a.order[pid] : xcd_group_remap<32>(pid, a.total));
+  }
+}
+
 // delta[row] = sum_d o[row][d] * do[row][d]: one wave per row, 4 rows per block
 template <int D>
 __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dO,
@@ -652,6 +874,38 @@ int prism_bsa_bwd_dq(const void* q, const void* k, const void* v, const void* do
   if (D == 128) bsa_bwd_dq_kernel<128><<<blocks, 256, 0, stream>>>(a);
   else bsa_bwd_dq_kernel<64><<<blocks, 256, 0, stream>>>(a);
   PRISM_LAUNCH_CHECK("prism_bsa_bwd_dq");
+  return PRISM_OK;
+}
+
+int prism_bsa_bwd_dq_quad(const void* q, const void* k, const void* v, const void* do_, const float* m2,
+                          const float* delta, int BH, int64_t Sq, int64_t Sk, int D, const uint64_t* tile_masks,
+                          const int64_t* ustart, const int32_t* ulen, const int32_t* ucols, const int32_t* quadmap,
+                          const int32_t* order, float sm_scale, void* dq, int32_t* work_counter, hipStream_t stream) {
+  int rc = check_common(q, k, BH, Sq, Sk, D, "prism_bsa_bwd_dq_quad");
+  if (rc) return rc;
+  PRISM_REQUIRE(v && do_ && m2 && delta && ustart && ulen && ucols && dq, "prism_bsa_bwd_dq_quad: null pointer");
+  PRISM_REQUIRE(Sq % 256 == 0, "prism_bsa_bwd_dq_quad: Sq must be a multiple of 256");
+  if (prism_debug_enabled()) {
+    PRISM_DEBUG_CHECK(prism_debug_check_lists("prism_bsa_bwd_dq_quad", ustart, ulen, ucols, (int64_t)BH * (Sq / 256),
+                                              Sk / 64, 2, tile_masks, stream));
+    PRISM_DEBUG_CHECK(prism_debug_check_maps("prism_bsa_bwd_dq_quad", quadmap, BH, Sq / 64, order,
+                                             (int64_t)BH * (Sq / 256), stream));
+  }
+  BwdArgs a = {};
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.do_ = (const uint16_t*)do_;
+  a.m2 = m2; a.delta = delta; a.tmask = tile_masks;
+  a.ustart = ustart; a.ulen = ulen; a.ucols = ucols; a.pairmap = quadmap; a.order = order; a.Sq = Sq; a.Sk = Sk;
+  a.npairs = (int)(Sq / 256);  // quads per head
+  a.sm_scale = sm_scale; a.scale_log2 = sm_scale * kLog2e; a.dq = (uint16_t*)dq;
+  a.total = (int)((int64_t)BH * a.npairs);
+  a.queue = work_counter;
+  if (a.queue) zero_counter_kernel<<<1, kQueueLanes, 0, stream>>>(a.queue);
+  const int res = !a.queue ? 0 : D == 128 ? resident_workgroups<bsa_bwd_dq_quad_kernel<128>>(512)
+                                          : resident_workgroups<bsa_bwd_dq_quad_kernel<64>>(512);
+  const unsigned blocks = (unsigned)(a.queue && res < a.total ? res : a.total);
+  if (D == 128) bsa_bwd_dq_quad_kernel<128><<<blocks, 512, 0, stream>>>(a);
+  else bsa_bwd_dq_quad_kernel<64><<<blocks, 512, 0, stream>>>(a);
+  PRISM_LAUNCH_CHECK("prism_bsa_bwd_dq_quad");
   return PRISM_OK;
 }
 

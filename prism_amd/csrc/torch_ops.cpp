@@ -671,9 +671,10 @@ std::tuple<Tensor, Tensor> bsa_bwd_dkdv(const Tensor& q_, const Tensor& k_, cons
   return {dk, dv};
 }
 
-Tensor bsa_bwd_dq(const Tensor& q_, const Tensor& k_, const Tensor& v_, const Tensor& do_, const Tensor& m2_,
-                  const Tensor& delta_, const OptT& masks_, const Tensor& us_, const Tensor& ul_, const Tensor& uc_,
-                  const OptT& pairmap_, const OptT& order_, double sm_scale) {
+// dQ over pair unions (quad = false) or quad unions (quad = true)
+Tensor bsa_bwd_dq_any(const Tensor& q_, const Tensor& k_, const Tensor& v_, const Tensor& do_, const Tensor& m2_,
+                      const Tensor& delta_, const OptT& masks_, const Tensor& us_, const Tensor& ul_, const Tensor& uc_,
+                      const OptT& pairmap_, const OptT& order_, double sm_scale, bool quad) {
   const AttnShape s = attn_shape(q_, k_, v_);
   check_union(us_, ul_, uc_);
   on_gpu(do_, "do");
@@ -692,11 +693,24 @@ Tensor bsa_bwd_dq(const Tensor& q_, const Tensor& k_, const Tensor& v_, const Te
   const Tensor us = us_.contiguous(), ul = ul_.contiguous(), uc = uc_.contiguous();
   const OptT masks = cont(masks_), pairmap = cont(pairmap_), order = cont(order_);
   Tensor dq = at::empty_like(q);
-  PRISM_TORCH_CALL(prism_bsa_bwd_dq, q.data_ptr(), k.data_ptr(), v.data_ptr(), d.data_ptr(), m2.data_ptr<float>(),
+  auto fn = quad ? &prism_bsa_bwd_dq_quad : &prism_bsa_bwd_dq;
+  PRISM_TORCH_CALL(fn, q.data_ptr(), k.data_ptr(), v.data_ptr(), d.data_ptr(), m2.data_ptr<float>(),
                    delta.data_ptr<float>(), (int)(s.B * s.H), s.Sq, s.Sk, (int)s.D, (const uint64_t*)p(masks),
                    us.data_ptr<int64_t>(), ul.data_ptr<int32_t>(), uc.data_ptr<int32_t>(), (const int32_t*)p(pairmap),
                    (const int32_t*)p(order), (float)sm_scale, dq.data_ptr(), work_counter(q).data_ptr<int32_t>(), stream_of(q));
   return dq;
+}
+
+Tensor bsa_bwd_dq(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& d, const Tensor& m2,
+                  const Tensor& delta, const OptT& masks, const Tensor& us, const Tensor& ul, const Tensor& uc,
+                  const OptT& pairmap, const OptT& order, double sm_scale) {
+  return bsa_bwd_dq_any(q, k, v, d, m2, delta, masks, us, ul, uc, pairmap, order, sm_scale, false);
+}
+
+Tensor bsa_bwd_dq_quad(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& d, const Tensor& m2,
+                       const Tensor& delta, const OptT& masks, const Tensor& us, const Tensor& ul, const Tensor& uc,
+                       const OptT& quadmap, const OptT& order, double sm_scale) {
+  return bsa_bwd_dq_any(q, k, v, d, m2, delta, masks, us, ul, uc, quadmap, order, sm_scale, true);
 }
 
 }  // namespace
@@ -744,6 +758,8 @@ TORCH_LIBRARY(prism, m) {
         "Tensor ustart, Tensor ulen, Tensor ucols, Tensor? pairmap, Tensor? order, float sm_scale) -> (Tensor, Tensor)");
   m.def("bsa_bwd_dq(Tensor q, Tensor k, Tensor v, Tensor do, Tensor m2, Tensor delta, Tensor? tile_masks, "
         "Tensor ustart, Tensor ulen, Tensor ucols, Tensor? pairmap, Tensor? order, float sm_scale) -> Tensor");
+  m.def("bsa_bwd_dq_quad(Tensor q, Tensor k, Tensor v, Tensor do, Tensor m2, Tensor delta, Tensor? tile_masks, "
+        "Tensor ustart, Tensor ulen, Tensor ucols, Tensor? quadmap, Tensor? order, float sm_scale) -> Tensor");
 }
 
 // GPU tensors of the ROCm build dispatch under torch's CUDA key
@@ -779,4 +795,5 @@ TORCH_LIBRARY_IMPL(prism, CUDA, m) {
   m.impl("bwd_preprocess", &bwd_preprocess);
   m.impl("bsa_bwd_dkdv", &bsa_bwd_dkdv);
   m.impl("bsa_bwd_dq", &bsa_bwd_dq);
+  m.impl("bsa_bwd_dq_quad", &bsa_bwd_dq_quad);
 }

@@ -92,17 +92,22 @@ class _Plan:
         # pair the query tiles of each zone by list overlap (fewest idle wave slots)
         self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lay.Nt)
         self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks, pairmap=self.qpair)
-        self._csr = ops.DeferredCompaction(2) if compact_lists else None
+        self._csr = ops.DeferredCompaction(3) if compact_lists else None
         if compact_lists:
             self._csr.add(0, self.qunion)
         # launch order of the forward and dQ kernels (the last workgroups ids
         # take the longest lists first: the launch does not end on a long one)
         self.qorder = ops.pair_order(self.qunion[1], 64)
-        # the forward's quad unions (two pairs of a zone per workgroup), used
-        # once by the forward kernel and released after it
-        self.qquad = self.qquad_order = None
-        if ops.FWD_QUAD and lay.Nt % 4 == 0:
-            self.qquad = ops.quad_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks, pairmap=self.qpair)
+        # quad unions (two pairs of a zone per workgroup: four query tiles per
+        # staged K / V tile), which the forward and dQ kernels walk instead of
+        # the pair unions when ops.QUADS is set (same results, bit for bit)
+        self.qquad = self.qquad_order = self.qquadmap = None
+        if ops.QUADS and lay.Nt % 4 == 0:
+            self.qquadmap = self.qpair
+            self.qquad = ops.quad_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks,
+                                        pairmap=self.qquadmap)
+            if compact_lists:
+                self._csr.add(2, self.qquad)
             self.qquad_order = ops.pair_order(self.qquad[1], 32)
         self.klists = None
         self.kpair = None
@@ -151,7 +156,11 @@ class _Plan:
             return
         self.build_key_lists()
         if self._csr is not None:
-            self.qunion, self.kunion = self._csr.finish([self.qunion, self.kunion])
+            lists = [self.qunion, self.kunion] + ([self.qquad] if self.qquad is not None else [])
+            done = self._csr.finish(lists)
+            self.qunion, self.kunion = done[:2]
+            if self.qquad is not None:
+                self.qquad = done[2]
             self._csr = None
         self.qcols = None
         self.klists = None
@@ -161,6 +170,8 @@ class _Plan:
     def list_bytes(self) -> int:
         """Bytes of the work lists the plan holds."""
         ts = [*self.qunion, self.qstart, self.qlen]
+        if self.qquad is not None:
+            ts += list(self.qquad)
         if self.qcols is not None:
             ts.append(self.qcols)
         if self.kunion is not None:
@@ -190,8 +201,7 @@ class _DynBSA(torch.autograd.Function):
                 plan.build_key_lists()
         if plan.qquad is not None:
             o_re, lse = ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qquad, sm_scale,
-                                         plan.qpair, plan.qquad_order)
-            plan.qquad = plan.qquad_order = None
+                                         plan.qquadmap, plan.qquad_order)
         else:
             o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
                                     plan.qorder)
@@ -223,9 +233,12 @@ class _DynBSA(torch.autograd.Function):
                     dk_re.device, lambda: (ops.scatter_rows(dk_re, lay, tk), ops.scatter_rows(dv_re, lay, tv)),
                     reads=(dk_re, dv_re), produces=lambda out: out)
 
+        quads = plan.qquad is not None
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid,
-                                          plan.tmasks, plan.qunion, plan.kunion, ctx.sm_scale, plan.qpair, plan.kpair,
-                                          plan.qorder, plan.korder, after_dkdv=scatter_dkdv)
+                                          plan.tmasks, plan.qquad if quads else plan.qunion, plan.kunion,
+                                          ctx.sm_scale, plan.qquadmap if quads else plan.qpair, plan.kpair,
+                                          plan.qquad_order if quads else plan.qorder, plan.korder,
+                                          after_dkdv=scatter_dkdv, q_quads=quads)
         dq = ops.scatter_rows(dq_re, lay, tq)
         if "dkdv" in side:
             (dk, dv), done = side["dkdv"]

@@ -457,7 +457,8 @@ class DeferredCompaction:
         self.offsets[i], self.events[i] = off, ev
 
     def finish(self, lists_seq):
-        for ev in self.events:
+        """lists_seq[i]: the lists added as i (slots never added are left out)."""
+        for ev in self.events[:len(lists_seq)]:
             ev.synchronize()
         nnz = self.host.tolist()
         return [(*csr_lists(self.offsets[i]), csr_fill(*lists, self.offsets[i], nnz[i]))
@@ -624,10 +625,10 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 OVERLAP_SIDE_WORK = True
 OVERLAP_DKDV_SCATTER = False
 
-# The forward over quad unions (bsa_fwd_quad: four query tiles per staged K / V
-# tile, bit-identical to bsa_fwd) when the query tiles per head are a multiple
-# of 4.
-FWD_QUAD = os.environ.get("PRISM_FWD_QUAD", "0") not in ("", "0")
+# The forward and dQ over quad unions (bsa_fwd_quad, bsa_bwd_dq_quad: four
+# query tiles per staged K / V tile, bit-identical to bsa_fwd and bsa_bwd_dq)
+# when the query tiles per head are a multiple of 4.
+QUADS = os.environ.get("PRISM_QUADS", "0") not in ("", "0")
 
 
 def side_launch(device: torch.device, fn, reads=(), produces=None):
@@ -653,12 +654,15 @@ def side_launch(device: torch.device, fn, reads=(), produces=None):
 
 def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: float,
             qpair: Optional[torch.Tensor] = None, kpair: Optional[torch.Tensor] = None,
-            qorder: Optional[torch.Tensor] = None, korder: Optional[torch.Tensor] = None, after_dkdv=None):
+            qorder: Optional[torch.Tensor] = None, korder: Optional[torch.Tensor] = None, after_dkdv=None,
+            q_quads: bool = False):
     """Backward over tile-order bf16 tensors; qunion / kunion = pair unions of
     the per-query-tile key lists and of the per-key-tile query lists, built
-    with the pairings qpair / kpair (None: neighbouring tiles).  Returns
-    dq, dk, dv (bf16, tile order).  after_dkdv(dk, dv), if given, is called
-    between the dK/dV and the dQ launches."""
+    with the pairings qpair / kpair (None: neighbouring tiles).  With q_quads,
+    qunion is the quad_union of the per-query-tile lists (quadmap qpair,
+    launch order qorder over quads) and dQ runs over quads (bit-identical).
+    Returns dq, dk, dv (bf16, tile order).  after_dkdv(dk, dv), if given, is
+    called between the dK/dV and the dQ launches."""
     _cuda(q, k, v, do, m2, delta, kv_valid, tmasks, qpair, kpair, qorder, korder)
     q, k, v, do = _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"), _bf16(do, "do")
     B, H, Sq, Sk, D = _attn_shapes(q, k, v)
@@ -683,8 +687,8 @@ def bsa_bwd(q, k, v, do, m2, delta, kv_valid, tmasks, qunion, kunion, sm_scale: 
         dk, dv = dkdv()
     if after_dkdv is not None:
         after_dkdv(dk, dv)
-    dq = _op("bsa_bwd_dq", q, k, v, do, m2, delta, tmasks, qunion[0], qunion[1], qunion[2], qpair, qorder,
-             float(sm_scale))
+    dq = _op("bsa_bwd_dq_quad" if q_quads else "bsa_bwd_dq", q, k, v, do, m2, delta, tmasks, qunion[0], qunion[1],
+             qunion[2], qpair, qorder, float(sm_scale))
     if BWD_CONCURRENT:
         main.wait_stream(side)
     return dq, dk, dv

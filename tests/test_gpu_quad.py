@@ -1,10 +1,11 @@
-"""The quad forward (prism_bsa_fwd_quad over prism_quad_union lists, one
-8-wave workgroup per four query tiles) against the pair forward
-(prism_bsa_fwd over prism_pair_union lists) on the same per-query-tile key
-lists: every query row walks its own list in the same order with the same
-arithmetic, so O and LSE must agree bit for bit.  Cases: D = 64 and 128,
-padded grids (partial key tiles) and unpadded, a launch order and none,
-lists with empty rows, and config 4's full-size lists."""
+"""The quad kernels (prism_bsa_fwd_quad and prism_bsa_bwd_dq_quad over
+prism_quad_union lists, one 8-wave workgroup per four query tiles) against
+the pair kernels (prism_bsa_fwd, prism_bsa_bwd_dq over prism_pair_union
+lists) on the same per-query-tile key lists: every query row walks its own
+list in the same order with the same arithmetic, so O, LSE and dQ must agree
+bit for bit.  Cases: D = 64 and 128, padded grids (partial key tiles) and
+unpadded, a launch order and none, lists with empty rows, config 4's
+full-size lists, and the autograd path with quads on and off."""
 import math
 
 import numpy as np
@@ -17,7 +18,7 @@ from tests.test_gpu_parity import CASES, bits_equal, dev, host, make, say
 pytestmark = pytest.mark.gpu
 
 
-def _quad_vs_pair(plan, D, with_order=True):
+def _quad_vs_pair(plan, D, with_order=True, seed=5):
     from prism_amd import ops
     sm = 1.0 / math.sqrt(D)
     o1, l1 = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm, plan.qpair, plan.qorder)
@@ -27,6 +28,18 @@ def _quad_vs_pair(plan, D, with_order=True):
     torch.cuda.synchronize()
     assert bits_equal(host(o2), host(o1)), "O"
     assert bits_equal(host(l2), host(l1)), "LSE"
+    # dQ over the quads against dQ over the pairs (dK / dV: the same launch)
+    plan.build_key_lists()
+    do = torch.randn(plan.q_re.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(seed))
+    do = do.to(torch.bfloat16)
+    m2, delta = ops.lse_to_m2(l1), ops.bwd_preprocess(o1, do)
+    g1 = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do, m2, delta, plan.kv_valid, plan.tmasks, plan.qunion,
+                     plan.kunion, sm, plan.qpair, plan.kpair, plan.qorder, plan.korder)
+    g2 = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do, m2, delta, plan.kv_valid, plan.tmasks, quad,
+                     plan.kunion, sm, plan.qpair, plan.kpair, order, plan.korder, q_quads=True)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dQ", "dK", "dV"), g2, g1):
+        assert bits_equal(host(a), host(b)), name
     return quad
 
 
@@ -84,3 +97,26 @@ def test_quad_forward_bitexact_fullsize_c4():
                             audio_token_norms=norms, input_grid=grid)
     say("quad fullsize c4: attention")
     _quad_vs_pair(plan, inp["D"])
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[-1]], ids=[CASES[0][0], CASES[-1][0]])
+def test_quads_autograd_identical(case, monkeypatch):
+    """flash_attn_bsa_3d_dynamic with ops.QUADS on and off: the same output
+    and q, k, v gradients, bit for bit (the plan's quad unions feed the
+    forward and dQ kernels)."""
+    from prism_amd import flash_attn_bsa_3d_dynamic, ops
+    c = make(case)
+    say("quads autograd", case)
+    valid = dev(c["valid"]).bool() if c["pad"] else None
+    outs = []
+    for quads in (False, True):
+        monkeypatch.setattr(ops, "QUADS", quads)
+        q, k, v = (dev(c[n]).requires_grad_(True) for n in ("qh", "kh", "vh"))
+        o = flash_attn_bsa_3d_dynamic(q, k, v, c["grid"], method="ivpq", sparsity=0.6, cdf_threshold=0.9,
+                                      valid_mask=valid)
+        assert (o.grad_fn.plan.qquad is not None) == (quads and o.grad_fn.plan.lay.Nt % 4 == 0)
+        o.backward(torch.randn(o.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(3))
+                   .to(o.dtype))
+        outs.append([host(t) for t in (o, q.grad, k.grad, v.grad)])
+    for name, a, b in zip(("O", "dQ", "dK", "dV"), *outs):
+        assert bits_equal(a, b), name
