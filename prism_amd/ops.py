@@ -627,8 +627,11 @@ OVERLAP_DKDV_SCATTER = False
 
 # The forward and dQ over quad unions (bsa_fwd_quad, bsa_bwd_dq_quad: four
 # query tiles per staged K / V tile, bit-identical to bsa_fwd and bsa_bwd_dq)
-# when the query tiles per head are a multiple of 4.
-QUADS = os.environ.get("PRISM_QUADS", "0") not in ("", "0")
+# when the query tiles per head are a multiple of 4; PRISM_QUADS=0 keeps the
+# pair kernels.  At config 4 the quads stage 42% fewer tile bytes: forward
+# 52.5 -> 49.7 ms, dQ 59.7 -> 59.4 ms (the quads' idle wave slots, 24%
+# against 8% for pairs, take back most of what the smaller stream saves).
+QUADS = os.environ.get("PRISM_QUADS", "1") not in ("", "0")
 
 
 def side_launch(device: torch.device, fn, reads=(), produces=None):
