@@ -77,6 +77,11 @@ def test_opcheck_selection_and_lists(plan):
     _check("pair_tiles", p.qstart, p.qlen, p.qcols, lay.Nt, lay.Nt)
     _check("pair_union", p.qstart, p.qlen, p.qcols, lay.Nt, lay.Nt, p.qpair, p.tmasks)
     _check("pair_order", p.qunion[1], 64, 8)
+    assert lay.Nt % 4 == 0
+    _check("quad_union", p.qstart, p.qlen, p.qcols, lay.Nt, lay.Nt, p.qpair, p.tmasks)
+    _check("lists_csr_offsets", p.qlen)
+    off, total = torch.ops.prism.lists_csr_offsets(p.qlen)
+    _check("lists_csr_fill", p.qstart, p.qlen, p.qcols, off, int(total.item()))
     # (data-dependent output length: schema check; the fake's symbolic size is
     # covered on the CPU)
     print("[case] opcheck lists_to_csr", flush=True)
@@ -102,6 +107,10 @@ def test_opcheck_attention(plan):
     ku = ops.pair_union(*kl, Nt)
     _check("bsa_bwd_dkdv", p.q_re, p.k_re, p.v_re, do, m2, delta, p.kv_valid, *ku, None, None, sm)
     _check("bsa_bwd_dq", p.q_re, p.k_re, p.v_re, do, m2, delta, p.tmasks, *p.qunion, p.qpair, p.qorder, sm)
+    quad = ops.quad_union(p.qstart, p.qlen, p.qcols, Nt, p.tmasks, pairmap=p.qpair)
+    qorder = ops.pair_order(quad[1], 32)
+    _check("bsa_fwd_quad", p.q_re, p.k_re, p.v_re, p.tmasks, *quad, p.qpair, qorder, sm)
+    _check("bsa_bwd_dq_quad", p.q_re, p.k_re, p.v_re, do, m2, delta, p.tmasks, *quad, p.qpair, qorder, sm)
 
 
 def test_errors_come_back_as_python_exceptions():
