@@ -383,26 +383,35 @@ def summarize_counters(fetch_csv, write_csv, calib_fetch_csv, calib_write_csv):
     print(json.dumps(out), flush=True)
 
 
-def query_side_unions(plan):
-    """(union lists, tiles per union) the forward and dQ kernels walk: the
-    plan's quad unions when it has them, else its pair unions."""
-    quad = getattr(plan, "qquad", None)
-    return (quad, 4) if quad is not None else (plan.qunion, 2)
-
-
 def staged_tile_bytes(plan, D: int) -> dict:
     """Bytes the attention kernels copy into LDS per launch: one 64 x D bf16
     tile of each operand per union entry (forward and dQ: K and V over the
     query-side pair or quad unions; dK/dV: Q and dO plus the m2 and delta rows
     over the key-side unions), whether the copy hits in L2 or not."""
     tile = 64 * D * 2
-    qu, r = query_side_unions(plan)
-    q_entries = int(qu[1].sum().item())
-    sfx = "_quad" if r == 4 else ""
-    out = {"prism_bsa_fwd" + sfx: 2 * tile * q_entries, "prism_bsa_bwd_dq" + sfx: 2 * tile * q_entries}
+    q_entries = int(plan.qunion[1].sum().item())
+    out = {"prism_bsa_fwd": 2 * tile * q_entries, "prism_bsa_bwd_dq": 2 * tile * q_entries}
+    quad = getattr(plan, "qquad", None)
+    if quad is not None:
+        quad_entries = int(quad[1].sum().item())
+        out.update({"prism_bsa_fwd_quad": 2 * tile * quad_entries, "prism_bsa_bwd_dq_quad": 2 * tile * quad_entries})
     if plan.kunion is not None:
         out["prism_bsa_bwd_dkdv"] = (2 * tile + 2 * 64 * 4) * int(plan.kunion[1].sum().item())
     return out
+
+
+def slot_efficiency(plan, sum_lens: int) -> dict:
+    """Fraction of the wave-tile slots of the forward and dQ kernels that do
+    math: Σlens over (tiles per union) x (union entries), for the pair unions
+    and, when the plan has them, the quad unions; and which unions the
+    forward and dQ launches of the plan walk."""
+    pair = sum_lens / max(1, 2 * int(plan.qunion[1].sum().item()))
+    quad = getattr(plan, "qquad", None)
+    qeff = None if quad is None else sum_lens / max(1, 4 * int(quad[1].sum().item()))
+    walk = {"forward": "quad" if getattr(plan, "quads", False) else "pair",
+            "dq": "quad" if getattr(plan, "dq_quads", False) else "pair"}
+    return {"union_slot_efficiency": round(pair, 4),
+            "quad_union_slot_efficiency": None if qeff is None else round(qeff, 4), "query_unions": walk}
 
 
 def measured_traffic(kernel: str):
@@ -657,7 +666,7 @@ def main():
     density = sum_lens / (B * H * Nt * Nt)
     n_qvalid = int((plan.tile_count > 0).sum().item()) if plan.tile_count is not None else Nt
     density_valid = sum_lens / (B * H * n_qvalid * Nt)  # over query tiles holding a valid token
-    # fraction of (wave, key tile) slots of the paired-tile kernels that do math (union_eff, below)
+    # fraction of (wave, key tile) slots of the forward and dQ kernels that do math (slot_efficiency, below)
     fl = 64 * 64 * D * sum_lens  # one 64x64xD product over all kept tile pairs
     kept_flops = (4 if fwd_only else 14) * fl  # FA convention: fwd 4, bwd 10
 
@@ -668,8 +677,7 @@ def main():
     X = B * H * Sp * D * 2   # one bf16 [B,H,S_p,D] tile-order tensor (zone grid)
     Xin = B * H * S * D * 2  # one bf16 [B,H,S,D] THW tensor (input grid)
     nnz_tiles = int(plan.sel["ntiles"].sum().item())
-    qu, per_union = query_side_unions(plan)
-    union_eff = sum_lens / max(1, per_union * int(qu[1].sum().item()))
+    slots = slot_efficiency(plan, sum_lens)
     staged = staged_tile_bytes(plan, D)
     with torch.no_grad():
         plan.settle()
@@ -777,8 +785,7 @@ def main():
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(gp),
                    "audio_tokens": CONFIGS[args.config][4], "topk": inp["topk"], "cdf_threshold": cdf,
                    "sparsity": sparsity, "N_b": Nb, "sum_lens": sum_lens, "density": round(density, 4),
-                   "density_valid_q": round(density_valid, 4), "union_slot_efficiency": round(union_eff, 4),
-                   "query_unions": "quad" if per_union == 4 else "pair",
+                   "density_valid_q": round(density_valid, 4), **slots,
                    "mfma_util_step": round(value / PEAK_BF16_TFLOPS, 4), "wall_ms_per_step": round(wall_ms, 3),
                    "ms_per_step_median": round(ms_median, 3),
                    "compact_lists": compact, "list_bytes": list_bytes, "list_bytes_peak": list_bytes_peak,
@@ -1028,8 +1035,7 @@ def run_uniform(args, inp):
         plan = plan_chunked(q.detach(), k.detach(), v.detach(), lq, lq, sparsity=sparsity, cdf_threshold=cdf,
                             sm_scale=1 / math.sqrt(D))
     sum_lens = plan.sum_lens()
-    qu, per_union = query_side_unions(plan)
-    union_eff = sum_lens / max(1, per_union * int(qu[1].sum().item()))
+    slots = slot_efficiency(plan, sum_lens)
     with torch.no_grad():
         plan.key_lists()
     staged = staged_tile_bytes(plan, D)
@@ -1071,8 +1077,7 @@ def run_uniform(args, inp):
                    "B": B, "H": H, "D": D, "grid": list(grid), "grid_padded": list(lq.pgrid), "chunk": list(chunk),
                    "topk": inp["topk"], "cdf_threshold": cdf, "sparsity": sparsity, "N_b": N_b,
                    "cpu_path_kept_tile_pairs": sum_lens,  # includes the padded query tiles the reference attends for "density": round(sum_lens / (B * H * lq.Nt * lq.Nt), 4),
-                   "union_slot_efficiency": round(union_eff, 4),
-                   "query_unions": "quad" if per_union == 4 else "pair", "wall_ms_per_step": round(wall_ms, 3),
+                   **slots, "wall_ms_per_step": round(wall_ms, 3),
                    "attention_ms": round(att_ms, 3),
                    "attention_mfma_util": round(kept_flops / (att_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(attn[dom][0] / (dom_ms * 1e-3) / 1e12, 2),

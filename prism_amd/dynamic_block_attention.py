@@ -102,11 +102,14 @@ class _Plan:
         # staged K / V tile), which the forward and dQ kernels walk instead of
         # the pair unions when ops.QUADS is set (same results, bit for bit)
         self.qquad = self.qquad_order = self.qquadmap = None
-        if ops.QUADS and lay.Nt % 4 == 0:
+        # dq_quads: dQ walks them too, so the backward keeps them
+        self.quads = ops.QUADS and lay.Nt % 4 == 0
+        self.dq_quads = self.quads and ops.DQ_QUADS
+        if self.quads:
             self.qquadmap = self.qpair
             self.qquad = ops.quad_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks,
                                         pairmap=self.qquadmap)
-            if compact_lists:
+            if compact_lists and self.dq_quads:
                 self._csr.add(2, self.qquad)
             self.qquad_order = ops.pair_order(self.qquad[1], 32)
         self.klists = None
@@ -149,19 +152,22 @@ class _Plan:
 
     def settle(self):
         """Keep only what the backward reads: the query-side and key-side pair
-        unions (compact CSR when the plan is compact, with one batched host
-        read of their nnz), pairings and launch orders.  The per-tile lists
-        (1.0 GB query-side and 0.66 GB key-side at config 4) are released."""
+        unions, and the quad unions when dQ walks them (compact CSR when the
+        plan is compact, with one batched host read of their nnz), pairings
+        and launch orders.  The per-tile lists (1.0 GB query-side and 0.66 GB
+        key-side at config 4) and the forward-only quad unions are released."""
         if self._settled:
             return
         self.build_key_lists()
         if self._csr is not None:
-            lists = [self.qunion, self.kunion] + ([self.qquad] if self.qquad is not None else [])
+            lists = [self.qunion, self.kunion] + ([self.qquad] if self.dq_quads else [])
             done = self._csr.finish(lists)
             self.qunion, self.kunion = done[:2]
-            if self.qquad is not None:
+            if self.dq_quads:
                 self.qquad = done[2]
             self._csr = None
+        if not self.dq_quads:  # the forward's only: released once it is queued
+            self.qquad = self.qquad_order = None
         self.qcols = None
         self.klists = None
         self.sel = {key: val for key, val in self.sel.items() if key != "tiles"}
@@ -233,7 +239,7 @@ class _DynBSA(torch.autograd.Function):
                     dk_re.device, lambda: (ops.scatter_rows(dk_re, lay, tk), ops.scatter_rows(dv_re, lay, tv)),
                     reads=(dk_re, dv_re), produces=lambda out: out)
 
-        quads = plan.qquad is not None
+        quads = plan.dq_quads
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, do_re, m2, delta, plan.kv_valid,
                                           plan.tmasks, plan.qquad if quads else plan.qunion, plan.kunion,
                                           ctx.sm_scale, plan.qquadmap if quads else plan.qpair, plan.kpair,

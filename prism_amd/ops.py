@@ -625,13 +625,17 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 OVERLAP_SIDE_WORK = True
 OVERLAP_DKDV_SCATTER = False
 
-# The forward and dQ over quad unions (bsa_fwd_quad, bsa_bwd_dq_quad: four
-# query tiles per staged K / V tile, bit-identical to bsa_fwd and bsa_bwd_dq)
-# when the query tiles per head are a multiple of 4; PRISM_QUADS=0 keeps the
-# pair kernels.  At config 4 the quads stage 42% fewer tile bytes: forward
-# 52.5 -> 49.7 ms, dQ 59.7 -> 59.4 ms (the quads' idle wave slots, 24%
-# against 8% for pairs, take back most of what the smaller stream saves).
+# The forward over quad unions (bsa_fwd_quad: four query tiles per staged K /
+# V tile, bit-identical to bsa_fwd) when the query tiles per head are a
+# multiple of 4; PRISM_QUADS=0 keeps the pair kernel.  With DQ_QUADS
+# (PRISM_DQ_QUADS=1) dQ walks the quad unions too (bsa_bwd_dq_quad,
+# bit-identical to bsa_bwd_dq), and the plan keeps them for the backward.
+# The quads stage 42% fewer tile bytes but leave more wave slots idle (24%
+# against 8% for pairs at config 4): forward 52.5 -> 49.7 ms there, dQ
+# 59.7 -> 59.4 ms; on the uniform path (35% idle) forward 56.1-57.0 -> 52.1
+# ms but dQ 60.6-60.7 -> 61.5 ms, so dQ stays on pairs by default.
 QUADS = os.environ.get("PRISM_QUADS", "1") not in ("", "0")
+DQ_QUADS = os.environ.get("PRISM_DQ_QUADS", "0") not in ("", "0")
 
 
 def side_launch(device: torch.device, fn, reads=(), produces=None):

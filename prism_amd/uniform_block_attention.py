@@ -79,11 +79,25 @@ class _ChunkPlan:
         self.qpair = ops.pair_tiles(self.qstart, self.qlen, self.qcols, lq.Nt, lk.Nt)
         self.qunion = ops.pair_union(self.qstart, self.qlen, self.qcols, lq.Nt, self.tmasks, col_tiles=lk.Nt,
                                      pairmap=self.qpair)
-        self._csr = ops.DeferredCompaction(2) if compact_lists else None
+        self._csr = ops.DeferredCompaction(3) if compact_lists else None
         if compact_lists:
             self._csr.add(0, self.qunion)
         # launch order of the forward and dQ kernels (longest lists last-dispatched first)
         self.qorder = ops.pair_order(self.qunion[1], 64)
+        # quad unions (two pairs per workgroup), which the forward and dQ
+        # kernels walk instead of the pair unions when ops.QUADS is set (same
+        # results, bit for bit)
+        self.qquad = self.qquad_order = self.qquadmap = None
+        # dq_quads: dQ walks them too, so the backward keeps them
+        self.quads = ops.QUADS and lq.Nt % 4 == 0
+        self.dq_quads = self.quads and ops.DQ_QUADS
+        if self.quads:
+            self.qquadmap = self.qpair
+            self.qquad = ops.quad_union(self.qstart, self.qlen, self.qcols, lq.Nt, self.tmasks, col_tiles=lk.Nt,
+                                        pairmap=self.qquadmap)
+            if compact_lists and self.dq_quads:
+                self._csr.add(2, self.qquad)
+            self.qquad_order = ops.pair_order(self.qquad[1], 32)
         self.klists = None
         self.kpair = None
         self.kunion = None
@@ -120,15 +134,22 @@ class _ChunkPlan:
         return self.kunion
 
     def settle(self):
-        """Keep only what the backward reads: both pair unions (compact CSR
-        when the plan is compact, one batched host read of their nnz),
-        pairings and launch orders; the per-tile lists are released."""
+        """Keep only what the backward reads: the pair unions, and the quad
+        unions when dQ walks them (compact CSR when the plan is compact, one
+        batched host read of their nnz), pairings and launch orders; the
+        per-tile lists and the forward-only quad unions are released."""
         if self._settled:
             return
         self.key_lists()
         if self._csr is not None:
-            self.qunion, self.kunion = self._csr.finish([self.qunion, self.kunion])
+            lists = [self.qunion, self.kunion] + ([self.qquad] if self.dq_quads else [])
+            done = self._csr.finish(lists)
+            self.qunion, self.kunion = done[:2]
+            if self.dq_quads:
+                self.qquad = done[2]
             self._csr = None
+        if not self.dq_quads:  # the forward's only: released once it is queued
+            self.qquad = self.qquad_order = None
         self.qcols = None
         self.klists = None
         self.sel = {key: val for key, val in self.sel.items() if key != "tiles"}
@@ -153,8 +174,12 @@ class _ChunkBSA(torch.autograd.Function):
                 plan.key_lists_side()
             else:
                 plan.key_lists()
-        o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
-                                plan.qorder)
+        if plan.qquad is not None:
+            o_re, lse = ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qquad, sm_scale,
+                                         plan.qquadmap, plan.qquad_order)
+        else:
+            o_re, lse = ops.bsa_fwd(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, plan.qunion, sm_scale, plan.qpair,
+                                    plan.qorder)
         plan.join_side()  # queued after the forward kernel: the key lists still run beside it
         if grads:
             plan.settle()  # release the per-tile lists; compact the unions while the forward runs
@@ -182,9 +207,12 @@ class _ChunkBSA(torch.autograd.Function):
                     lambda: (ops.chunk_scatter_rows(dk_re, plan.lk, tk), ops.chunk_scatter_rows(dv_re, plan.lk, tv)),
                     reads=(dk_re, dv_re), produces=lambda out: out)
 
+        quads = plan.dq_quads
         dq_re, dk_re, dv_re = ops.bsa_bwd(plan.q_re, plan.k_re, plan.v_re, gd["rows"], m2, gd["rowdot"],
-                                          plan.kv_valid, plan.tmasks, plan.qunion, kunion, ctx.sm_scale, plan.qpair,
-                                          plan.kpair, plan.qorder, plan.korder, after_dkdv=scatter_dkdv)
+                                          plan.kv_valid, plan.tmasks, plan.qquad if quads else plan.qunion, kunion,
+                                          ctx.sm_scale, plan.qquadmap if quads else plan.qpair, plan.kpair,
+                                          plan.qquad_order if quads else plan.qorder, plan.korder,
+                                          after_dkdv=scatter_dkdv, q_quads=quads)
         dq = ops.chunk_scatter_rows(dq_re, plan.lq, tq)
         if "dkdv" in side:
             (dk, dv), done = side["dkdv"]

@@ -99,24 +99,69 @@ def test_quad_forward_bitexact_fullsize_c4():
     _quad_vs_pair(plan, inp["D"])
 
 
+SWITCHES = ((False, False), (True, False), (True, True))  # (ops.QUADS, ops.DQ_QUADS)
+
+
 @pytest.mark.parametrize("case", [CASES[0], CASES[-1]], ids=[CASES[0][0], CASES[-1][0]])
 def test_quads_autograd_identical(case, monkeypatch):
-    """flash_attn_bsa_3d_dynamic with ops.QUADS on and off: the same output
-    and q, k, v gradients, bit for bit (the plan's quad unions feed the
-    forward and dQ kernels)."""
+    """flash_attn_bsa_3d_dynamic with the forward on pairs, on quads, and the
+    forward and dQ on quads: the same output and q, k, v gradients, bit for
+    bit."""
     from prism_amd import flash_attn_bsa_3d_dynamic, ops
     c = make(case)
     say("quads autograd", case)
     valid = dev(c["valid"]).bool() if c["pad"] else None
     outs = []
-    for quads in (False, True):
+    for quads, dq_quads in SWITCHES:
         monkeypatch.setattr(ops, "QUADS", quads)
+        monkeypatch.setattr(ops, "DQ_QUADS", dq_quads)
         q, k, v = (dev(c[n]).requires_grad_(True) for n in ("qh", "kh", "vh"))
         o = flash_attn_bsa_3d_dynamic(q, k, v, c["grid"], method="ivpq", sparsity=0.6, cdf_threshold=0.9,
                                       valid_mask=valid)
-        assert (o.grad_fn.plan.qquad is not None) == (quads and o.grad_fn.plan.lay.Nt % 4 == 0)
+        plan = o.grad_fn.plan
+        assert plan.lay.Nt % 4 == 0 and plan.quads == quads and plan.dq_quads == dq_quads
+        assert (plan.qquad is not None) == dq_quads  # kept for the backward only when dQ walks it
         o.backward(torch.randn(o.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(3))
                    .to(o.dtype))
         outs.append([host(t) for t in (o, q.grad, k.grad, v.grad)])
-    for name, a, b in zip(("O", "dQ", "dK", "dV"), *outs):
-        assert bits_equal(a, b), name
+    for other in outs[1:]:
+        for name, a, b in zip(("O", "dQ", "dK", "dV"), outs[0], other):
+            assert bits_equal(a, b), name
+
+
+def test_quads_uniform_and_cross_identical(monkeypatch):
+    """The uniform-shape branch (run_bsa_uniform, padded grid) and the
+    cross-modal BSA (flash_attn_bsa_cross, audio queries over video keys)
+    with the forward on pairs, on quads, and the forward and dQ on quads: the
+    same output and gradients, bit for bit."""
+    from prism_amd import ops
+    from prism_amd.adapter import run_bsa_uniform
+    from prism_amd.uniform_block_attention import flash_attn_bsa_cross
+    from tests.cases import bf16 as to_bf16
+    rng = np.random.default_rng(23)
+    D = 128
+    grid = (7, 16, 16)
+    qh, kh, vh = (to_bf16(rng.standard_normal((1, 2, int(np.prod(grid)), D)).astype(np.float32)) for _ in range(3))
+    aq = to_bf16(rng.standard_normal((1, 2, 460, D)).astype(np.float32))  # 8 query tiles, the last partial
+    calls = {
+        "uniform": (lambda q, k, v: run_bsa_uniform(q, k, v, grid, {"sparsity": 0.6, "cdf_threshold": 0.9}),
+                    (qh, kh, vh)),
+        "cross": (lambda q, k, v: flash_attn_bsa_cross(q, k, v, "1d", "3d", k_grid_size=grid, chunk_size_q=64,
+                                                       chunk_3d_shape_k=(4, 4, 4), sparsity=0.5),
+                  (aq, kh, vh)),
+    }
+    for name, (fn, arrays) in calls.items():
+        outs = []
+        for quads, dq_quads in SWITCHES:
+            say("quads", name, quads, dq_quads)
+            monkeypatch.setattr(ops, "QUADS", quads)
+            monkeypatch.setattr(ops, "DQ_QUADS", dq_quads)
+            q, k, v = (dev(a).requires_grad_(True) for a in arrays)
+            o = fn(q, k, v)
+            assert o.grad_fn.plan.quads == quads and o.grad_fn.plan.dq_quads == dq_quads, name
+            o.backward(torch.randn(o.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(4))
+                       .to(o.dtype))
+            outs.append([host(t) for t in (o, q.grad, k.grad, v.grad)])
+        for other in outs[1:]:
+            for what, a, b in zip(("O", "dQ", "dK", "dV"), outs[0], other):
+                assert bits_equal(a, b), (name, what)
