@@ -77,16 +77,17 @@ def test_quad_forward_bitexact_vs_pair(case):
             assert bool(int(e) & 16) == bool(partial), (qd, t)
 
 
-def test_quad_forward_bitexact_fullsize_c4():
-    """Config 4's lists (as benchmarked): the quad and pair forwards agree bit
-    for bit over all 14,400 pairs."""
+@pytest.mark.parametrize("cfg", ["c2", "c3", "c4"])
+def test_quad_forward_bitexact_fullsize(cfg):
+    """Configs 2-4 at full size (the benchmark's inputs and lists): the quad
+    and pair forwards and dQ agree bit for bit over every quad."""
     import bench
     from prism_amd import ops, plan_dynamic, a2v_token_norms
     from prism_amd.adapter import padded_grid
     from prism_amd.dynamic_block_shape import _gradient_and_shapes
     from tests.test_gpu_fullsize import _sparsity
-    say("quad fullsize c4: inputs")
-    inp = bench.make_inputs("c4")
+    say("quad fullsize", cfg, "inputs")
+    inp = bench.make_inputs(cfg)
     grid = inp["grid"]
     gp, _ = padded_grid(grid)
     with torch.no_grad():
@@ -95,7 +96,7 @@ def test_quad_forward_bitexact_fullsize_c4():
         sp, cdf = _sparsity(inp, ops.ZoneLayout(sid, gp, grid).N_b)
         plan = plan_dynamic(inp["q"], inp["k"], inp["v"], gp, method="ivpq", sparsity=sp, cdf_threshold=cdf,
                             audio_token_norms=norms, input_grid=grid)
-    say("quad fullsize c4: attention")
+    say("quad fullsize", cfg, "attention")
     _quad_vs_pair(plan, inp["D"])
 
 
