@@ -6,7 +6,10 @@
 // (per-query-tile key lists for the forward and dQ passes, per-key-tile query
 // lists for dK/dV): entry = tile << 3 | partial << 2 | in_second << 1 | in_first.
 // It replaces the per-iteration merge of two list cursors, whose dependent
-// index loads sat on the critical path of every key tile.
+// index loads sat on the critical path of every key tile.  prism_quad_union
+// does the same for QUADS of tiles (two pairs of a zone, for the forward and
+// dQ kernels that take four query tiles per workgroup): entry = tile << 5 |
+// partial << 4 | one member bit per row.
 //
 // prism_tile_masks packs the per-token key validity of each 64-token tile into
 // one 64-bit word (bit j = token j valid), read with one scalar load by the
