@@ -166,3 +166,50 @@ def test_quads_uniform_and_cross_identical(monkeypatch):
         for other in outs[1:]:
             for what, a, b in zip(("O", "dQ", "dK", "dV"), outs[0], other):
                 assert bits_equal(a, b), (name, what)
+
+
+def test_quad_debug_mode_checks_lists(monkeypatch):
+    """PRISM_DEBUG=1: prism_bsa_fwd_quad and prism_bsa_bwd_dq_quad check their
+    quad unions and maps on the host before launching.  Valid lists give the
+    same bits as without the checks; corrupted ones (kept inside the operands'
+    bounds) raise ValueError naming the defect."""
+    from prism_amd import ops, plan_dynamic
+    case = CASES[1]
+    c = make(case)
+    say("quad debug", case)
+    D = c["q"].shape[-1]
+    sm = 1.0 / math.sqrt(D)
+    plan = plan_dynamic(dev(c["qh"]), dev(c["kh"]), dev(c["vh"]), c["grid"], method="ivpq", sparsity=0.6,
+                        cdf_threshold=0.9, valid_mask=dev(c["valid"]).bool() if c["pad"] else None)
+    quad = ops.quad_union(plan.qstart, plan.qlen, plan.qcols, plan.lay.Nt, plan.tmasks, pairmap=plan.qpair)
+    order = ops.pair_order(quad[1], 32)
+    o, lse = ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, quad, sm, plan.qpair, order)
+    do = torch.randn(plan.q_re.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(8))
+    do = do.to(torch.bfloat16)
+    m2, delta = ops.lse_to_m2(lse), ops.bwd_preprocess(o, do)
+    dq_args = lambda u, om: (plan.q_re, plan.k_re, plan.v_re, do, m2, delta, plan.tmasks, *u, plan.qpair, om, sm)
+    dq = torch.ops.prism.bsa_bwd_dq_quad(*dq_args(quad, order))
+    monkeypatch.setenv("PRISM_DEBUG", "1")
+    say("quad debug: valid lists")
+    o2, lse2 = ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, quad, sm, plan.qpair, order)
+    dq2 = torch.ops.prism.bsa_bwd_dq_quad(*dq_args(quad, order))
+    assert bits_equal(host(o), host(o2)) and bits_equal(host(lse), host(lse2)) and bits_equal(host(dq), host(dq2))
+    us, ul, uc = quad
+    r = int(torch.nonzero(ul >= 2)[0, 0])
+    s = int(us[r])
+    bad = uc.clone()
+    bad[s] = bad[s] & ~15  # an entry that belongs to no tile of its quad
+    say("quad debug: entry without member bits")
+    with pytest.raises(ValueError, match="belongs to no tile of its quad"):
+        ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, (us, ul, bad), sm, plan.qpair, order)
+    bad = uc.clone()
+    bad[s], bad[s + 1] = uc[s + 1], uc[s]
+    say("quad debug: descending entries in dQ")
+    with pytest.raises(ValueError, match="not above"):
+        torch.ops.prism.bsa_bwd_dq_quad(*dq_args((us, ul, bad), order))
+    bad_order = order.clone()
+    bad_order[1] = bad_order[0]
+    say("quad debug: launch order with a repeated quad")
+    with pytest.raises(ValueError, match="twice"):
+        ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, quad, sm, plan.qpair, bad_order)
+    torch.cuda.synchronize()
