@@ -213,3 +213,45 @@ def test_quad_debug_mode_checks_lists(monkeypatch):
     with pytest.raises(ValueError, match="twice"):
         ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, quad, sm, plan.qpair, bad_order)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[-1]], ids=[CASES[0][0], CASES[-1][0]])
+def test_quad_work_queue_bit_identical(case):
+    """prism_bsa_fwd_quad and prism_bsa_bwd_dq_quad through the C-ABI with
+    work_counter = NULL (one workgroup per quad) and with a counter
+    (persistent workgroups over the per-XCD work queues; the counter starts
+    with garbage, which the call clears, and is reused by the next call):
+    the same bits as the operators."""
+    from prism_amd import ops, plan_dynamic
+    c = make(case)
+    say("quad work queue", case)
+    q = dev(c["qh"])
+    B, H, S, D = q.shape
+    BH, sm = B * H, 1.0 / math.sqrt(D)
+    plan = plan_dynamic(q, dev(c["kh"]), dev(c["vh"]), c["grid"], method="ivpq", sparsity=0.6, cdf_threshold=0.9,
+                        valid_mask=dev(c["valid"]).bool() if c["pad"] else None)
+    Sp = plan.q_re.shape[2]
+    quad = ops.quad_union(plan.qstart, plan.qlen, plan.qcols, plan.lay.Nt, plan.tmasks, pairmap=plan.qpair)
+    order = ops.pair_order(quad[1], 32)
+    o, lse = ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, quad, sm, plan.qpair, order)
+    do = torch.randn(plan.q_re.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(9))
+    do = do.to(plan.q_re.dtype)
+    m2, delta = ops.lse_to_m2(lse), ops.bwd_preprocess(o, do)
+    dq = torch.ops.prism.bsa_bwd_dq_quad(plan.q_re, plan.k_re, plan.v_re, do, m2, delta, plan.tmasks, *quad,
+                                         plan.qpair, order, sm)
+    ptr = lambda t: None if t is None else t.data_ptr()
+    stream = torch.cuda.current_stream().cuda_stream
+    counter = torch.full((8,), 12345, dtype=torch.int32, device="cuda")
+    for ctr in (None, counter, counter):
+        say("quad work queue: counter", ctr is not None)
+        o2, lse2, dq2 = torch.empty_like(o), torch.empty_like(lse), torch.empty_like(dq)
+        ops._lib.call("prism_bsa_fwd_quad", ptr(plan.q_re), ptr(plan.k_re), ptr(plan.v_re), BH, Sp, Sp, D,
+                      ptr(plan.tmasks), *(ptr(t) for t in quad), ptr(plan.qpair), ptr(order), sm, ptr(o2), ptr(lse2),
+                      ptr(ctr), stream)
+        if ctr is not None:
+            counter.fill_(-7)  # garbage again: the dQ call clears it too
+        ops._lib.call("prism_bsa_bwd_dq_quad", ptr(plan.q_re), ptr(plan.k_re), ptr(plan.v_re), ptr(do), ptr(m2),
+                      ptr(delta), BH, Sp, Sp, D, ptr(plan.tmasks), *(ptr(t) for t in quad), ptr(plan.qpair),
+                      ptr(order), sm, ptr(dq2), ptr(ctr), stream)
+        torch.cuda.synchronize()
+        assert bits_equal(host(o), host(o2)) and bits_equal(host(lse), host(lse2)) and bits_equal(host(dq), host(dq2))
