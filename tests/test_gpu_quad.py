@@ -255,3 +255,48 @@ def test_quad_work_queue_bit_identical(case):
                       ptr(order), sm, ptr(dq2), ptr(ctr), stream)
         torch.cuda.synchronize()
         assert bits_equal(host(o), host(o2)) and bits_equal(host(lse), host(lse2)) and bits_equal(host(dq), host(dq2))
+
+
+def test_quad_graph_capture_replays():
+    """The quad forward and dQ over a prebuilt plan, captured in one HIP graph
+    (persistent launches with their counter-zeroing kernels, outputs and
+    counters from the graph's memory pool): three replays, with eager work
+    and synchronisations between them, each give the eager bits."""
+    from prism_amd import ops, plan_dynamic
+    c = make(CASES[-1])
+    say("quad graph capture")
+    D = c["q"].shape[-1]
+    sm = 1.0 / math.sqrt(D)
+    plan = plan_dynamic(dev(c["qh"]), dev(c["kh"]), dev(c["vh"]), c["grid"], method="ivpq", sparsity=0.6,
+                        cdf_threshold=0.9)
+    quad = ops.quad_union(plan.qstart, plan.qlen, plan.qcols, plan.lay.Nt, plan.tmasks, pairmap=plan.qpair)
+    order = ops.pair_order(quad[1], 32)
+    do = torch.randn(plan.q_re.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(10))
+    do = do.to(plan.q_re.dtype)
+
+    def step():
+        o, lse = ops.bsa_fwd_quad(plan.q_re, plan.k_re, plan.v_re, plan.tmasks, quad, sm, plan.qpair, order)
+        m2, delta = ops.lse_to_m2(lse), ops.bwd_preprocess(o, do)
+        dq = torch.ops.prism.bsa_bwd_dq_quad(plan.q_re, plan.k_re, plan.v_re, do, m2, delta, plan.tmasks, *quad,
+                                             plan.qpair, order, sm)
+        return o, lse, dq
+
+    ref = [host(t) for t in step()]
+    warm = torch.cuda.Stream()
+    warm.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm):
+        step()
+    torch.cuda.current_stream().wait_stream(warm)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for rep in range(3):
+        say("quad graph replay", rep)
+        junk = torch.full((1 << 20,), float(rep), device="cuda").cumsum(0)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, t, r in zip(("O", "LSE", "dQ"), outs, ref):
+            assert bits_equal(host(t), r), (rep, name)
+        del junk
