@@ -475,7 +475,9 @@ __device__ __forceinline__ void bsa_fwd_quad(const FwdArgs& a, uint8_t* smem, in
       pend = (e & mybit) != 0;
       if (pend) {
         s_phase(sK, sacc);
+        __builtin_amdgcn_s_setprio(2);  // the row max as in group 0 (-0.3%; no priorities at all: +5%)
         mask_max(e, sacc, m_new, alpha, mb, move);
+        __builtin_amdgcn_s_setprio(0);
         v_reads(sK + RT::BYTES, vfr);
       }
     }
