@@ -84,6 +84,12 @@ def attn_fwd_bsa_varlen(q, k, v, sm_scale, block_indices, block_indices_lens, ch
     qstart, qlen, qcols = _lists_from_dense(block_indices, block_indices_lens)
     Ntq, Ntk = q.shape[2] // 64, k.shape[2] // 64
     tm = ops.tile_masks(ops._u8(kv_valid_mask))
+    if ops.QUADS and Ntq % 4 == 0:
+        # four query tiles per staged K / V tile (two overlap pairs of each
+        # group of 8), the same outputs bit for bit
+        qpair = ops.pair_tiles(qstart, qlen, qcols, Ntq, Ntk)
+        quad = ops.quad_union(qstart, qlen, qcols, Ntq, tm, col_tiles=Ntk, pairmap=qpair)
+        return ops.bsa_fwd_quad(q, k, v, tm, quad, sm_scale, qpair, ops.pair_order(quad[1], 32))
     qunion = ops.pair_union(qstart, qlen, qcols, Ntq, tm, col_tiles=Ntk)
     return ops.bsa_fwd(q, k, v, tm, qunion, sm_scale)
 
