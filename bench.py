@@ -14,6 +14,7 @@ Prints ONE JSON line.  value = kept-block algorithmic FLOP/s of the step
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -144,6 +145,8 @@ def time_region(fn, steps, warmup):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()  # no cyclic garbage collection inside the timed region
     t0 = time.perf_counter()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for a, b in ev:
@@ -152,6 +155,7 @@ def time_region(fn, steps, warmup):
         b.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    gc.enable()
     per = [a.elapsed_time(b) for a, b in ev]
     return sum(per) / steps, statistics.median(per), wall / steps * 1e3
 
@@ -632,6 +636,11 @@ def main():
         step()
     torch.cuda.synchronize()
     log("[bench] timed steps")
+    # no cyclic garbage collection inside the timed region (a collection of
+    # the earlier steps' plans and events stalled the host for ~50 ms, long
+    # enough to leave the GPU idle in a 25 ms forward-only step)
+    gc.collect()
+    gc.disable()
     # timed region: every C-ABI launch is bracketed by HIP events on its stream
     with ops.kernel_timing() as tm:
         st = torch.cuda.Event(enable_timing=True)
@@ -646,6 +655,7 @@ def main():
         en.record()
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    gc.enable()
     ms = st.elapsed_time(en) / args.steps
     import statistics
     ms_median = statistics.median(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
@@ -1019,6 +1029,8 @@ def run_uniform(args, inp):
         step()
     torch.cuda.synchronize()
     log("[bench] timed steps")
+    gc.collect()
+    gc.disable()  # no cyclic garbage collection inside the timed region
     with ops.kernel_timing() as tm:
         st = torch.cuda.Event(enable_timing=True)
         en = torch.cuda.Event(enable_timing=True)
@@ -1029,6 +1041,7 @@ def run_uniform(args, inp):
         en.record()
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    gc.enable()
     ms = st.elapsed_time(en) / args.steps
     kt = ops.summarize(tm)
     with torch.no_grad():
