@@ -102,9 +102,10 @@ class _Plan:
         # staged K / V tile), which the forward and dQ kernels walk instead of
         # the pair unions when ops.QUADS is set (same results, bit for bit)
         self.qquad = self.qquad_order = self.qquadmap = None
-        # dq_quads: dQ walks them too, so the backward keeps them
+        # dq_quads: dQ walks them too (by default on this path), so the
+        # backward keeps them
         self.quads = ops.QUADS and lay.Nt % 4 == 0
-        self.dq_quads = self.quads and ops.DQ_QUADS
+        self.dq_quads = self.quads and ops.DQ_QUADS is not False
         if self.quads:
             self.qquadmap = self.qpair
             self.qquad = ops.quad_union(self.qstart, self.qlen, self.qcols, lay.Nt, self.tmasks,

@@ -627,15 +627,18 @@ OVERLAP_DKDV_SCATTER = False
 
 # The forward over quad unions (bsa_fwd_quad: four query tiles per staged K /
 # V tile, bit-identical to bsa_fwd) when the query tiles per head are a
-# multiple of 4; PRISM_QUADS=0 keeps the pair kernel.  With DQ_QUADS
-# (PRISM_DQ_QUADS=1) dQ walks the quad unions too (bsa_bwd_dq_quad,
-# bit-identical to bsa_bwd_dq), and the plan keeps them for the backward.
-# The quads stage 42% fewer tile bytes but leave more wave slots idle (24%
-# against 8% for pairs at config 4): forward 52.5 -> 49.7 ms there, dQ
-# 59.7 -> 59.4 ms; on the uniform path (35% idle) forward 56.1-57.0 -> 52.1
-# ms but dQ 60.6-60.7 -> 61.5 ms, so dQ stays on pairs by default.
+# multiple of 4; PRISM_QUADS=0 keeps the pair kernel.  dQ over the same quad
+# unions (bsa_bwd_dq_quad, bit-identical to bsa_bwd_dq; the plan then keeps
+# them for the backward): DQ_QUADS None (the default) takes it on the
+# dynamic-shape path and not on the uniform and cross paths; True / False
+# (PRISM_DQ_QUADS=1 / 0) force it either way.  The quads stage 42% fewer
+# tile bytes but leave more wave slots idle (24% against 8% for pairs at
+# config 4): forward 52.5 -> 49.7 ms there, dQ 59.6 -> 59.1 ms; on the
+# uniform path (35% idle) forward 56.1-57.0 -> 52.1 ms but dQ 60.6-60.7 ->
+# 61.5 ms.
 QUADS = os.environ.get("PRISM_QUADS", "1") not in ("", "0")
-DQ_QUADS = os.environ.get("PRISM_DQ_QUADS", "0") not in ("", "0")
+_dq_env = os.environ.get("PRISM_DQ_QUADS", "")
+DQ_QUADS: Optional[bool] = None if _dq_env == "" else _dq_env != "0"
 
 
 def side_launch(device: torch.device, fn, reads=(), produces=None):

@@ -88,9 +88,11 @@ class _ChunkPlan:
         # kernels walk instead of the pair unions when ops.QUADS is set (same
         # results, bit for bit)
         self.qquad = self.qquad_order = self.qquadmap = None
-        # dq_quads: dQ walks them too, so the backward keeps them
+        # dq_quads: dQ walks them too (only when ops.DQ_QUADS forces it on
+        # these paths, whose quads leave more slots idle), so the backward
+        # keeps them
         self.quads = ops.QUADS and lq.Nt % 4 == 0
-        self.dq_quads = self.quads and ops.DQ_QUADS
+        self.dq_quads = self.quads and ops.DQ_QUADS is True
         if self.quads:
             self.qquadmap = self.qpair
             self.qquad = ops.quad_union(self.qstart, self.qlen, self.qcols, lq.Nt, self.tmasks, col_tiles=lk.Nt,

@@ -100,14 +100,16 @@ def test_quad_forward_bitexact_fullsize(cfg):
     _quad_vs_pair(plan, inp["D"])
 
 
-SWITCHES = ((False, False), (True, False), (True, True))  # (ops.QUADS, ops.DQ_QUADS)
+# (ops.QUADS, ops.DQ_QUADS); None: the path's default (dQ on quads on the
+# dynamic-shape path, on pairs on the uniform and cross paths)
+SWITCHES = ((False, False), (True, False), (True, True), (True, None))
 
 
 @pytest.mark.parametrize("case", [CASES[0], CASES[-1]], ids=[CASES[0][0], CASES[-1][0]])
 def test_quads_autograd_identical(case, monkeypatch):
-    """flash_attn_bsa_3d_dynamic with the forward on pairs, on quads, and the
-    forward and dQ on quads: the same output and q, k, v gradients, bit for
-    bit."""
+    """flash_attn_bsa_3d_dynamic with the forward on pairs, on quads, the
+    forward and dQ on quads, and the defaults: the same output and q, k, v
+    gradients, bit for bit."""
     from prism_amd import flash_attn_bsa_3d_dynamic, ops
     c = make(case)
     say("quads autograd", case)
@@ -120,8 +122,9 @@ def test_quads_autograd_identical(case, monkeypatch):
         o = flash_attn_bsa_3d_dynamic(q, k, v, c["grid"], method="ivpq", sparsity=0.6, cdf_threshold=0.9,
                                       valid_mask=valid)
         plan = o.grad_fn.plan
-        assert plan.lay.Nt % 4 == 0 and plan.quads == quads and plan.dq_quads == dq_quads
-        assert (plan.qquad is not None) == dq_quads  # kept for the backward only when dQ walks it
+        want_dq = quads and dq_quads is not False
+        assert plan.lay.Nt % 4 == 0 and plan.quads == quads and plan.dq_quads == want_dq
+        assert (plan.qquad is not None) == want_dq  # kept for the backward only when dQ walks it
         o.backward(torch.randn(o.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(3))
                    .to(o.dtype))
         outs.append([host(t) for t in (o, q.grad, k.grad, v.grad)])
@@ -159,7 +162,7 @@ def test_quads_uniform_and_cross_identical(monkeypatch):
             monkeypatch.setattr(ops, "DQ_QUADS", dq_quads)
             q, k, v = (dev(a).requires_grad_(True) for a in arrays)
             o = fn(q, k, v)
-            assert o.grad_fn.plan.quads == quads and o.grad_fn.plan.dq_quads == dq_quads, name
+            assert o.grad_fn.plan.quads == quads and o.grad_fn.plan.dq_quads == (quads and dq_quads is True), name
             o.backward(torch.randn(o.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(4))
                        .to(o.dtype))
             outs.append([host(t) for t in (o, q.grad, k.grad, v.grad)])
